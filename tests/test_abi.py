@@ -1,0 +1,126 @@
+"""The C ABI without a GPU: exports, struct layout against the header, host-side checks."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+import torch  # noqa: F401  (load order: torch before the HIP library)
+
+from conftest import ROOT
+from mamba3_amd import _hip
+
+HEADER = os.path.join(ROOT, "include", "mamba3_hip.h")
+
+
+def _declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    return re.findall(r"^(?:int|const char\*)\s+(m3_\w+)\s*\(", text, flags=re.M)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_hip.LIB_PATH):
+        pytest.skip("libmamba3_hip.so is not built (run __graft_entry__.build())")
+    return _hip.load()
+
+
+def test_header_declares_the_expected_entry_points():
+    assert sorted(_declared_functions()) == sorted(_hip.ENTRY_POINTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.m3_abi_version() == _hip.ABI_VERSION
+    assert lib.m3_last_error() == b""
+
+
+def _c_layout() -> dict[str, tuple[int, dict[str, int]]]:
+    """sizeof / offsetof of every struct field, from the header compiled with gcc."""
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    structs = {"m3_tensor": _hip.Tensor, "m3_scan_args": _hip.ScanArgs,
+               "m3_step_args": _hip.StepArgs, "m3_chunk_state_args": _hip.ChunkStateArgs}
+    lines = ['#include "mamba3_hip.h"', "#include <stdio.h>", "#include <stddef.h>",
+             "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["return 0;", "}"]
+    tmp = os.path.join(os.environ.get("TMPDIR", "/tmp"), f"m3_layout_{os.getpid()}")
+    with open(tmp + ".c", "w") as f:
+        f.write("\n".join(lines))
+    inc = ["-I/opt/rocm/include", f"-I{os.path.join(ROOT, 'include')}"]
+    subprocess.run(["gcc", "-D__HIP_PLATFORM_AMD__", *inc, tmp + ".c", "-o", tmp], check=True)
+    out = subprocess.run([tmp], check=True, capture_output=True, text=True).stdout
+    os.remove(tmp)
+    os.remove(tmp + ".c")
+    layout: dict[str, tuple[int, dict[str, int]]] = {}
+    for line in out.splitlines():
+        cname, field, value = line.split()
+        size, fields = layout.get(cname, (0, {}))
+        if field == "sizeof":
+            size = int(value)
+        else:
+            fields[field] = int(value)
+        layout[cname] = (size, fields)
+    return layout
+
+
+def test_ctypes_structs_match_the_header_layout():
+    layout = _c_layout()
+    for cname, py in (("m3_tensor", _hip.Tensor), ("m3_scan_args", _hip.ScanArgs),
+                      ("m3_step_args", _hip.StepArgs),
+                      ("m3_chunk_state_args", _hip.ChunkStateArgs)):
+        size, fields = layout[cname]
+        assert ctypes.sizeof(py) == size, cname
+        for field, _ in py._fields_:
+            assert getattr(py, field).offset == fields[field], (cname, field)
+
+
+def test_null_arguments_are_rejected_without_touching_the_device(lib):
+    for name in ("m3_scan_fwd", "m3_step", "m3_chunk_state"):
+        rc = getattr(lib, name)(None, None)
+        assert rc == 1, name
+        assert b"NULL" in lib.m3_last_error()
+
+
+def test_scan_validation_on_the_host(lib):
+    args = _hip.ScanArgs(batch=1, length=4, heads=2, groups=1, rank=1, d_state=12,
+                         head_dim=8, num_angles=3)
+    rc = lib.m3_scan_fwd(ctypes.byref(args), None)
+    assert rc == 2 and b"power of 2" in lib.m3_last_error()
+    args.d_state = 16
+    rc = lib.m3_scan_fwd(ctypes.byref(args), None)
+    assert rc == 1 and b"q: required tensor is NULL" in lib.m3_last_error()
+    args.heads, args.groups = 3, 2
+    assert lib.m3_scan_fwd(ctypes.byref(args), None) == 1
+    assert b"heads % groups" in lib.m3_last_error()
+
+
+def test_step_validation_on_the_host(lib):
+    args = _hip.StepArgs(batch=1, heads=2, groups=1, rank=3, d_state=16, head_dim=8,
+                         num_angles=4, phase_mode=_hip.PHASE_ANGLES, mimo_rotation=1)
+    # rank 3 is rejected only at launch; the angle count check comes first for MIMO
+    args.num_angles = 3
+    assert lib.m3_step(ctypes.byref(args), None) == 2
+    assert b"num_angles" in lib.m3_last_error()
+    args.num_angles = 4
+    assert lib.m3_step(ctypes.byref(args), None) == 1
+    assert b"required tensor is NULL" in lib.m3_last_error()
+
+
+def test_tensor_descriptor_records_pointer_dtype_and_strides():
+    t = torch.zeros(2, 3, 4, dtype=torch.bfloat16)[:, 1:, ::2]
+    d = _hip.tensor(t)
+    assert d.ptr == t.data_ptr()
+    assert d.dtype == _hip.BF16
+    assert list(d.stride)[:3] == list(t.stride())
+    assert list(d.stride)[3:] == [0, 0]
+    assert _hip.tensor(None).ptr is None
