@@ -1,0 +1,283 @@
+"""Benchmark of the Mamba-3 mixer hot path on one MI355X.
+
+Headline workload: the SISO prefill scan of
+``Mamba3(d_model=1024, d_state=128, depth=1, mimo_rank=1)`` on ``x [8, 8192, 1024]`` under
+bf16 autocast, seed 1. A step is one pass of the fused scan kernel (``m3_scan_fwd``:
+B/C RMSNorm, dt / A, bounded phase, bias, rotation, chunked SSD, D skip, SiLU gate) over the
+whole batch, with its input, the ``in_proj`` output, already resident in HBM. ``value`` is
+prefill tokens/s of that kernel. Also reported, in the same JSON line:
+
+* ``roofline``: the scan kernel against the HBM roof (its binding roof: arithmetic intensity
+  ~201 flop/B at the reference chunk is below the MI355X ridge of ~315 flop/B);
+  ``roofline_mfma``: the same kernel against dense bf16 MFMA;
+* ``forward``: tokens/s of the whole mixer forward (norm, in_proj, scan, out_proj, residual);
+* ``decode``: BASELINE.json configs[3], ``Mamba3(2048, 128, 24, 1)`` with bf16 weights and an
+  FP32 state, 2048-token prefill, then 512 hipGraph replays of ``step`` at B = 256, plus the
+  step kernel alone against the HBM roof;
+* ``cpu_baseline``: the CPU oracle (a restatement of the reference's portable path) on a
+  bounded sample of the same scan, on this host's cores.
+
+Usage: ``python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-decode] [--no-cpu]``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
+METRIC = "prefill tok/s (B=8,L=8K) + decode tok/s (B=256) on 1 GPU; % MFMA/HBM roofline"
+
+
+def prefill_bytes(batch, length, d_model, proj):
+    """Algorithmic bytes of one scan launch: the in_proj output read once, y written once."""
+    return batch * length * (2 * proj + 2 * 2 * d_model)
+
+
+def prefill_flops(batch, length, heads, n, p, rank, chunk):
+    """Chunked-SSD FLOPs (causal lower triangle incl. diagonal) at chunk size ``chunk``."""
+    return batch * length * heads * ((chunk + 1) * rank * rank * (n + p) + 4 * rank * n * p)
+
+
+def decode_bytes_per_layer_row(heads, p, n, s, rank):
+    """Bytes one decode step moves per (layer, batch row) in the step kernel."""
+    return (2 * heads * p * n * 4 + heads * (4 * rank * n + 8 * p + 8 * s + 12)
+            + 4 * rank * n + 2 * s)
+
+
+def _events_time(fn, iters):
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1000.0
+
+
+def bench_prefill(steps, warmup, log):
+    from mamba3_amd import Mamba3, ops
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(1)
+    model = Mamba3(1024, d_state=128, depth=1, mimo_rank=1).eval()
+    x = torch.randn(8, 8192, 1024)
+    model = model.to(dev)
+    x = x.to(dev)
+    mixer = model.layers[0].mixer
+    batch, length = x.shape[:2]
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        proj = mixer.in_proj(model.layers[0].norm(x))
+        torch.cuda.synchronize()
+        chunk = mixer.inference_chunk_size
+
+        def scan():
+            ops.scan_projection(proj, mixer, chunk_size=chunk)
+
+        for _ in range(warmup):
+            scan()
+        assert ops._HIP_LAST_SCAN_DISPATCH
+        t_scan = _events_time(scan, steps)
+
+        def forward():
+            model(x)
+
+        for _ in range(max(1, warmup // 2)):
+            forward()
+        fwd_iters = max(3, steps // 4)
+        t_fwd = _events_time(forward, fwd_iters)
+    per_launch = t_scan / steps
+    tokens = batch * length
+    proj_size = mixer.in_proj.weight.shape[0]
+    nbytes = prefill_bytes(batch, length, 1024, proj_size)
+    flops_ref = prefill_flops(batch, length, mixer.nheads, 128, mixer.headdim, 1, 256)
+    flops_own = prefill_flops(batch, length, mixer.nheads, 128, mixer.headdim, 1, 64)
+    gbs = nbytes / per_launch / 1e9
+    tflops = flops_ref / per_launch / 1e12
+    log(f"prefill scan: {per_launch * 1e3:.3f} ms/launch, {tokens / per_launch:.4e} tok/s, "
+        f"{gbs:.0f} GB/s, {tflops:.1f} TFLOP/s (C_ref=256)")
+    return dict(
+        per_launch=per_launch, tokens=tokens, t_total=t_scan,
+        roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                      frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
+                      kernel="m3::scan_kernel<__bf16, 1>", bytes_per_launch=nbytes),
+        roofline_mfma=dict(bound="mfma", achieved=round(tflops, 1), peak=MFMA_BF16_PEAK_TFLOPS,
+                           unit="TFLOP/s", frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                           flops_per_launch_at_c256=flops_ref,
+                           flops_per_launch_at_kernel_chunk64=flops_own),
+        forward=dict(tok_s=round(tokens / (t_fwd / fwd_iters), 1),
+                     ms_per_forward=round(t_fwd / fwd_iters * 1e3, 3)),
+        proj=proj_size)
+
+
+def bench_decode(batch, steps, log, rank=1, prefix=2048):
+    from mamba3_amd import Mamba3, ops
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(3)
+    model = Mamba3(2048, d_state=128, depth=24, mimo_rank=rank).eval()
+    model = model.to(device=dev, dtype=torch.bfloat16)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    mixer = model.layers[0].mixer
+    with torch.inference_mode():
+        x = torch.randn(batch, prefix, 2048, device=dev, dtype=torch.bfloat16, generator=gen)
+        _, cache = model.prefill(x)
+        del x
+        decoder = model.cuda_graph(batch_size=batch)
+        for layer_cache, src in zip(decoder.cache, cache):
+            for dst, s in zip(layer_cache, src):
+                dst.copy_(s)
+        del cache
+        nxt = torch.randn(steps, batch, 1, 2048, device=dev, dtype=torch.bfloat16,
+                          generator=gen)
+        decoder(nxt[0])
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            decoder.input.copy_(nxt[i])
+            decoder.replay()
+        end.record()
+        torch.cuda.synchronize()
+        t = start.elapsed_time(end) / 1000.0
+        # the step kernel alone, layer-0 shapes, in place on the decoder's cache
+        proj = mixer.in_proj(model.layers[0].norm(nxt[0]))
+        layer_cache = decoder.cache[0]
+
+        def step_kernel():
+            ops.step_projection(proj, mixer, layer_cache, inplace=True)
+
+        for _ in range(3):
+            step_kernel()
+        iters = 20
+        t_k = _events_time(step_kernel, iters) / iters
+    nb = decode_bytes_per_layer_row(mixer.nheads, mixer.headdim, 128, mixer.num_angles,
+                                    rank) * batch
+    gbs = nb / t_k / 1e9
+    tok_s = steps * batch / t
+    log(f"decode B={batch} R={rank}: {t / steps * 1e3:.3f} ms/step, {tok_s:.1f} tok/s; "
+        f"step kernel {t_k * 1e6:.1f} us, {gbs:.0f} GB/s")
+    return dict(batch=batch, rank=rank, steps=steps, tok_s=round(tok_s, 1),
+                ms_per_step=round(t / steps * 1e3, 4),
+                step_kernel=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS,
+                                 unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
+                                 us_per_launch=round(t_k * 1e6, 2), bytes_per_launch=nb,
+                                 kernel=f"m3::step_kernel<__bf16, {rank}>"))
+
+
+def bench_cpu(log, batch=8, length=8192):
+    """The CPU oracle (portable-path restatement) on the prefill scan, ``x[batch, length]``."""
+    from oracle import portable as op
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    torch.manual_seed(1)
+    params = op.init_params(1024, d_state=128, depth=1, mimo_rank=1)
+    dims = op.Dims(1024, 128, 1)
+    x = torch.randn(batch, length, 1024)
+    pre = "layers.0.mixer."
+    with torch.inference_mode():
+        proj = torch.nn.functional.linear(op.rms_norm(x, params["layers.0.norm.weight"]),
+                                          params[pre + "in_proj.weight"])
+
+        def hot_path():
+            sizes = dims.split_sizes
+            z, xv, b, c, ddt, da, trap, ang = torch.split(proj, sizes, dim=-1)
+            hh, pp, nn_ = dims.nheads, dims.headdim, dims.d_state
+            z = z.reshape(batch, length, hh, pp)
+            xv = xv.reshape(batch, length, hh, pp)
+            k = op.rms_norm(b.reshape(batch, length, 1, 1, nn_), params[pre + "B_norm.weight"])
+            q = op.rms_norm(c.reshape(batch, length, 1, 1, nn_), params[pre + "C_norm.weight"])
+            dt = torch.nn.functional.softplus(ddt + params[pre + "dt_bias"])
+            adt = (-op.heavy_tail(da)).clamp(max=-op.A_FLOOR) * dt
+            phase = op.phase_scan(ang, dt)
+            return op.ssd_scan(q.permute(0, 1, 3, 2, 4), k.permute(0, 1, 3, 2, 4), xv, z, adt,
+                               dt, trap, params[pre + "D"], chunk_size=256, phase=phase,
+                               q_bias=params[pre + "C_bias"], k_bias=params[pre + "B_bias"])
+
+        hot_path()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            hot_path()
+            times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    tok_s = batch * length / t
+    log(f"cpu oracle: {t:.3f} s for {batch}x{length} tokens on {cores} threads -> "
+        f"{tok_s:.1f} tok/s")
+    return dict(value=round(tok_s, 1), unit="tok/s", cores=cores, kind="port",
+                sample=(f"the scan hot path (B/C RMSNorm, dt/A, phase, chunked SSD at chunk 256) "
+                        f"of config 2's mixer on x[{batch}, {length}, 1024] in FP32, median of 3 after "
+                        f"1 warmup"))
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--decode-batch", type=int, default=256)
+    ap.add_argument("--decode-steps", type=int, default=512)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-batch", type=int, default=8)
+    ap.add_argument("--cpu-tokens", type=int, default=8192)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: the Mamba-3 hot path of this build runs on a single "
+              "MI355X (batch and heads shard without communication; see DESIGN.md).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    def log(msg):
+        print(msg, file=sys.stderr, flush=True)
+
+    pre = bench_prefill(args.steps, args.warmup, log)
+    decode = None
+    if not args.no_decode:
+        decode = bench_decode(args.decode_batch, args.decode_steps, log)
+    cpu = None if args.no_cpu else bench_cpu(log, args.cpu_batch, args.cpu_tokens)
+    value = pre["tokens"] / pre["per_launch"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["per_launch"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs, random-init weights)",
+        "config": {"workload": "config 2: SISO prefill scan (m3_scan_fwd) of "
+                               "Mamba3(1024, 128, depth=1, mimo_rank=1), x[8, 8192, 1024], "
+                               "bf16 autocast, in_proj output resident in HBM",
+                   "global_batch": 8, "seq_len": 8192, "parallelism": "none (1 GPU)"},
+        "roofline": pre["roofline"],
+        "roofline_mfma": pre["roofline_mfma"],
+        "forward": pre["forward"],
+        "decode": decode,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

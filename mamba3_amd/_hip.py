@@ -130,6 +130,22 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise TypeError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16")
 
 
+def scan_workspace(args: ScanArgs, device: torch.device) -> torch.Tensor | None:
+    """Allocate (through torch's caching allocator) the workspace ``m3_scan_fwd`` needs and
+    record it in ``args``; the caller keeps the returned tensor alive across the call."""
+    lib = load()
+    nbytes = ctypes.c_size_t(0)
+    rc = lib.m3_scan_workspace_size(ctypes.byref(args), ctypes.byref(nbytes))
+    if rc != 0:
+        raise HipError("m3_scan_workspace_size", rc, lib.m3_last_error().decode(errors="replace"))
+    if nbytes.value == 0:
+        return None
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=device)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = nbytes.value
+    return ws
+
+
 def call(name: str, args: ctypes.Structure, device: torch.device) -> None:
     """Invoke an entry point on ``device``'s current torch stream; raise on failure."""
     lib = load()

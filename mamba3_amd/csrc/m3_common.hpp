@@ -44,6 +44,11 @@ __device__ __forceinline__ float ldx(const void* p, int dtype, int64_t i) {
   return static_cast<float>(static_cast<const _Float16*>(p)[i]);
 }
 
+// A runtime-dtype pointer advanced by `i` elements.
+__device__ __forceinline__ const void* offx(const void* p, int dtype, int64_t i) {
+  return static_cast<const char*>(p) + i * (dtype == M3_F32 ? 4 : 2);
+}
+
 // ---------------------------------------------------------------- scalar math
 
 // torch.nn.functional.softplus with beta = 1, threshold = 20.

@@ -1,107 +1,120 @@
 // Chunked Mamba-3 SSD for CDNA4 (gfx950).
 //
-// One persistent workgroup (4 waves) per (batch, head) walks the sequence in sub-chunks of
-// ROWS flattened (token, rank) rows. The FP32 state lives in MFMA accumulator registers for the
-// whole sequence, stored transposed (S^T [N, P]) as 16x16 tiles spread over the four waves, so
-// the per-chunk state update of the reference (_triton.py:294-413, launched once per chunk by
-// ops.py:444-504) is fused into the same kernel and the state never round-trips through HBM.
+// Two launches per call:
+//   prep_kernel  head-independent per-token work, once per token instead of once per head:
+//                the RMSNorm factors of the raw B / C rows (model.py:190-191) and
+//                pi * tanh(angle) of the phase increments (model.py:225-228), into a workspace.
+//   scan_kernel  one persistent workgroup (8 waves) per (batch, head) walks the sequence in
+//                sub-chunks of ROWS flattened (token, rank) rows. The FP32 state lives in MFMA
+//                accumulator registers for the whole sequence (stored transposed, S^T [N, P],
+//                as 16x16 tiles spread over the waves), so the per-chunk state update that the
+//                reference launches once per chunk (_triton.py:294-413 from ops.py:444-504) is
+//                fused and the state never round-trips through HBM.
 //
-// Per sub-chunk:
-//   prologue  per-token dt / adt / trap from the raw projection or given (model.py:195-198),
-//             exp-trapezoid scale and diagonal (ops.py:659-671), within-chunk cumsum of adt,
-//             bounded phase (model.py:215-256), RMSNorm of raw B/C (model.py:190-191), head
-//             bias and rotation in the activation dtype (ops.py:35-84, 700-714), k * scale and
-//             k * scale * end_decay (ops.py:743, 806-807), rank values v * mimo_x, z * mimo_z;
-//             staged in LDS as MFMA operands.
-//   scores    Sc^T = K_s Q^T                    (MFMA, FP32 accumulate)       ops.py:763-765
-//   weights   W = rnd(Sc * decay)  masked by token, diagonal gamma / scale     ops.py:770-787
-//   intra     W V   (W stays in registers: the K axis is permuted consistently in both operands)
-//   inter     Q rnd(S)^T * exp(cum)                                          ops.py:753-759
-//   epilogue  (inter + intra + D v) silu(z), MIMO rank sum                   ops.py:792-802
-//   carry     S^T = exp(cum_last) S^T + Ke^T V                               ops.py:806-816
+// Per sub-chunk of scan_kernel (the global loads of sub-chunk c+1 are issued into registers
+// before the MFMA work of sub-chunk c, so their latency hides behind it):
+//   scalars  dt, adt, trap from the raw projection or given (model.py:195-198), the
+//            exp-trapezoid gamma and scale (ops.py:659-671), within-chunk cumsum of adt.
+//   phase    bounded phase (model.py:215-256): 64-token blocks of fmod-reduced increments with
+//            an fmod-reduced carry, 4 tokens per lane plus a cross-lane scan; cos / sin.
+//   q / k    RMSNorm, head bias, rotation (ops.py:35-84, 700-714) -> Q, K (row-major) and K^T.
+//   v / z    rank values v * mimo_x, z * mimo_z, and v * scale * end_decay -> V^T, Vs^T, Z^T.
+//   scores   Sc^T = K Q^T                                  (MFMA, FP32 accumulate) ops.py:763
+//   weights  W = rnd(Sc * d), d[t,s] = scale_s exp(cum_t - cum_s) for s < t, gamma_t at s = t:
+//            the reference's K * scale and diagonal gamma / scale fold (ops.py:743, 770-787).
+//   intra    W V   (W stays in registers: the K axis is permuted alike in both operands)
+//   inter    Q rnd(S)^T * exp(cum)                                               ops.py:753
+//   epilogue (inter + intra + D v) silu(z), MIMO rank sum                    ops.py:792-802
+//   carry    S^T = exp(cum_last) S^T + K^T Vs                                ops.py:806-816
+//
+// Products and sums are evaluated in FP32 and rounded to the activation dtype once, where the
+// data become MFMA operands; the reference rounds some intermediates (bias add, rotation,
+// k * scale) separately in the activation dtype.
 //
 // Replaces ops._fused_chunk_scan (ops.py:253-367) / its driver (ops.py:370-505) and the Triton
 // kernels _chunk_main_kernel (_triton.py:74-291) and _chunk_state_kernel (_triton.py:294-413);
 // the same kernel serves the portable entry ops.mamba3_scan (ops.py:544-822).
 #include "m3_common.hpp"
 #include "m3_host.hpp"
+#include "m3_math.h"
 
 namespace m3 {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
-constexpr int kMaxStateTiles = 16;  // 16x16 state tiles per wave (N_pad * P_pad <= 16384)
+constexpr int kThreads = 512;
+constexpr int kWaves = 8;
+constexpr int kTiles = 4;  // 16x16 state tiles per wave (N_pad * P_pad <= 128 * 64)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // MFMA policy per activation type: 16-bit types use 16x16x32 (K = 32, 8 elements per lane),
 // FP32 uses 16x16x4 (K = 4, one element per lane). ROWS is the sub-chunk height.
 template <typename T> struct Mma;
 template <> struct Mma<__bf16> {
-  static constexpr int KS = 32, ROWS = 64, PAD = 8;
+  static constexpr int ROWS = 64, PAD = 8;
   typedef bf16x8 v8;
   typedef bf16x4 v4;
+  typedef bf16x2 v2;
   static __device__ __forceinline__ f4 mma(v8 a, v8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
 };
 template <> struct Mma<_Float16> {
-  static constexpr int KS = 32, ROWS = 64, PAD = 8;
+  static constexpr int ROWS = 64, PAD = 8;
   typedef f16x8 v8;
   typedef f16x4 v4;
+  typedef f16x2 v2;
   static __device__ __forceinline__ f4 mma(v8 a, v8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
 template <> struct Mma<float> {
-  static constexpr int KS = 4, ROWS = 32, PAD = 4;
+  static constexpr int ROWS = 32, PAD = 4;
+  typedef f4 v4;
+  typedef f32x2 v2;
   static __device__ __forceinline__ f4 mma(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
 };
 
-// Geometry shared by host and device.
+// Compile-time LDS layout. Operand tiles are padded to N = 128 and P = 64 (the largest shapes
+// the kernel takes; every Mamba3 configuration has P <= 64), so every offset and loop bound is a
+// constant; smaller shapes run on zero padding.
+constexpr int kNPad = 128, kPPad = 64, kSMax = 32, kTokMax = 64, kRMax = 4;
+constexpr int kNT = kNPad / 16, kPT = kPPad / 16;  // 16-row tiles of N and P
+
+template <typename T> struct Layout {
+  static constexpr int ROWS = Mma<T>::ROWS, PAD = Mma<T>::PAD, ES = sizeof(T);
+  static constexpr int LQ = kNPad + PAD;   // row stride (elements) of Qs, Ks, Sb
+  static constexpr int LR = ROWS + PAD;    // row stride (elements) of KT, VT, VsT, ZT
+  static constexpr int al(int x) { return (x + 15) / 16 * 16; }
+  static constexpr int QS = 0;
+  static constexpr int KS = al(QS + ROWS * LQ * ES);
+  static constexpr int KT = al(KS + ROWS * LQ * ES);
+  static constexpr int VT = al(KT + kNPad * LR * ES);
+  static constexpr int VS = al(VT + kPPad * LR * ES);
+  static constexpr int ZT = al(VS + kPPad * LR * ES);
+  static constexpr int SB = al(ZT + kPPad * LR * ES);
+  static constexpr int FB = al(SB + kPPad * LQ * ES);
+  // float scratch, offsets in floats from FB
+  static constexpr int CUM = 0, ECUM = 64, SCL = 128, GAM = 192, VSF = 256, DTV = 320;
+  static constexpr int CS = 384, SN = CS + kTokMax * kSMax, PBASE = SN + kTokMax * kSMax;
+  static constexpr int POFF = PBASE + kSMax, MX = POFF + kSMax, MZ = MX + kRMax * kPPad;
+  static constexpr int MO = MZ + kRMax * kPPad, ECL = MO + kRMax * kPPad;
+  static constexpr int BYTES = FB + 4 * (ECL + 4);
+};
+
+// Per-launch values shared by host and device.
 struct ScanGeom {
-  int n_pad, p_pad;      // N rounded up to 32, P rounded up to 16
-  int lq;                // row stride (elements) of Qs, Ks, Sb
-  int lr;                // row stride (elements) of KeT, VT, ZT
-  int tok;               // tokens per sub-chunk (ROWS / R)
-  int nt, pt;            // 16-row tiles of N_pad and P_pad
-  int xcd_map;           // 1: map blocks so an XCD holds consecutive (b, h)
-  // LDS byte offsets
-  int o_qs, o_ks, o_ket, o_vt, o_zt, o_sb, o_f;
-  int bytes;
+  int xcd_map;           // 1: map blocks so each XCD holds consecutive (b, h)
+  int vec_qk, vec_vz;    // 1: q/k rows and v/z rows may be loaded with 16 / 8-byte vectors
+  int prep_w, prep_q, prep_k, prep_a;  // workspace floats per token and field offsets (-1: none)
 };
-
-// Float scratch in LDS, offsets in floats from o_f.
-struct FOff {
-  int cum, ecum, diag, scale, eend, cs, sn, pbase, poff, mx, mz, mo, ecl;
-};
-
-__device__ __forceinline__ FOff f_offsets(int tok, int S, int R, int P) {
-  FOff o;
-  o.cum = 0;
-  o.ecum = o.cum + 64;
-  o.diag = o.ecum + 64;
-  o.scale = o.diag + 64;
-  o.eend = o.scale + 64;
-  o.cs = o.eend + 64;
-  o.sn = o.cs + tok * S;
-  o.pbase = o.sn + tok * S;
-  o.poff = o.pbase + S;
-  o.mx = o.poff + S;
-  o.mz = o.mx + R * P;
-  o.mo = o.mz + R * P;
-  o.ecl = o.mo + R * P;
-  return o;
-}
-
-static inline int f_floats(int tok, int S, int R, int P) {
-  return 5 * 64 + 2 * tok * S + 2 * S + 3 * R * P + 4;
-}
 
 __device__ __forceinline__ f4 zero4() {
   f4 z;
@@ -127,17 +140,157 @@ __device__ __forceinline__ T* lds_t(char* base, int off) {
   return reinterpret_cast<T*>(base + off);
 }
 
+// ------------------------------------------------------------------ raw register tiles
+
+// Activation elements held as raw bits until they are used: W8 words hold 8 elements,
+// W4 words hold 4 (two 16-bit elements per word, or one FP32 element per word).
+template <typename T> struct Words {
+  static constexpr int W8 = sizeof(T) == 4 ? 8 : 4;
+  static constexpr int W4 = sizeof(T) == 4 ? 4 : 2;
+};
+
+__device__ __forceinline__ float bits_to_f(uint32_t bits16, __bf16*) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ float bits_to_f(uint32_t bits16, _Float16*) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+template <typename T, int NW>
+__device__ __forceinline__ float raw_get(const uint32_t (&w)[NW], int i) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(w[i]);
+  } else {
+    const uint32_t x = w[i >> 1];
+    return bits_to_f((i & 1) ? (x >> 16) : (x & 0xffffu), static_cast<T*>(nullptr));
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t elem_bits(const T* p) {
+  if constexpr (sizeof(T) == 4) {
+    return __float_as_uint(*p);
+  } else {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, *p));
+  }
+}
+
+// Load up to E elements (n valid, the rest zero) into raw words; one vector load when `vec`
+// and all E are valid (16 bytes, or 8 bytes for four 16-bit elements).
+template <typename T, int E, int NW>
+__device__ __forceinline__ void load_words(uint32_t (&w)[NW], const T* p, int n, bool vec) {
+  if (vec && n >= E) {
+    if constexpr (NW == 2) {
+      const uint2 q = *reinterpret_cast<const uint2*>(p);
+      w[0] = q.x; w[1] = q.y;
+    } else {
+#pragma unroll
+      for (int j = 0; j < NW; j += 4) {
+        const uint4 q = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(p) + j);
+        w[j] = q.x; w[j + 1] = q.y; w[j + 2] = q.z; w[j + 3] = q.w;
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < NW; ++j) w[j] = 0u;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    if (i < n) {
+      const uint32_t e = elem_bits(p + i);
+      if constexpr (sizeof(T) == 4) {
+        w[i] = e;
+      } else {
+        w[i >> 1] |= e << (16 * (i & 1));
+      }
+    }
+  }
+}
+
+// Two adjacent activation values stored with one LDS write.
+template <typename T>
+__device__ __forceinline__ void st_pair(T* dst, float a, float b) {
+  typename Mma<T>::v2 v;
+  v[0] = from_f<T>(a);
+  v[1] = from_f<T>(b);
+  *reinterpret_cast<typename Mma<T>::v2*>(dst) = v;
+}
+
+template <typename T>
+__device__ __forceinline__ void st_row8(T* dst, const float* x) {
+  if constexpr (sizeof(T) == 4) {
+    f4 a, b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { a[i] = x[i]; b[i] = x[4 + i]; }
+    reinterpret_cast<f4*>(dst)[0] = a;
+    reinterpret_cast<f4*>(dst)[1] = b;
+  } else {
+    typename Mma<T>::v8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = from_f<T>(x[i]);
+    *reinterpret_cast<typename Mma<T>::v8*>(dst) = v;
+  }
+}
+
+// ------------------------------------------------------------------ prep
+
+// One wave per token: RMSNorm factors of the raw q / k rows and pi * tanh(angle).
+template <typename T>
+__global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const ScanGeom g,
+                                                   float* __restrict__ out) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (tok >= static_cast<int64_t>(a.batch) * a.length) return;
+  const int b = static_cast<int>(tok / a.length);
+  const int t = static_cast<int>(tok - static_cast<int64_t>(b) * a.length);
+  float* o = out + tok * g.prep_w;
+  const int N = a.d_state;
+  if (g.prep_q >= 0) {
+    for (int gr = 0; gr < a.groups * a.rank; ++gr) {
+      const int gi = gr / a.rank, r = gr - gi * a.rank;
+#pragma unroll
+      for (int which = 0; which < 2; ++which) {
+        const m3_tensor& x = which ? a.k : a.q;
+        const T* p = static_cast<const T*>(x.ptr) + b * x.stride[0] + t * x.stride[1] +
+                     gi * x.stride[2] + r * x.stride[3];
+        float ss = 0.f;
+        for (int n = lane; n < N; n += 64) {
+          const float v = to_f(p[n]);
+          ss += v * v;
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) {
+          o[(which ? g.prep_k : g.prep_q) + gr] =
+              1.f / sqrtf(ss / static_cast<float>(N) + a.norm_eps);
+        }
+      }
+    }
+  }
+  if (g.prep_a >= 0) {
+    for (int s = lane; s < a.num_angles; s += 64) {
+      const float th = ldx(a.phase.ptr, a.phase.dtype,
+                           b * a.phase.stride[0] + t * a.phase.stride[1] + s * a.phase.stride[2]);
+      o[g.prep_a + s] = __fmul_rn(kPi, tanhf(th));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ scan
+
 template <typename T, int R>
-__global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, const ScanGeom g) {
+__global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, const ScanGeom g,
+                                                        const float* __restrict__ prep) {
   using M = Mma<T>;
   constexpr int ROWS = M::ROWS;
   constexpr int RT = ROWS / 16;        // 16-row tiles per sub-chunk
   constexpr int WPR = kWaves / RT;     // waves sharing one query row tile
+  constexpr bool F32 = sizeof(T) == 4;
   const int H = a.heads, L = a.length, N = a.d_state, P = a.head_dim, S = a.num_angles;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
 
-  // ---- block -> (b, h)
+  // ---- block -> (b, h): with xcd_map, the blocks of one XCD (blockIdx % 8) take consecutive
+  // (b, h), so the heads of one batch row share that XCD's L2 for q, k and the angles.
   int bid = blockIdx.x;
   if (g.xcd_map) {
     const int per = gridDim.x >> 3;
@@ -147,64 +300,107 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   const int grp = h / (H / a.groups);
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  T* Qs = lds_t<T>(smem, g.o_qs);
-  T* Ks = lds_t<T>(smem, g.o_ks);
-  T* KeT = lds_t<T>(smem, g.o_ket);
-  T* VT = lds_t<T>(smem, g.o_vt);
-  T* ZT = lds_t<T>(smem, g.o_zt);
-  T* Sb = lds_t<T>(smem, g.o_sb);
-  float* F = lds_t<float>(smem, g.o_f);
-  const FOff fo = f_offsets(g.tok, S, R, P);
-  const int LQ = g.lq, LR = g.lr, NP = g.n_pad, PP = g.p_pad, TOK = g.tok;
+  using Lay = Layout<T>;
+  T* Qs = lds_t<T>(smem, Lay::QS);
+  T* Ks = lds_t<T>(smem, Lay::KS);
+  T* KT = lds_t<T>(smem, Lay::KT);
+  T* VT = lds_t<T>(smem, Lay::VT);
+  T* VsT = lds_t<T>(smem, Lay::VS);
+  T* ZT = lds_t<T>(smem, Lay::ZT);
+  T* Sb = lds_t<T>(smem, Lay::SB);
+  float* F = lds_t<float>(smem, Lay::FB);
+  constexpr int LQ = Lay::LQ, LR = Lay::LR, NP = kNPad, TOK = ROWS / R;
+  const int PW = g.prep_w;
 
-  const bool norm = a.q_norm_w.ptr != nullptr;
+  const bool norm = g.prep_q >= 0;
   const bool bias = a.q_bias.ptr != nullptr;
   const bool rotate = a.phase_mode != M3_PHASE_NONE;
+  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
   const float Dh = ldx(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
 
-  // ---- one-time LDS setup: zero the padded operand regions, MIMO parameters, phase carry
-  for (int i = tid; i < (g.o_f - g.o_qs) / 2; i += kThreads) {
-    reinterpret_cast<uint16_t*>(smem + g.o_qs)[i] = 0;
+  // ---- lane roles
+  // q / k: row pair rp (rows 2rp, 2rp+1), columns n0 .. n0+7
+  const int rp = tid >> 4, n0 = 8 * (tid & 15);
+  const bool qk_on = rp < ROWS / 2 && n0 < N;
+  const int qk_n = min(8, N - n0);
+  // v / z: token pair vp (tokens 2vp, 2vp+1), columns p0 .. p0+3
+  constexpr int p4 = kPPad >> 2;
+  const int vp = tid / p4, p0 = 4 * (tid - vp * p4);
+  const bool vz_on = 2 * vp < TOK && p0 < P;
+  const int vz_n = min(4, P - p0);
+  // phase: angle ps, token group pg (tokens 4pg .. 4pg+3)
+  const int PG = TOK >> 2;
+  const int pg = tid % PG, ps = tid / PG;
+  const bool ph_on = rotate && ps < S;
+
+  // ---- one-time LDS setup: zero the operand regions (padding), MIMO parameters, phase carry
+  for (int i = tid; i < Lay::FB / 4; i += kThreads) {
+    reinterpret_cast<uint32_t*>(smem)[i] = 0u;
   }
   for (int i = tid; i < R * P; i += kThreads) {
     const int r = i / P, p = i - r * P;
+    const int o = r * kPPad + p;
     if (R > 1) {
-      F[fo.mx + i] = rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
-                                h * a.mimo_x.stride[0] + r * a.mimo_x.stride[1] + p));
-      F[fo.mz + i] = rnd<T>(ldx(a.mimo_z.ptr, a.mimo_z.dtype,
-                                h * a.mimo_z.stride[0] + r * a.mimo_z.stride[1] + p));
-      F[fo.mo + i] = ldx(a.mimo_out.ptr, a.mimo_out.dtype,
-                         h * a.mimo_out.stride[0] + r * a.mimo_out.stride[1] + p);
+      F[Lay::MX + o] = rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
+                                  h * a.mimo_x.stride[0] + r * a.mimo_x.stride[1] + p));
+      F[Lay::MZ + o] = rnd<T>(ldx(a.mimo_z.ptr, a.mimo_z.dtype,
+                                  h * a.mimo_z.stride[0] + r * a.mimo_z.stride[1] + p));
+      F[Lay::MO + o] = ldx(a.mimo_out.ptr, a.mimo_out.dtype,
+                           h * a.mimo_out.stride[0] + r * a.mimo_out.stride[1] + p);
     } else {
-      F[fo.mx + i] = 1.f;
-      F[fo.mz + i] = 1.f;
-      F[fo.mo + i] = 1.f;
+      F[Lay::MX + o] = 1.f;
+      F[Lay::MZ + o] = 1.f;
+      F[Lay::MO + o] = 1.f;
     }
   }
   for (int s = tid; s < S; s += kThreads) {
-    F[fo.pbase + s] = 0.f;
-    F[fo.poff + s] = a.initial_phase.ptr != nullptr
+    F[Lay::PBASE + s] = 0.f;
+    F[Lay::POFF + s] = a.initial_phase.ptr != nullptr
                          ? static_cast<const float*>(a.initial_phase.ptr)
                                [b * a.initial_phase.stride[0] + h * a.initial_phase.stride[1] +
                                 s * a.initial_phase.stride[2]]
                          : 0.f;
   }
 
-  // ---- the state: S^T tiles (ni, pj), tile u = w + 4k; lane holds n = 16 ni + 4 lg + i,
-  // p = 16 pj + l16.
-  const int n_tiles = g.nt * g.pt;
-  f4 st[kMaxStateTiles];
+  // per-lane constants of the q / k role: rounded norm weights and the biases of its rows
+  // (rows 2rp, 2rp+1 have ranks (2rp) % R, (2rp+1) % R: one set suffices when R == 1)
+  constexpr int NB = R == 1 ? 1 : 2;
+  float wq[8], wk[8], bq[NB][8], bk[NB][8];
 #pragma unroll
-  for (int k = 0; k < kMaxStateTiles; ++k) {
+  for (int i = 0; i < 8; ++i) {
+    const int n = n0 + i;
+    const bool ok = qk_on && n < N;
+    wq[i] = (ok && norm) ? rnd<T>(ldx(a.q_norm_w.ptr, a.q_norm_w.dtype, n * a.q_norm_w.stride[0]))
+                         : 1.f;
+    wk[i] = (ok && norm) ? rnd<T>(ldx(a.k_norm_w.ptr, a.k_norm_w.dtype, n * a.k_norm_w.stride[0]))
+                         : 1.f;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int r = (2 * rp + j) % R;
+      bq[j][i] = (ok && bias) ? rnd<T>(ldx(a.q_bias.ptr, a.q_bias.dtype,
+                                           h * a.q_bias.stride[0] + r * a.q_bias.stride[1] + n))
+                              : 0.f;
+      bk[j][i] = (ok && bias) ? rnd<T>(ldx(a.k_bias.ptr, a.k_bias.dtype,
+                                           h * a.k_bias.stride[0] + r * a.k_bias.stride[1] + n))
+                              : 0.f;
+    }
+  }
+
+  // ---- the state: S^T tiles (ni, pj), tile u = w + 8k; lane holds n = 16 ni + 4 lg + i,
+  // p = 16 pj + l16.
+  constexpr int n_tiles = kNT * kPT;
+  f4 st[kTiles];
+#pragma unroll
+  for (int k = 0; k < kTiles; ++k) {
     st[k] = zero4();
     const int u = w + kWaves * k;
-    if (u < n_tiles) {
-      const int ni = u / g.pt, pj = u - ni * g.pt;
+    if (u < n_tiles && a.initial_state.ptr != nullptr) {
+      const int ni = u / kPT, pj = u - ni * kPT;
       const int p = 16 * pj + l16;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int n = 16 * ni + 4 * lg + i;
-        if (a.initial_state.ptr != nullptr && p < P && n < N) {
+        if (p < P && n < N) {
           st[k][i] = static_cast<const float*>(a.initial_state.ptr)
               [b * a.initial_state.stride[0] + h * a.initial_state.stride[1] +
                p * a.initial_state.stride[2] + n];
@@ -223,10 +419,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
                                    b * a.trap.stride[0] + h * a.trap.stride[2]));
     const float c0 = dt0 * (1.f - tr0);
 #pragma unroll
-    for (int k = 0; k < kMaxStateTiles; ++k) {
+    for (int k = 0; k < kTiles; ++k) {
       const int u = w + kWaves * k;
       if (u >= n_tiles) continue;
-      const int ni = u / g.pt, pj = u - ni * g.pt;
+      const int ni = u / kPT, pj = u - ni * kPT;
       const int p = 16 * pj + l16;
       if (p >= P) continue;
       const float v0 = to_f(static_cast<const T*>(a.initial_value.ptr)
@@ -250,300 +446,424 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       }
     }
   }
+
+  // ---- per-(b, h) bases of the per-token reads (hoisted out of the sub-chunk loop)
+  const T* q_row = static_cast<const T*>(a.q.ptr) + b * a.q.stride[0] + grp * a.q.stride[2] + n0;
+  const T* k_row = static_cast<const T*>(a.k.ptr) + b * a.k.stride[0] + grp * a.k.stride[2] + n0;
+  // token / rank strides fit 32 bits (they are strides within one batch row)
+  const int q_t = static_cast<int>(a.q.stride[1]), q_r = static_cast<int>(a.q.stride[3]);
+  const int k_t = static_cast<int>(a.k.stride[1]), k_r = static_cast<int>(a.k.stride[3]);
+  const T* v_row = static_cast<const T*>(a.value.ptr) + b * a.value.stride[0] +
+                   h * a.value.stride[2] + p0;
+  const T* z_row = static_cast<const T*>(a.gate.ptr) + b * a.gate.stride[0] +
+                   h * a.gate.stride[2] + p0;
+  const int v_t = static_cast<int>(a.value.stride[1]), z_t = static_cast<int>(a.gate.stride[1]);
+  const int dt_d = a.dt.dtype, aa_d = a.a.dtype, tr_d = a.trap.dtype;
+  const void* dt_row = offx(a.dt.ptr, dt_d, b * a.dt.stride[0] + h * a.dt.stride[2]);
+  const void* aa_row = offx(a.a.ptr, aa_d, b * a.a.stride[0] + h * a.a.stride[2]);
+  const void* tr_row = offx(a.trap.ptr, tr_d, b * a.trap.stride[0] + h * a.trap.stride[2]);
+  const int dt_t = static_cast<int>(a.dt.stride[1]), aa_t = static_cast<int>(a.a.stride[1]);
+  const int tr_t = static_cast<int>(a.trap.stride[1]);
+  const bool raw_dt = a.raw_dt != 0, mimo_rot = a.mimo_rotation != 0;
+  const float dt_bias = raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0])
+                               : 0.f;
+  const float* prep_row = prep + static_cast<int64_t>(b) * L * PW;
+  const float* ph_row = a.phase_mode == M3_PHASE_GIVEN
+                            ? static_cast<const float*>(a.phase.ptr) + b * a.phase.stride[0] +
+                                  h * a.phase.stride[2] + ps * a.phase.stride[3]
+                            : nullptr;
+  const int ph_t = a.phase_mode == M3_PHASE_GIVEN ? static_cast<int>(a.phase.stride[1]) : 0;
+  float* fph = a.final_phase.ptr != nullptr
+                   ? static_cast<float*>(a.final_phase.ptr) + b * a.final_phase.stride[0] +
+                         h * a.final_phase.stride[1] + ps * a.final_phase.stride[2]
+                   : nullptr;
+  T* out_row = static_cast<T*>(a.out.ptr) + b * a.out.stride[0] + h * a.out.stride[2];
+  const int out_t = static_cast<int>(a.out.stride[1]);
+
+  // ---- registers the next sub-chunk's global data is loaded into
+  constexpr int W8 = Words<T>::W8, W4 = Words<T>::W4;
+  uint32_t rq[2][W8], rk[2][W8], rv[2][W4], rz[2][W4];
+  float fq[2] = {1.f, 1.f}, fk[2] = {1.f, 1.f};
+  float sdt = 0.f, sa = 0.f, str = 0.f, ldt = 0.f, ltr = 0.f;
+  float pa[4] = {0.f, 0.f, 0.f, 0.f};
+
   __syncthreads();
-
-  // ---- sub-chunk loop
-  for (int t0 = 0; t0 < L; t0 += TOK) {
-    const int width = min(TOK, L - t0);
-
-    // (1) per-token scalars: every wave computes them for lane = token.
-    const int tg = t0 + lane;
-    const bool tv = lane < width;
-    float dt = 0.f, adt = 0.f, tr = 0.f;
-    if (tv) {
-      dt_adt(a.raw_dt, ldx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + tg * a.dt.stride[1] +
-                                                     h * a.dt.stride[2]),
-             ldx(a.a.ptr, a.a.dtype, b * a.a.stride[0] + tg * a.a.stride[1] + h * a.a.stride[2]),
-             a.raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]) : 0.f, dt,
-             adt);
-      tr = sigmoidf(ldx(a.trap.ptr, a.trap.dtype,
-                        b * a.trap.stride[0] + tg * a.trap.stride[1] + h * a.trap.stride[2]));
-    }
+  const int nsub = (L + TOK - 1) / TOK;
+  // c = -1 only loads sub-chunk 0; iteration c consumes the registers loaded for it, issues the
+  // loads of sub-chunk c + 1, then computes c while those loads are in flight.
+  for (int c = -1; c < nsub; ++c) {
+   const int t0 = c * TOK;
+   const int width = min(TOK, L - t0);
+   if (c >= 0) {
+    // (1) per-token scalars, wave 0, lane = token
     if (w == 0) {
-      // right trapezoid endpoint of the next token: dt_{t+1} (1 - trap_{t+1}), 0 past the end
-      float left = dt * (1.f - tr);
-      float right = __shfl_down(left, 1);
-      if (lane == TOK - 1 || lane == 63) {
+      const bool tv = lane < width;
+      const int tg = t0 + lane;
+      float dt = 0.f, adt = 0.f, tr = 0.f;
+      if (tv) {
+        dt_adt(raw_dt, sdt, sa, dt_bias, dt, adt);
+        tr = sigmoidf(str);
+      }
+      float right = __shfl_down(dt * (1.f - tr), 1);
+      if (lane == TOK - 1) {
         right = 0.f;
-        const int tn = t0 + TOK;
-        if (lane == TOK - 1 && tn < L) {
+        if (t0 + TOK < L) {
           float dtn, adtn;
-          dt_adt(a.raw_dt, ldx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + tn * a.dt.stride[1] +
-                                                         h * a.dt.stride[2]),
-                 ldx(a.a.ptr, a.a.dtype,
-                     b * a.a.stride[0] + tn * a.a.stride[1] + h * a.a.stride[2]),
-                 a.raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]) : 0.f,
-                 dtn, adtn);
-          const float trn = sigmoidf(ldx(a.trap.ptr, a.trap.dtype,
-                                         b * a.trap.stride[0] + tn * a.trap.stride[1] +
-                                             h * a.trap.stride[2]));
-          right = dtn * (1.f - trn);
+          dt_adt(raw_dt, ldt, 0.f, dt_bias, dtn, adtn);
+          right = dtn * (1.f - sigmoidf(ltr));
         }
       }
-      if (!(tg + 1 < L)) right = 0.f;
+      if (!(tg + 1 < L) || lane >= TOK) right = 0.f;
       const float gamma = dt * tr;
       const float scale = gamma + right;
       const float cum = wave_incl_scan(tv ? adt : 0.f, lane);
       const float cum_last = __shfl(cum, width - 1);
-      if (lane < 64) {
-        const float c = tv ? cum : cum_last;
-        F[fo.cum + lane] = c;
-        F[fo.ecum + lane] = tv ? expf(c) : 0.f;
-        F[fo.diag + lane] = tv ? gamma / scale : 0.f;
-        F[fo.scale + lane] = tv ? rnd<T>(scale) : 0.f;
-        F[fo.eend + lane] = tv ? rnd<T>(expf(cum_last - cum)) : 0.f;
-      }
-      if (lane == 0) F[fo.ecl] = expf(cum_last);
+      F[Lay::CUM + lane] = tv ? cum : cum_last;
+      F[Lay::ECUM + lane] = tv ? __expf(cum) : 0.f;
+      F[Lay::SCL + lane] = tv ? scale : 0.f;
+      F[Lay::GAM + lane] = tv ? gamma : 0.f;
+      F[Lay::VSF + lane] = tv ? scale * __expf(cum_last - cum) : 0.f;
+      F[Lay::DTV + lane] = tv ? dt : 0.f;
+      if (lane == 0) F[Lay::ECL] = __expf(cum_last);
     }
+    __syncthreads();
 
-    // (2) phase and its cos / sin per (token, angle), angle s handled by wave s % 4.
-    if (rotate) {
-      const bool new_block = (t0 & 63) == 0;
-      for (int s = w; s < S; s += kWaves) {
-        float ph = 0.f;
-        if (a.phase_mode == M3_PHASE_GIVEN) {
-          if (tv) {
-            ph = static_cast<const float*>(a.phase.ptr)[b * a.phase.stride[0] +
-                                                        tg * a.phase.stride[1] +
-                                                        h * a.phase.stride[2] +
-                                                        s * a.phase.stride[3]];
-          }
-        } else {
-          float inc = 0.f;
-          if (tv) {
-            inc = phase_inc(ldx(a.phase.ptr, a.phase.dtype,
-                                b * a.phase.stride[0] + tg * a.phase.stride[1] +
-                                    s * a.phase.stride[2]),
-                            dt);
-          }
-          const float loc = wave_incl_scan(inc, lane);
-          float base = F[fo.pbase + s], off = F[fo.poff + s];
-          if (new_block && t0 > 0) {
-            off = fmodf(__fadd_rn(off, base), kTwoPi);
-            base = 0.f;
-          }
-          ph = fmodf(__fadd_rn(__fadd_rn(base, loc), off), kTwoPi);
-          const float tot = __shfl(loc, 63);
-          if (lane == 0) {
-            F[fo.pbase + s] = __fadd_rn(base, tot);
-            F[fo.poff + s] = off;
-          }
-          if (tv && tg == L - 1 && a.final_phase.ptr != nullptr) {
-            static_cast<float*>(a.final_phase.ptr)[b * a.final_phase.stride[0] +
-                                                   h * a.final_phase.stride[1] +
-                                                   s * a.final_phase.stride[2]] = ph;
-          }
+    // (2) phase of (token 4pg + i, angle ps) and its cos / sin
+    if (ph_on) {
+      float ph[4];
+      if (angles) {
+        float c[4];
+        float run = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tt = 4 * pg + i;
+          const float inc = tt < width ? m3_fmod_2pi(__fmul_rn(pa[i], F[Lay::DTV + tt])) : 0.f;
+          run = __fadd_rn(run, inc);
+          c[i] = run;
         }
-        if (lane < TOK) {
-          F[fo.cs + lane * S + s] = rnd<T>(cosf(ph));
-          F[fo.sn + lane * S + s] = rnd<T>(sinf(ph));
+        // exclusive scan of the group totals over the PG lanes of this angle
+        float incl = run;
+        for (int o = 1; o < PG; o <<= 1) {
+          const float u = __shfl_up(incl, o, PG);
+          if (pg >= o) incl = __fadd_rn(incl, u);
         }
+        const float excl = __fsub_rn(incl, run);
+        float base = F[Lay::PBASE + ps], off = F[Lay::POFF + ps];
+        if ((t0 & 63) == 0 && t0 > 0) {
+          off = m3_fmod_2pi(__fadd_rn(off, base));
+          base = 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ph[i] = m3_fmod_2pi(__fadd_rn(__fadd_rn(base, __fadd_rn(excl, c[i])), off));
+          const int tg = t0 + 4 * pg + i;
+          if (tg == L - 1 && fph != nullptr) *fph = ph[i];
+        }
+        if (pg == PG - 1) {
+          F[Lay::PBASE + ps] = __fadd_rn(base, incl);
+          F[Lay::POFF + ps] = off;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ph[i] = pa[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tt = 4 * pg + i;
+        float sv, cv;
+        __sincosf(ph[i], &sv, &cv);
+        F[Lay::CS + tt * kSMax + ps] = cv;
+        F[Lay::SN + tt * kSMax + ps] = sv;
       }
     }
     __syncthreads();
 
-    // (3) q / k rows: RMSNorm, bias, rotation, scale -> Qs, Ks, KeT.
-    const bool mimo_pairs = a.mimo_rotation != 0;
-    for (int row = w; row < ROWS; row += kWaves) {
-      const int tt = row / R, r = row - tt * R;
-      const int tgr = t0 + tt;
-      const bool valid = tt < width;
-      const int64_t qo = b * a.q.stride[0] + tgr * a.q.stride[1] + grp * a.q.stride[2] +
-                         r * a.q.stride[3];
-      const int64_t ko = b * a.k.stride[0] + tgr * a.k.stride[1] + grp * a.k.stride[2] +
-                         r * a.k.stride[3];
-      const int half = N >> 1;
-      // each lane owns pairs j = lane + 64 m
-      float q0[2], q1[2], k0[2], k1[2];
-      int e0[2], e1[2];
-      float ssq = 0.f, ssk = 0.f;
+    // (3) q / k rows -> Qs, Ks (row-major), KT (transposed); rows 2rp, 2rp+1
+    if (qk_on) {
+      float kt[2][8];
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int j = lane + 64 * m;
-        e0[m] = mimo_pairs ? j : 2 * j;
-        e1[m] = mimo_pairs ? j + half : 2 * j + 1;
-        q0[m] = q1[m] = k0[m] = k1[m] = 0.f;
-        if (valid && j < half) {
-          const T* qp = static_cast<const T*>(a.q.ptr) + qo;
-          const T* kp = static_cast<const T*>(a.k.ptr) + ko;
-          q0[m] = to_f(qp[e0[m]]);
-          q1[m] = to_f(qp[e1[m]]);
-          k0[m] = to_f(kp[e0[m]]);
-          k1[m] = to_f(kp[e1[m]]);
-          ssq += q0[m] * q0[m] + q1[m] * q1[m];
-          ssk += k0[m] * k0[m] + k1[m] * k1[m];
+      for (int j = 0; j < 2; ++j) {
+        const int row = 2 * rp + j, tt = row / R, r = row - tt * R;
+        const bool ok = tt < width;
+        float q[8], k[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          q[i] = fmaf(raw_get<T>(rq[j], i), fq[j] * wq[i], bq[R == 1 ? 0 : j][i]);
+          k[i] = fmaf(raw_get<T>(rk[j], i), fk[j] * wk[i], bk[R == 1 ? 0 : j][i]);
+          if (!ok) q[i] = k[i] = 0.f;
         }
-      }
-      float rq = 1.f, rk = 1.f;
-      if (norm) {
-        ssq = wave_sum(ssq);
-        ssk = wave_sum(ssk);
-        rq = 1.f / sqrtf(ssq / static_cast<float>(N) + a.norm_eps);
-        rk = 1.f / sqrtf(ssk / static_cast<float>(N) + a.norm_eps);
-      }
-      const float sc = F[fo.scale + tt];
-      const float ee = F[fo.eend + tt];
+        if (rotate && ok) {
+          if (!mimo_rot) {
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int j = lane + 64 * m;
-        if (j >= half) continue;
-        float a0 = q0[m], a1 = q1[m], c0 = k0[m], c1 = k1[m];
-        if (valid) {
-          if (norm) {
-            const float wq0 = rnd<T>(ldx(a.q_norm_w.ptr, a.q_norm_w.dtype,
-                                         e0[m] * a.q_norm_w.stride[0]));
-            const float wq1 = rnd<T>(ldx(a.q_norm_w.ptr, a.q_norm_w.dtype,
-                                         e1[m] * a.q_norm_w.stride[0]));
-            const float wk0 = rnd<T>(ldx(a.k_norm_w.ptr, a.k_norm_w.dtype,
-                                         e0[m] * a.k_norm_w.stride[0]));
-            const float wk1 = rnd<T>(ldx(a.k_norm_w.ptr, a.k_norm_w.dtype,
-                                         e1[m] * a.k_norm_w.stride[0]));
-            a0 = rnd<T>(a0 * rq * wq0);
-            a1 = rnd<T>(a1 * rq * wq1);
-            c0 = rnd<T>(c0 * rk * wk0);
-            c1 = rnd<T>(c1 * rk * wk1);
-          }
-          if (bias) {
-            const int64_t bo = h * a.q_bias.stride[0] + r * a.q_bias.stride[1];
-            const int64_t bk = h * a.k_bias.stride[0] + r * a.k_bias.stride[1];
-            a0 = add_r<T>(a0, rnd<T>(ldx(a.q_bias.ptr, a.q_bias.dtype, bo + e0[m])));
-            a1 = add_r<T>(a1, rnd<T>(ldx(a.q_bias.ptr, a.q_bias.dtype, bo + e1[m])));
-            c0 = add_r<T>(c0, rnd<T>(ldx(a.k_bias.ptr, a.k_bias.dtype, bk + e0[m])));
-            c1 = add_r<T>(c1, rnd<T>(ldx(a.k_bias.ptr, a.k_bias.dtype, bk + e1[m])));
-          }
-          if (rotate && j < S) {
-            const float cc = F[fo.cs + tt * S + j], ss = F[fo.sn + tt * S + j];
-            const float ra0 = sub_r<T>(mul_r<T>(a0, cc), mul_r<T>(a1, ss));
-            const float ra1 = add_r<T>(mul_r<T>(a0, ss), mul_r<T>(a1, cc));
-            const float rc0 = sub_r<T>(mul_r<T>(c0, cc), mul_r<T>(c1, ss));
-            const float rc1 = add_r<T>(mul_r<T>(c0, ss), mul_r<T>(c1, cc));
-            a0 = ra0; a1 = ra1; c0 = rc0; c1 = rc1;
-          }
-          if (tgr == L - 1 && a.final_k.ptr != nullptr) {
-            T* fk = static_cast<T*>(a.final_k.ptr) + b * a.final_k.stride[0] +
-                    h * a.final_k.stride[1] + r * a.final_k.stride[2];
-            fk[e0[m]] = from_f<T>(c0);
-            fk[e1[m]] = from_f<T>(c1);
+            for (int i = 0; i < 8; i += 2) {
+              const int jn = (n0 + i) >> 1;
+              if (jn < S) {
+                const float cc = F[Lay::CS + tt * kSMax + jn], ss = F[Lay::SN + tt * kSMax + jn];
+                const float q0 = q[i], q1 = q[i + 1], k0 = k[i], k1 = k[i + 1];
+                q[i] = fmaf(q0, cc, -q1 * ss);
+                q[i + 1] = fmaf(q0, ss, q1 * cc);
+                k[i] = fmaf(k0, cc, -k1 * ss);
+                k[i + 1] = fmaf(k0, ss, k1 * cc);
+              }
+            }
+          } else {
+            // pairs (n, n + N/2) for n < S = N/4: the partner lives N/16 lanes away (N >= 16),
+            // or in this lane (N <= 8)
+            const int half = N >> 1;
+            float qp[8], kp[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              if (half >= 8) {
+                qp[i] = __shfl_xor(q[i], half >> 3, 16);
+                kp[i] = __shfl_xor(k[i], half >> 3, 16);
+              } else {
+                qp[i] = q[i ^ half];
+                kp[i] = k[i ^ half];
+              }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const int n = n0 + i;
+              if (n < S) {  // first quarter: x cos - partner sin
+                const float cc = F[Lay::CS + tt * kSMax + n], ss = F[Lay::SN + tt * kSMax + n];
+                q[i] = fmaf(q[i], cc, -qp[i] * ss);
+                k[i] = fmaf(k[i], cc, -kp[i] * ss);
+              } else if (n >= 2 * S && n < 3 * S) {  // third quarter: partner sin + x cos
+                const float cc = F[Lay::CS + tt * kSMax + n - 2 * S], ss = F[Lay::SN + tt * kSMax + n - 2 * S];
+                q[i] = fmaf(qp[i], ss, q[i] * cc);
+                k[i] = fmaf(kp[i], ss, k[i] * cc);
+              }
+            }
           }
         }
-        const float ks0 = mul_r<T>(c0, sc), ks1 = mul_r<T>(c1, sc);
-        Qs[row * LQ + e0[m]] = from_f<T>(a0);
-        Qs[row * LQ + e1[m]] = from_f<T>(a1);
-        Ks[row * LQ + e0[m]] = from_f<T>(ks0);
-        Ks[row * LQ + e1[m]] = from_f<T>(ks1);
-        KeT[e0[m] * LR + row] = from_f<T>(mul_r<T>(ks0, ee));
-        KeT[e1[m] * LR + row] = from_f<T>(mul_r<T>(ks1, ee));
-      }
-    }
-    // (4) value / gate rows -> VT, ZT (rank values, activation dtype).
-    for (int idx = tid; idx < TOK * P; idx += kThreads) {
-      const int tt = idx / P, p = idx - tt * P;
-      const int tgr = t0 + tt;
-      float v = 0.f, z = 0.f;
-      if (tt < width) {
-        v = to_f(static_cast<const T*>(a.value.ptr)[b * a.value.stride[0] +
-                                                    tgr * a.value.stride[1] +
-                                                    h * a.value.stride[2] + p]);
-        z = to_f(static_cast<const T*>(a.gate.ptr)[b * a.gate.stride[0] +
-                                                   tgr * a.gate.stride[1] +
-                                                   h * a.gate.stride[2] + p]);
+        st_row8<T>(Qs + row * LQ + n0, q);
+        st_row8<T>(Ks + row * LQ + n0, k);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
       }
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int row = tt * R + r;
-        VT[p * LR + row] = from_f<T>(R > 1 ? mul_r<T>(v, F[fo.mx + r * P + p]) : v);
-        ZT[p * LR + row] = from_f<T>(R > 1 ? mul_r<T>(z, F[fo.mz + r * P + p]) : z);
+      for (int i = 0; i < 8; ++i) {
+        if (n0 + i < N) st_pair<T>(KT + (n0 + i) * LR + 2 * rp, kt[0][i], kt[1][i]);
       }
     }
-    // (5) the state at the start of this sub-chunk, rounded to the activation dtype -> Sb[p][n].
+    // (4) value / gate -> VT, VsT, ZT (transposed), tokens 2vp, 2vp+1, columns p0 .. p0+3
+    if (vz_on) {
+      float v[2][4], z[2][4];
 #pragma unroll
-    for (int k = 0; k < kMaxStateTiles; ++k) {
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[j][i] = raw_get<T>(rv[j], i);
+          z[j][i] = raw_get<T>(rz[j], i);
+        }
+      }
+      const float f0 = F[Lay::VSF + 2 * vp], f1 = F[Lay::VSF + 2 * vp + 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = p0 + i;
+        if (p >= P) continue;
+        if (R == 1) {
+          const int row = 2 * vp;
+          st_pair<T>(VT + p * LR + row, v[0][i], v[1][i]);
+          st_pair<T>(VsT + p * LR + row, v[0][i] * f0, v[1][i] * f1);
+          st_pair<T>(ZT + p * LR + row, z[0][i], z[1][i]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const float fj = j ? f1 : f0;
+#pragma unroll
+            for (int r = 0; r < R; r += 2) {
+              const int row = (2 * vp + j) * R + r;
+              const float va = mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p]);
+              const float vb = mul_r<T>(v[j][i], F[Lay::MX + (r + 1) * kPPad + p]);
+              st_pair<T>(VT + p * LR + row, va, vb);
+              st_pair<T>(VsT + p * LR + row, va * fj, vb * fj);
+              st_pair<T>(ZT + p * LR + row, mul_r<T>(z[j][i], F[Lay::MZ + r * kPPad + p]),
+                         mul_r<T>(z[j][i], F[Lay::MZ + (r + 1) * kPPad + p]));
+            }
+          }
+        }
+      }
+    }
+    // (5) the state at the start of this sub-chunk, rounded to the activation dtype -> Sb[p][n]
+#pragma unroll
+    for (int k = 0; k < kTiles; ++k) {
       const int u = w + kWaves * k;
       if (u < n_tiles) {
-        const int ni = u / g.pt, pj = u - ni * g.pt;
+        const int ni = u / kPT, pj = u - ni * kPT;
         T* dst = Sb + (16 * pj + l16) * LQ + 16 * ni + 4 * lg;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[i] = from_f<T>(st[k][i]);
+        st_pair<T>(dst, st[k][0], st[k][1]);
+        st_pair<T>(dst + 2, st[k][2], st[k][3]);
       }
     }
     __syncthreads();
+
+   }  // c >= 0 (stages 1-5)
+
+   // ---- loads of sub-chunk c + 1 into registers; they fly while sub-chunk c computes
+   if (c + 1 < nsub) {
+    const int n0t = t0 + TOK;  // first token of sub-chunk c + 1
+    const int nw = min(TOK, L - n0t);
+    if (qk_on) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int row = 2 * rp + j, tt = row / R, r = row - tt * R;
+        const bool ok = tt < nw;
+        const int64_t tg = n0t + tt;
+        load_words<T, 8>(rq[j], q_row + tg * q_t + r * q_r, ok ? qk_n : 0, g.vec_qk);
+        load_words<T, 8>(rk[j], k_row + tg * k_t + r * k_r, ok ? qk_n : 0, g.vec_qk);
+        if (norm && ok) {
+          const float* pr = prep_row + tg * PW;
+          fq[j] = pr[g.prep_q + grp * R + r];
+          fk[j] = pr[g.prep_k + grp * R + r];
+        }
+      }
+    }
+    if (vz_on) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int tt = 2 * vp + j;
+        const bool ok = tt < nw;
+        const int64_t tg = n0t + tt;
+        load_words<T, 4>(rv[j], v_row + tg * v_t, ok ? vz_n : 0, g.vec_vz);
+        load_words<T, 4>(rz[j], z_row + tg * z_t, ok ? vz_n : 0, g.vec_vz);
+      }
+    }
+    if (w == 0) {
+      const int64_t tg = n0t + lane;
+      sdt = sa = str = ldt = ltr = 0.f;
+      if (lane < nw) {
+        sdt = ldx(dt_row, dt_d, tg * dt_t);
+        sa = ldx(aa_row, aa_d, tg * aa_t);
+        str = ldx(tr_row, tr_d, tg * tr_t);
+      }
+      const int64_t tn = n0t + TOK;
+      if (lane == TOK - 1 && tn < L) {
+        ldt = ldx(dt_row, dt_d, tn * dt_t);
+        ltr = ldx(tr_row, tr_d, tn * tr_t);
+      }
+    }
+    if (ph_on) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tt = 4 * pg + i;
+        const int64_t tg = n0t + tt;
+        pa[i] = 0.f;
+        if (tt < nw) {
+          pa[i] = angles ? prep_row[tg * PW + g.prep_a + ps] : ph_row[tg * ph_t];
+        }
+      }
+    }
+   }
+
+   if (c >= 0) {
 
     // (6) outputs for query row tile `it` and P tiles pj = wp, wp + WPR, ...
     {
       const int it = w / WPR, wp = w - it * WPR;
-      const int trow = 16 * it + l16;            // query row in D-layout columns
+      const int trow = 16 * it + l16;
       const int tq = trow / R;
-      const float cum_t = F[fo.cum + tq];
-      const float diag_t = F[fo.diag + tq];
-      // scores^T tiles (sj <= it): rows s = 16 sj + 4 lg + i, column t = trow
+      const float cum_t = F[Lay::CUM + tq];
+      const float gam_t = F[Lay::GAM + tq];
       f4 wsc[RT];
+      if constexpr (!F32) {
+        // the query rows of this tile: B operand of the scores, A operand of the inter term
+        typename M::v8 qv[4];
 #pragma unroll
-      for (int sj = 0; sj < RT; ++sj) {
-        wsc[sj] = zero4();
-        if (sj > it) continue;
-        f4 acc = zero4();
-        if constexpr (sizeof(T) == 2) {
-          for (int kk = 0; kk < NP; kk += 32) {
-            const typename M::v8 av =
-                *reinterpret_cast<const typename M::v8*>(Ks + (16 * sj + l16) * LQ + kk + 8 * lg);
-            const typename M::v8 bv =
-                *reinterpret_cast<const typename M::v8*>(Qs + trow * LQ + kk + 8 * lg);
-            acc = M::mma(av, bv, acc);
-          }
-        } else {
-          for (int kk = 0; kk < NP; kk += 4) {
-            acc = M::mma(Ks[(16 * sj + l16) * LQ + kk + lg], Qs[trow * LQ + kk + lg], acc);
-          }
+        for (int kk = 0; kk < 4; ++kk) {
+          if (32 * kk < NP) qv[kk] = *reinterpret_cast<const typename M::v8*>(
+                                    Qs + trow * LQ + 32 * kk + 8 * lg);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int srow = 16 * sj + 4 * lg + i;
-          const int ts = srow / R;
-          const float d = tq > ts ? expf(cum_t - F[fo.cum + ts]) : (tq == ts ? diag_t : 0.f);
-          wsc[sj][i] = rnd<T>(acc[i] * d);
+        for (int sj = 0; sj < RT; ++sj) {
+          wsc[sj] = zero4();
+          if (sj > it) continue;
+          f4 acc = zero4();
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) {
+            if (32 * kk < NP) {
+              const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
+                  Ks + (16 * sj + l16) * LQ + 32 * kk + 8 * lg);
+              acc = M::mma(av, qv[kk], acc);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int ts = (16 * sj + 4 * lg + i) / R;
+            const float d = tq > ts ? F[Lay::SCL + ts] * __expf(cum_t - F[Lay::CUM + ts])
+                                    : (tq == ts ? gam_t : 0.f);
+            wsc[sj][i] = rnd<T>(acc[i] * d);
+          }
         }
-      }
-      for (int pj = wp; pj < g.pt; pj += WPR) {
-        const int pcol = 16 * pj + l16;
-        f4 yi = zero4(), ye = zero4();
-        // intra: W V with the K axis permuted as the D-layout of wsc
-        if constexpr (sizeof(T) == 2) {
+        for (int pj = wp; pj < kPT; pj += WPR) {
+          const int pcol = 16 * pj + l16;
+          f4 yi = zero4(), ye = zero4();
 #pragma unroll
           for (int m = 0; m < (RT + 1) / 2; ++m) {
             if (2 * m > it) continue;
-            typename M::v8 av;
+            typename M::v8 av, bv;
             const typename M::v4 b0 =
                 *reinterpret_cast<const typename M::v4*>(VT + pcol * LR + 32 * m + 4 * lg);
             const typename M::v4 b1 =
                 *reinterpret_cast<const typename M::v4*>(VT + pcol * LR + 32 * m + 16 + 4 * lg);
-            typename M::v8 bv;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               av[i] = from_f<T>(wsc[2 * m][i]);
-              av[4 + i] = (2 * m + 1 < RT) ? from_f<T>(wsc[2 * m + 1][i]) : from_f<T>(0.f);
+              av[4 + i] = from_f<T>(2 * m + 1 < RT ? wsc[2 * m + 1][i] : 0.f);
               bv[i] = b0[i];
               bv[4 + i] = b1[i];
             }
             yi = M::mma(av, bv, yi);
           }
-          for (int kk = 0; kk < NP; kk += 32) {
-            const typename M::v8 av =
-                *reinterpret_cast<const typename M::v8*>(Qs + (16 * it + l16) * LQ + kk + 8 * lg);
-            const typename M::v8 bv =
-                *reinterpret_cast<const typename M::v8*>(Sb + pcol * LQ + kk + 8 * lg);
-            ye = M::mma(av, bv, ye);
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) {
+            if (32 * kk < NP) {
+              const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
+                  Sb + pcol * LQ + 32 * kk + 8 * lg);
+              ye = M::mma(qv[kk], bv, ye);
+            }
           }
-        } else {
+          if (pcol < P) {
+            const typename M::v4 vv =
+                *reinterpret_cast<const typename M::v4*>(VT + pcol * LR + 16 * it + 4 * lg);
+            const typename M::v4 zz =
+                *reinterpret_cast<const typename M::v4*>(ZT + pcol * LR + 16 * it + 4 * lg);
+            float y = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int row = 16 * it + 4 * lg + i;
+              const int tt = row / R, r = row - tt * R;
+              const float zf = to_f(zz[i]);
+              float yr = (fmaf(ye[i], F[Lay::ECUM + tt], yi[i]) + Dh * to_f(vv[i])) *
+                         __fdividef(zf, 1.f + __expf(-zf));
+              if (R > 1) yr *= F[Lay::MO + r * kPPad + pcol];
+              y = (R > 1 && r > 0) ? y + yr : yr;
+              if (r == R - 1 && tt < width) {
+                out_row[(t0 + tt) * out_t + pcol] = from_f<T>(y);
+              }
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int sj = 0; sj < RT; ++sj) {
+          wsc[sj] = zero4();
+          if (sj > it) continue;
+          f4 acc = zero4();
+          for (int kk = 0; kk < NP; kk += 4) {
+            acc = M::mma(Ks[(16 * sj + l16) * LQ + kk + lg], Qs[trow * LQ + kk + lg], acc);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int ts = (16 * sj + 4 * lg + i) / R;
+            const float d = tq > ts ? F[Lay::SCL + ts] * __expf(cum_t - F[Lay::CUM + ts])
+                                    : (tq == ts ? gam_t : 0.f);
+            wsc[sj][i] = acc[i] * d;
+          }
+        }
+        for (int pj = wp; pj < kPT; pj += WPR) {
+          const int pcol = 16 * pj + l16;
+          f4 yi = zero4(), ye = zero4();
 #pragma unroll
           for (int sj = 0; sj < RT; ++sj) {
             if (sj > it) continue;
@@ -553,68 +873,77 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
             }
           }
           for (int kk = 0; kk < NP; kk += 4) {
-            ye = M::mma(Qs[(16 * it + l16) * LQ + kk + lg], Sb[pcol * LQ + kk + lg], ye);
+            ye = M::mma(Qs[trow * LQ + kk + lg], Sb[pcol * LQ + kk + lg], ye);
           }
-        }
-        // epilogue: rows 16 it + 4 lg + i, column pcol
-        if (pcol < P) {
-          float y = 0.f;
+          if (pcol < P) {
+            float y = 0.f;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int row = 16 * it + 4 * lg + i;
-            const int tt = row / R, r = row - tt * R;
-            const float v = to_f(VT[pcol * LR + row]);
-            const float z = to_f(ZT[pcol * LR + row]);
-            float yr = (ye[i] * F[fo.ecum + tt] + yi[i] + Dh * v) * siluf(z);
-            if (R > 1) yr *= F[fo.mo + r * P + pcol];
-            y = (R > 1 && r > 0) ? y + yr : yr;
-            if (r == R - 1 && tt < width) {
-              static_cast<T*>(a.out.ptr)[b * a.out.stride[0] + (t0 + tt) * a.out.stride[1] +
-                                         h * a.out.stride[2] + pcol] = from_f<T>(y);
+            for (int i = 0; i < 4; ++i) {
+              const int row = 16 * it + 4 * lg + i;
+              const int tt = row / R, r = row - tt * R;
+              const float zf = ZT[pcol * LR + row];
+              float yr = (fmaf(ye[i], F[Lay::ECUM + tt], yi[i]) + Dh * VT[pcol * LR + row]) *
+                         __fdividef(zf, 1.f + __expf(-zf));
+              if (R > 1) yr *= F[Lay::MO + r * kPPad + pcol];
+              y = (R > 1 && r > 0) ? y + yr : yr;
+              if (r == R - 1 && tt < width) {
+                out_row[(t0 + tt) * out_t + pcol] = y;
+              }
             }
           }
         }
       }
     }
 
-    // (7) state carry: S^T = exp(cum_last) S^T + Ke^T V
+    // (7) state carry: S^T = exp(cum_last) S^T + K^T Vs
     {
-      const float ecl = F[fo.ecl];
+      const float ecl = F[Lay::ECL];
 #pragma unroll
-      for (int k = 0; k < kMaxStateTiles; ++k) {
+      for (int k = 0; k < kTiles; ++k) {
         const int u = w + kWaves * k;
         if (u >= n_tiles) continue;
-        const int ni = u / g.pt, pj = u - ni * g.pt;
+        const int ni = u / kPT, pj = u - ni * kPT;
         f4 acc = zero4();
-        if constexpr (sizeof(T) == 2) {
+        if constexpr (!F32) {
 #pragma unroll
           for (int kk = 0; kk < ROWS; kk += 32) {
-            const typename M::v8 av =
-                *reinterpret_cast<const typename M::v8*>(KeT + (16 * ni + l16) * LR + kk + 8 * lg);
-            const typename M::v8 bv =
-                *reinterpret_cast<const typename M::v8*>(VT + (16 * pj + l16) * LR + kk + 8 * lg);
+            const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
+                KT + (16 * ni + l16) * LR + kk + 8 * lg);
+            const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
+                VsT + (16 * pj + l16) * LR + kk + 8 * lg);
             acc = M::mma(av, bv, acc);
           }
         } else {
 #pragma unroll
           for (int kk = 0; kk < ROWS; kk += 4) {
-            acc = M::mma(KeT[(16 * ni + l16) * LR + kk + lg], VT[(16 * pj + l16) * LR + kk + lg],
+            acc = M::mma(KT[(16 * ni + l16) * LR + kk + lg], VsT[(16 * pj + l16) * LR + kk + lg],
                          acc);
           }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st[k][i] = ecl * st[k][i] + acc[i];
+        for (int i = 0; i < 4; ++i) st[k][i] = fmaf(ecl, st[k][i], acc[i]);
       }
     }
     __syncthreads();
+   }  // c >= 0 (stages 6-7)
+  }
+
+  // ---- final k: the biased, rotated k of token L-1, still in Ks from the last sub-chunk
+  if (a.final_k.ptr != nullptr && L > 0) {
+    const int tl = (L - 1) - (nsub - 1) * TOK;  // its row in the last sub-chunk
+    for (int i = tid; i < R * N; i += kThreads) {
+      const int r = i / N, n = i - r * N;
+      static_cast<T*>(a.final_k.ptr)[b * a.final_k.stride[0] + h * a.final_k.stride[1] +
+                                     r * a.final_k.stride[2] + n] = Ks[(tl * R + r) * LQ + n];
+    }
   }
 
   // ---- final state
 #pragma unroll
-  for (int k = 0; k < kMaxStateTiles; ++k) {
+  for (int k = 0; k < kTiles; ++k) {
     const int u = w + kWaves * k;
     if (u >= n_tiles) continue;
-    const int ni = u / g.pt, pj = u - ni * g.pt;
+    const int ni = u / kPT, pj = u - ni * kPT;
     const int p = 16 * pj + l16;
     if (p >= P) continue;
 #pragma unroll
@@ -631,40 +960,59 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 
 // ------------------------------------------------------------------ host side
 
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 template <typename T>
 static ScanGeom make_geom(const m3_scan_args& a) {
-  using M = Mma<T>;
   ScanGeom g{};
   const int es = sizeof(T);
-  g.n_pad = (a.d_state + 31) / 32 * 32;
-  g.p_pad = (a.head_dim + 15) / 16 * 16;
-  g.lq = g.n_pad + M::PAD;
-  g.lr = M::ROWS + M::PAD;
-  g.tok = M::ROWS / a.rank;
-  g.nt = g.n_pad / 16;
-  g.pt = g.p_pad / 16;
   const int total = a.batch * a.heads;
   g.xcd_map = (total % 8 == 0) ? 1 : 0;
-  auto al = [](int x) { return (x + 15) / 16 * 16; };
-  g.o_qs = 0;
-  g.o_ks = al(g.o_qs + M::ROWS * g.lq * es);
-  g.o_ket = al(g.o_ks + M::ROWS * g.lq * es);
-  g.o_vt = al(g.o_ket + g.n_pad * g.lr * es);
-  g.o_zt = al(g.o_vt + g.p_pad * g.lr * es);
-  g.o_sb = al(g.o_zt + g.p_pad * g.lr * es);
-  g.o_f = al(g.o_sb + g.p_pad * g.lq * es);
-  g.bytes = g.o_f + 4 * f_floats(g.tok, a.num_angles, a.rank, a.head_dim);
+  // vector loads need every row start aligned: base pointers and all outer strides
+  auto vec_ok = [&](const m3_tensor& t, int dims, int need) {
+    if ((reinterpret_cast<uintptr_t>(t.ptr) % need) != 0) return false;
+    for (int i = 0; i < dims - 1; ++i) {
+      if ((t.stride[i] * es) % need != 0) return false;
+    }
+    return true;
+  };
+  g.vec_qk = (a.d_state % 8 == 0) && vec_ok(a.q, 5, 16) && vec_ok(a.k, 5, 16);
+  const int vneed = es * 4;  // 4 elements per v / z load
+  g.vec_vz = (a.head_dim % 4 == 0) && vec_ok(a.value, 4, vneed) && vec_ok(a.gate, 4, vneed);
+  const bool norm = a.q_norm_w.ptr != nullptr;
+  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
+  const int gr = a.groups * a.rank;
+  g.prep_q = norm ? 0 : -1;
+  g.prep_k = norm ? gr : -1;
+  g.prep_a = angles ? (norm ? 2 * gr : 0) : -1;
+  g.prep_w = (norm ? 2 * gr : 0) + (angles ? a.num_angles : 0);
   return g;
+}
+
+static size_t workspace_bytes(const m3_scan_args& a, int prep_w) {
+  return static_cast<size_t>(a.batch) * a.length * prep_w * sizeof(float);
 }
 
 template <typename T, int R>
 static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
   const ScanGeom g = make_geom<T>(a);
-  if (g.nt * g.pt > kWaves * kMaxStateTiles) {
-    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: d_state x head_dim too large for the state tiles");
-  }
-  if (g.bytes > 160 * 1024) {
-    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: shape needs %d bytes of LDS", g.bytes);
+  static_assert(Layout<T>::BYTES <= 160 * 1024, "LDS layout exceeds 160 KiB");
+  const float* prep = nullptr;
+  if (g.prep_w > 0) {
+    const size_t need = workspace_bytes(a, g.prep_w);
+    if (a.workspace == nullptr || a.workspace_bytes < need || !aligned16(a.workspace)) {
+      return fail(M3_EWORKSPACE, "m3_scan_fwd: needs a 16-byte aligned workspace of %zu bytes",
+                  need);
+    }
+    prep = static_cast<const float*>(a.workspace);
+    const int64_t tokens = static_cast<int64_t>(a.batch) * a.length;
+    if (tokens > 0) {
+      const dim3 pgrid(static_cast<unsigned>((tokens + 3) / 4)), pblock(256);
+      hipLaunchKernelGGL(prep_kernel<T>, pgrid, pblock, 0, stream, a, g,
+                         static_cast<float*>(a.workspace));
+      int rc = check_launch("m3_scan_fwd (prep)");
+      if (rc != M3_OK) return rc;
+    }
   }
   static bool attr_set = false;
   if (!attr_set) {
@@ -676,7 +1024,7 @@ static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
     attr_set = true;
   }
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kThreads);
-  hipLaunchKernelGGL((scan_kernel<T, R>), grid, block, g.bytes, stream, a, g);
+  hipLaunchKernelGGL((scan_kernel<T, R>), grid, block, Layout<T>::BYTES, stream, a, g, prep);
   return check_launch("m3_scan_fwd");
 }
 
@@ -699,9 +1047,15 @@ static int validate_scan(const m3_scan_args& a) {
   }
   if (a.heads % a.groups != 0) return fail(M3_EINVAL, "m3_scan_fwd: heads %% groups != 0");
   if (!valid_dtype(a.act_dtype)) return fail(M3_EINVAL, "m3_scan_fwd: invalid act_dtype");
-  if (!pow2(a.d_state) || a.d_state < 4 || a.d_state > 256) {
-    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: d_state %d must be a power of 2 in [4, 256]",
+  if (!pow2(a.d_state) || a.d_state < 4 || a.d_state > 128) {
+    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: d_state %d must be a power of 2 in [4, 128]",
                 a.d_state);
+  }
+  if (a.head_dim > kPPad) {
+    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: head_dim %d > %d", a.head_dim, kPPad);
+  }
+  if (a.num_angles > kSMax) {
+    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: num_angles %d > %d", a.num_angles, kSMax);
   }
   if (a.phase_mode < M3_PHASE_NONE || a.phase_mode > M3_PHASE_ANGLES) {
     return fail(M3_EINVAL, "m3_scan_fwd: invalid phase_mode");
@@ -753,12 +1107,20 @@ static int validate_scan(const m3_scan_args& a) {
   return M3_OK;
 }
 
+static int prep_width(const m3_scan_args& a) {
+  const bool norm = a.q_norm_w.ptr != nullptr;
+  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
+  return (norm ? 2 * a.groups * a.rank : 0) + (angles ? a.num_angles : 0);
+}
+
 }  // namespace m3
 
 extern "C" int m3_scan_workspace_size(const m3_scan_args* args, size_t* bytes) {
   m3::clear_error();
-  if (args == nullptr || bytes == nullptr) return m3::fail(M3_EINVAL, "NULL argument");
-  *bytes = 0;
+  if (args == nullptr || bytes == nullptr) {
+    return m3::fail(M3_EINVAL, "m3_scan_workspace_size: NULL argument");
+  }
+  *bytes = m3::workspace_bytes(*args, m3::prep_width(*args));
   return M3_OK;
 }
 
@@ -775,122 +1137,4 @@ extern "C" int m3_scan_fwd(const m3_scan_args* args, hipStream_t stream) {
     case M3_BF16: return launch_scan<__bf16>(a, stream);
     default: return launch_scan<_Float16>(a, stream);
   }
-}
-
-// ------------------------------------------------------------------ standalone chunk state
-
-namespace m3 {
-
-constexpr int kCsRows = 64;   // rows staged in LDS per pass
-constexpr int kCsMaxE = 64;   // state elements per thread (P * N <= 16384)
-
-// One chunk's state update (_triton.py:294-413) with the portable path's rounding points:
-// ke = rnd(rnd(k * rnd(scale)) * rnd(exp(cum_last - cum))); S' = exp(cum_last) S + V^T ke.
-template <typename T>
-__global__ __launch_bounds__(kThreads) void chunk_state_kernel(const m3_chunk_state_args a) {
-  const int H = a.heads, W = a.width, R = a.rank, N = a.d_state, P = a.head_dim;
-  const int b = blockIdx.x / H, h = blockIdx.x - (blockIdx.x / H) * H;
-  const int tid = threadIdx.x;
-  extern __shared__ float cs_smem[];
-  float* ke = cs_smem;                 // [kCsRows][N]
-  float* vv = cs_smem + kCsRows * N;   // [kCsRows][P]
-  const float* cum = static_cast<const float*>(a.cumulative.ptr) + b * a.cumulative.stride[0] +
-                     h * a.cumulative.stride[1];
-  const float* scl = static_cast<const float*>(a.scale.ptr) + b * a.scale.stride[0] +
-                     h * a.scale.stride[1];
-  const float cl = cum[(W - 1) * a.cumulative.stride[2]];
-  const int rows = W * R, total = P * N;
-  float acc[kCsMaxE];
-#pragma unroll
-  for (int i = 0; i < kCsMaxE; ++i) acc[i] = 0.f;
-  for (int r0 = 0; r0 < rows; r0 += kCsRows) {
-    __syncthreads();
-    for (int idx = tid; idx < kCsRows * N; idx += kThreads) {
-      const int row = r0 + idx / N, n = idx - (idx / N) * N;
-      float v = 0.f;
-      if (row < rows) {
-        const int t = row / R, r = row - t * R;
-        const float k = to_f(static_cast<const T*>(a.k.ptr)[b * a.k.stride[0] + h * a.k.stride[1] +
-                                                             t * a.k.stride[2] +
-                                                             r * a.k.stride[3] + n]);
-        const float sc = rnd<T>(scl[t * a.scale.stride[2]]);
-        const float ee = rnd<T>(expf(cl - cum[t * a.cumulative.stride[2]]));
-        v = mul_r<T>(mul_r<T>(k, sc), ee);
-      }
-      ke[idx] = v;
-    }
-    for (int idx = tid; idx < kCsRows * P; idx += kThreads) {
-      const int row = r0 + idx / P, p = idx - (idx / P) * P;
-      float v = 0.f;
-      if (row < rows) {
-        const int t = row / R, r = row - t * R;
-        v = to_f(static_cast<const T*>(a.value.ptr)[b * a.value.stride[0] + h * a.value.stride[1] +
-                                                    t * a.value.stride[2] +
-                                                    r * a.value.stride[3] + p]);
-      }
-      vv[idx] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kCsMaxE; ++i) {
-      const int e = tid + kThreads * i;
-      if (e < total) {
-        const int p = e / N, n = e - (e / N) * N;
-        float s = 0.f;
-        for (int j = 0; j < kCsRows; ++j) s += vv[j * P + p] * ke[j * N + n];
-        acc[i] += s;
-      }
-    }
-  }
-  const float ecl = expf(cl);
-  const float* sin_ = static_cast<const float*>(a.state_in.ptr) + b * a.state_in.stride[0] +
-                      h * a.state_in.stride[1];
-  float* sout = static_cast<float*>(a.state_out.ptr) + b * a.state_out.stride[0] +
-                h * a.state_out.stride[1];
-#pragma unroll
-  for (int i = 0; i < kCsMaxE; ++i) {
-    const int e = tid + kThreads * i;
-    if (e < total) {
-      const int p = e / N, n = e - (e / N) * N;
-      const float old = sin_[p * a.state_in.stride[2] + n];
-      sout[p * a.state_out.stride[2] + n] = ecl * old + acc[i];
-    }
-  }
-}
-
-}  // namespace m3
-
-extern "C" int m3_chunk_state(const m3_chunk_state_args* args, hipStream_t stream) {
-  using namespace m3;
-  clear_error();
-  if (args == nullptr) return fail(M3_EINVAL, "m3_chunk_state: args is NULL");
-  const m3_chunk_state_args& a = *args;
-  if (a.batch < 0 || a.width <= 0 || a.heads <= 0 || a.rank <= 0 || a.d_state <= 0 ||
-      a.head_dim <= 0) {
-    return fail(M3_EINVAL, "m3_chunk_state: invalid dimensions");
-  }
-  if (!valid_dtype(a.act_dtype)) return fail(M3_EINVAL, "m3_chunk_state: invalid act_dtype");
-  if (a.d_state * a.head_dim > kThreads * kCsMaxE) {
-    return fail(M3_EUNSUPPORTED, "m3_chunk_state: d_state x head_dim > %d", kThreads * kCsMaxE);
-  }
-  const size_t lds = sizeof(float) * kCsRows * (a.d_state + a.head_dim);
-  if (lds > 64 * 1024) return fail(M3_EUNSUPPORTED, "m3_chunk_state: d_state + head_dim too large");
-  const int act = a.act_dtype, N = a.d_state, P = a.head_dim;
-  int rc;
-  if ((rc = check_tensor(a.k, "k", 5, N, true, act)) ||
-      (rc = check_tensor(a.value, "value", 5, P, true, act)) ||
-      (rc = check_tensor(a.cumulative, "cumulative", 3, 1, true, M3_F32)) ||
-      (rc = check_tensor(a.scale, "scale", 3, 1, true, M3_F32)) ||
-      (rc = check_tensor(a.state_in, "state_in", 4, N, true, M3_F32)) ||
-      (rc = check_tensor(a.state_out, "state_out", 4, N, true, M3_F32))) {
-    return rc;
-  }
-  if (a.batch == 0) return M3_OK;
-  const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kThreads);
-  switch (act) {
-    case M3_F32: hipLaunchKernelGGL(chunk_state_kernel<float>, grid, block, lds, stream, a); break;
-    case M3_BF16: hipLaunchKernelGGL(chunk_state_kernel<__bf16>, grid, block, lds, stream, a); break;
-    default: hipLaunchKernelGGL(chunk_state_kernel<_Float16>, grid, block, lds, stream, a); break;
-  }
-  return check_launch("m3_chunk_state");
 }

@@ -183,6 +183,7 @@ def mamba3_scan(q, k, value, gate, adt, dt, trap_logits, D, *, mimo_x=None, mimo
     args.out = _hip.tensor(out)
     args.final_state = _hip.tensor(final_state)
     with torch.cuda.device(device):
+        keep.append(_hip.scan_workspace(args, device))
         _hip.call("m3_scan_fwd", args, device)
     _HIP_LAST_SCAN_DISPATCH = True
     return out, final_state
@@ -401,6 +402,7 @@ def scan_projection(proj: torch.Tensor, mixer, *, cache=None, want_cache: bool =
     args.final_phase = _hip.tensor(final_phase)
     args.final_k = _hip.tensor(final_k)
     with torch.cuda.device(device):
+        keep.append(_hip.scan_workspace(args, device))
         _hip.call("m3_scan_fwd", args, device)
     _HIP_LAST_SCAN_DISPATCH = True
     return out, final_state, final_phase, final_k
