@@ -75,6 +75,7 @@ template <> struct Mma<_Float16> {
 };
 template <> struct Mma<float> {
   static constexpr int ROWS = 32, PAD = 4;
+  typedef float v8;  // unused: FP32 operands are single elements
   typedef f4 v4;
   typedef f32x2 v2;
   static __device__ __forceinline__ f4 mma(float a, float b, f4 c) {
@@ -101,12 +102,16 @@ template <typename T> struct Layout {
   static constexpr int ZT = al(VS + kPPad * LR * ES);
   static constexpr int SB = al(ZT + kPPad * LR * ES);
   static constexpr int FB = al(SB + kPPad * LQ * ES);
-  // float scratch, offsets in floats from FB
-  static constexpr int CUM = 0, ECUM = 64, SCL = 128, GAM = 192, VSF = 256, DTV = 320;
-  static constexpr int CS = 384, SN = CS + kTokMax * kSMax, PBASE = SN + kTokMax * kSMax;
+  // float scratch, offsets in floats from FB. Per-token scalars of one sub-chunk (token-indexed,
+  // kTokMax each) form a block; two blocks alternate between consecutive sub-chunks.
+  static constexpr int DTV = 0, CUM = 64, ECUM = 128, SCL = 192, GAM = 256, VSF = 320;
+  static constexpr int BSC = 384, CEND = 448, ECL = 452, SCB = 464;  // SCB: block size
+  static constexpr int SC0 = 0, SC1 = SCB;
+  static constexpr int CSS = kSMax + 1;  // token stride of the cos / sin tables (bank spread)
+  static constexpr int CS = 2 * SCB, SN = CS + kTokMax * CSS, PBASE = SN + kTokMax * CSS;
   static constexpr int POFF = PBASE + kSMax, MX = POFF + kSMax, MZ = MX + kRMax * kPPad;
-  static constexpr int MO = MZ + kRMax * kPPad, ECL = MO + kRMax * kPPad;
-  static constexpr int BYTES = FB + 4 * (ECL + 4);
+  static constexpr int MO = MZ + kRMax * kPPad;
+  static constexpr int BYTES = FB + 4 * (MO + kRMax * kPPad);
 };
 
 // Per-launch values shared by host and device.
@@ -124,14 +129,6 @@ __device__ __forceinline__ f4 zero4() {
 
 __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-__device__ __forceinline__ float wave_incl_scan(float v, int lane) {
-  for (int o = 1; o < 64; o <<= 1) {
-    const float u = __shfl_up(v, o);
-    if (lane >= o) v += u;
-  }
   return v;
 }
 
@@ -216,6 +213,19 @@ __device__ __forceinline__ void st_pair(T* dst, float a, float b) {
   *reinterpret_cast<typename Mma<T>::v2*>(dst) = v;
 }
 
+// Four adjacent activation values stored with one LDS write.
+template <typename T>
+__device__ __forceinline__ void st_quad(T* dst, f4 x) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<f4*>(dst) = x;
+  } else {
+    typename Mma<T>::v4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = from_f<T>(x[i]);
+    *reinterpret_cast<typename Mma<T>::v4*>(dst) = v;
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ void st_row8(T* dst, const float* x) {
   if constexpr (sizeof(T) == 4) {
@@ -277,19 +287,77 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
 
 // ------------------------------------------------------------------ scan
 
-template <typename T, int R>
+// Wave-level scans with DPP row shifts (no LDS traffic). row_shr:n = 0x110 + n; lanes whose
+// source lies before their 16-lane row read 0.
+template <int CTRL>
+__device__ __forceinline__ float dpp_shr(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                               CTRL, 0xf, 0xf, true));
+}
+
+// Inclusive scan within aligned segments of SEG lanes (SEG a power of 2, <= 16).
+template <int SEG>
+__device__ __forceinline__ float seg_incl_scan(float x, int lane) {
+  const int j = lane & (SEG - 1);
+  if constexpr (SEG > 1) { const float u = dpp_shr<0x111>(x); x += j >= 1 ? u : 0.f; }
+  if constexpr (SEG > 2) { const float u = dpp_shr<0x112>(x); x += j >= 2 ? u : 0.f; }
+  if constexpr (SEG > 4) { const float u = dpp_shr<0x114>(x); x += j >= 4 ? u : 0.f; }
+  if constexpr (SEG > 8) { const float u = dpp_shr<0x118>(x); x += j >= 8 ? u : 0.f; }
+  return x;
+}
+
+__device__ __forceinline__ float readlane_f(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
+// Inclusive scan over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_incl_scan(float x, int lane) {
+  x = seg_incl_scan<16>(x, lane);
+  const float r0 = readlane_f(x, 15), r1 = readlane_f(x, 31), r2 = readlane_f(x, 47);
+  const int row = lane >> 4;
+  x += row >= 1 ? r0 : 0.f;
+  x += row >= 2 ? r1 : 0.f;
+  x += row >= 3 ? r2 : 0.f;
+  return x;
+}
+
+// Transposed operand tiles ([n or p][row]) XOR-swizzle their 8-row groups by a per-row-of-
+// the-tile key so that the column-wise stores of the prologue spread over the LDS banks;
+// every reader applies the same swizzle. Groups of 8 (16-bit: 16 bytes) stay contiguous.
+template <int ROWS>
+__device__ __forceinline__ int swz(int row, int key) {
+  return row ^ (8 * (key & (ROWS / 8 - 1)));
+}
+
+template <typename T, int R, bool FULL>
 __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, const ScanGeom g,
                                                         const float* __restrict__ prep) {
   using M = Mma<T>;
+  using Lay = Layout<T>;
   constexpr int ROWS = M::ROWS;
   constexpr int RT = ROWS / 16;        // 16-row tiles per sub-chunk
   constexpr int WPR = kWaves / RT;     // waves sharing one query row tile
+  constexpr int TOK = ROWS / R;        // tokens per sub-chunk
+  constexpr int TPT = 16 / R;          // tokens per 16-row tile
+  constexpr int PG = TOK / 4;          // phase lanes per angle (4 tokens each)
   constexpr bool F32 = sizeof(T) == 4;
-  const int H = a.heads, L = a.length, N = a.d_state, P = a.head_dim, S = a.num_angles;
+  constexpr int LQ = Lay::LQ, LR = Lay::LR, NP = kNPad, CSS = Lay::CSS;
+  // FULL: the model's shape (N = 128, P = 64, S = 32) in projection form with vector loads
+  const int N = FULL ? kNPad : a.d_state;
+  const int P = FULL ? kPPad : a.head_dim;
+  const int S = FULL ? kSMax : a.num_angles;
+  const bool norm = FULL || g.prep_q >= 0;
+  const bool bias = FULL || a.q_bias.ptr != nullptr;
+  const bool rotate = FULL || a.phase_mode != M3_PHASE_NONE;
+  const bool angles = FULL || a.phase_mode == M3_PHASE_ANGLES;
+  const bool raw_dt = FULL || a.raw_dt != 0;
+  const bool mimo_rot = FULL ? (R > 1) : (a.mimo_rotation != 0);
+  const bool vec_qk = FULL || g.vec_qk, vec_vz = FULL || g.vec_vz;
+  const int H = a.heads, L = a.length;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
 
-  // ---- block -> (b, h): with xcd_map, the blocks of one XCD (blockIdx % 8) take consecutive
+  // ---- block -> (b, h): with xcd_map the blocks of one XCD (blockIdx % 8) take consecutive
   // (b, h), so the heads of one batch row share that XCD's L2 for q, k and the angles.
   int bid = blockIdx.x;
   if (g.xcd_map) {
@@ -300,7 +368,6 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   const int grp = h / (H / a.groups);
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  using Lay = Layout<T>;
   T* Qs = lds_t<T>(smem, Lay::QS);
   T* Ks = lds_t<T>(smem, Lay::KS);
   T* KT = lds_t<T>(smem, Lay::KT);
@@ -309,13 +376,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   T* ZT = lds_t<T>(smem, Lay::ZT);
   T* Sb = lds_t<T>(smem, Lay::SB);
   float* F = lds_t<float>(smem, Lay::FB);
-  constexpr int LQ = Lay::LQ, LR = Lay::LR, NP = kNPad, TOK = ROWS / R;
   const int PW = g.prep_w;
-
-  const bool norm = g.prep_q >= 0;
-  const bool bias = a.q_bias.ptr != nullptr;
-  const bool rotate = a.phase_mode != M3_PHASE_NONE;
-  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
   const float Dh = ldx(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
 
   // ---- lane roles
@@ -324,19 +385,16 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   const bool qk_on = rp < ROWS / 2 && n0 < N;
   const int qk_n = min(8, N - n0);
   // v / z: token pair vp (tokens 2vp, 2vp+1), columns p0 .. p0+3
-  constexpr int p4 = kPPad >> 2;
-  const int vp = tid / p4, p0 = 4 * (tid - vp * p4);
+  constexpr int P4 = kPPad / 4;
+  const int vp = tid / P4, p0 = 4 * (tid % P4);
   const bool vz_on = 2 * vp < TOK && p0 < P;
   const int vz_n = min(4, P - p0);
   // phase: angle ps, token group pg (tokens 4pg .. 4pg+3)
-  const int PG = TOK >> 2;
   const int pg = tid % PG, ps = tid / PG;
   const bool ph_on = rotate && ps < S;
 
   // ---- one-time LDS setup: zero the operand regions (padding), MIMO parameters, phase carry
-  for (int i = tid; i < Lay::FB / 4; i += kThreads) {
-    reinterpret_cast<uint32_t*>(smem)[i] = 0u;
-  }
+  for (int i = tid; i < Lay::FB / 4; i += kThreads) reinterpret_cast<uint32_t*>(smem)[i] = 0u;
   for (int i = tid; i < R * P; i += kThreads) {
     const int r = i / P, p = i - r * P;
     const int o = r * kPPad + p;
@@ -356,10 +414,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   for (int s = tid; s < S; s += kThreads) {
     F[Lay::PBASE + s] = 0.f;
     F[Lay::POFF + s] = a.initial_phase.ptr != nullptr
-                         ? static_cast<const float*>(a.initial_phase.ptr)
-                               [b * a.initial_phase.stride[0] + h * a.initial_phase.stride[1] +
-                                s * a.initial_phase.stride[2]]
-                         : 0.f;
+                           ? static_cast<const float*>(a.initial_phase.ptr)
+                                 [b * a.initial_phase.stride[0] + h * a.initial_phase.stride[1] +
+                                  s * a.initial_phase.stride[2]]
+                           : 0.f;
   }
 
   // per-lane constants of the q / k role: rounded norm weights and the biases of its rows
@@ -411,9 +469,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // Endpoint continuation (ops.py:681-686): S += dt_0 (1 - trap_0) sum_r (v_prev mx_r) k_prev_r.
   if (a.initial_k.ptr != nullptr && L > 0) {
     float dt0, adt0;
-    dt_adt(a.raw_dt, ldx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + h * a.dt.stride[2]),
+    dt_adt(raw_dt, ldx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + h * a.dt.stride[2]),
            ldx(a.a.ptr, a.a.dtype, b * a.a.stride[0] + h * a.a.stride[2]),
-           a.raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]) : 0.f, dt0,
+           raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]) : 0.f, dt0,
            adt0);
     const float tr0 = sigmoidf(ldx(a.trap.ptr, a.trap.dtype,
                                    b * a.trap.stride[0] + h * a.trap.stride[2]));
@@ -464,15 +522,15 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   const void* tr_row = offx(a.trap.ptr, tr_d, b * a.trap.stride[0] + h * a.trap.stride[2]);
   const int dt_t = static_cast<int>(a.dt.stride[1]), aa_t = static_cast<int>(a.a.stride[1]);
   const int tr_t = static_cast<int>(a.trap.stride[1]);
-  const bool raw_dt = a.raw_dt != 0, mimo_rot = a.mimo_rotation != 0;
   const float dt_bias = raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0])
                                : 0.f;
   const float* prep_row = prep + static_cast<int64_t>(b) * L * PW;
-  const float* ph_row = a.phase_mode == M3_PHASE_GIVEN
+  const float* ph_row = (!FULL && a.phase_mode == M3_PHASE_GIVEN)
                             ? static_cast<const float*>(a.phase.ptr) + b * a.phase.stride[0] +
                                   h * a.phase.stride[2] + ps * a.phase.stride[3]
                             : nullptr;
-  const int ph_t = a.phase_mode == M3_PHASE_GIVEN ? static_cast<int>(a.phase.stride[1]) : 0;
+  const int ph_t = (!FULL && a.phase_mode == M3_PHASE_GIVEN) ? static_cast<int>(a.phase.stride[1])
+                                                             : 0;
   float* fph = a.final_phase.ptr != nullptr
                    ? static_cast<float*>(a.final_phase.ptr) + b * a.final_phase.stride[0] +
                          h * a.final_phase.stride[1] + ps * a.final_phase.stride[2]
@@ -489,323 +547,303 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 
   __syncthreads();
   const int nsub = (L + TOK - 1) / TOK;
-  // c = -1 only loads sub-chunk 0; iteration c consumes the registers loaded for it, issues the
-  // loads of sub-chunk c + 1, then computes c while those loads are in flight.
+  // Iteration c consumes the registers loaded for sub-chunk c, issues the loads of c + 1, then
+  // computes c while they are in flight; at its end wave 0 turns the per-token scalars of c + 1
+  // into the other half of the double-buffered scalar block. c = -1 only primes sub-chunk 0.
   for (int c = -1; c < nsub; ++c) {
-   const int t0 = c * TOK;
-   const int width = min(TOK, L - t0);
-   if (c >= 0) {
-    // (1) per-token scalars, wave 0, lane = token
-    if (w == 0) {
-      const bool tv = lane < width;
-      const int tg = t0 + lane;
-      float dt = 0.f, adt = 0.f, tr = 0.f;
-      if (tv) {
-        dt_adt(raw_dt, sdt, sa, dt_bias, dt, adt);
-        tr = sigmoidf(str);
-      }
-      float right = __shfl_down(dt * (1.f - tr), 1);
-      if (lane == TOK - 1) {
-        right = 0.f;
-        if (t0 + TOK < L) {
-          float dtn, adtn;
-          dt_adt(raw_dt, ldt, 0.f, dt_bias, dtn, adtn);
-          right = dtn * (1.f - sigmoidf(ltr));
-        }
-      }
-      if (!(tg + 1 < L) || lane >= TOK) right = 0.f;
-      const float gamma = dt * tr;
-      const float scale = gamma + right;
-      const float cum = wave_incl_scan(tv ? adt : 0.f, lane);
-      const float cum_last = __shfl(cum, width - 1);
-      F[Lay::CUM + lane] = tv ? cum : cum_last;
-      F[Lay::ECUM + lane] = tv ? __expf(cum) : 0.f;
-      F[Lay::SCL + lane] = tv ? scale : 0.f;
-      F[Lay::GAM + lane] = tv ? gamma : 0.f;
-      F[Lay::VSF + lane] = tv ? scale * __expf(cum_last - cum) : 0.f;
-      F[Lay::DTV + lane] = tv ? dt : 0.f;
-      if (lane == 0) F[Lay::ECL] = __expf(cum_last);
-    }
-    __syncthreads();
-
-    // (2) phase of (token 4pg + i, angle ps) and its cos / sin
-    if (ph_on) {
-      float ph[4];
-      if (angles) {
-        float c[4];
-        float run = 0.f;
+    const int t0 = c * TOK;
+    const int width = min(TOK, L - t0);
+    const float* SC = F + ((c & 1) ? Lay::SC1 : Lay::SC0);
+    if (c >= 0) {
+      // (1) phase of (token 4pg + i, angle ps), its cos / sin
+      if (ph_on) {
+        float ph[4];
+        if (angles) {
+          float cpre[4];
+          float run = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tt = 4 * pg + i;
-          const float inc = tt < width ? m3_fmod_2pi(__fmul_rn(pa[i], F[Lay::DTV + tt])) : 0.f;
-          run = __fadd_rn(run, inc);
-          c[i] = run;
-        }
-        // exclusive scan of the group totals over the PG lanes of this angle
-        float incl = run;
-        for (int o = 1; o < PG; o <<= 1) {
-          const float u = __shfl_up(incl, o, PG);
-          if (pg >= o) incl = __fadd_rn(incl, u);
-        }
-        const float excl = __fsub_rn(incl, run);
-        float base = F[Lay::PBASE + ps], off = F[Lay::POFF + ps];
-        if ((t0 & 63) == 0 && t0 > 0) {
-          off = m3_fmod_2pi(__fadd_rn(off, base));
-          base = 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          ph[i] = m3_fmod_2pi(__fadd_rn(__fadd_rn(base, __fadd_rn(excl, c[i])), off));
-          const int tg = t0 + 4 * pg + i;
-          if (tg == L - 1 && fph != nullptr) *fph = ph[i];
-        }
-        if (pg == PG - 1) {
-          F[Lay::PBASE + ps] = __fadd_rn(base, incl);
-          F[Lay::POFF + ps] = off;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ph[i] = pa[i];
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tt = 4 * pg + i;
-        float sv, cv;
-        __sincosf(ph[i], &sv, &cv);
-        F[Lay::CS + tt * kSMax + ps] = cv;
-        F[Lay::SN + tt * kSMax + ps] = sv;
-      }
-    }
-    __syncthreads();
-
-    // (3) q / k rows -> Qs, Ks (row-major), KT (transposed); rows 2rp, 2rp+1
-    if (qk_on) {
-      float kt[2][8];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int row = 2 * rp + j, tt = row / R, r = row - tt * R;
-        const bool ok = tt < width;
-        float q[8], k[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          q[i] = fmaf(raw_get<T>(rq[j], i), fq[j] * wq[i], bq[R == 1 ? 0 : j][i]);
-          k[i] = fmaf(raw_get<T>(rk[j], i), fk[j] * wk[i], bk[R == 1 ? 0 : j][i]);
-          if (!ok) q[i] = k[i] = 0.f;
-        }
-        if (rotate && ok) {
-          if (!mimo_rot) {
-#pragma unroll
-            for (int i = 0; i < 8; i += 2) {
-              const int jn = (n0 + i) >> 1;
-              if (jn < S) {
-                const float cc = F[Lay::CS + tt * kSMax + jn], ss = F[Lay::SN + tt * kSMax + jn];
-                const float q0 = q[i], q1 = q[i + 1], k0 = k[i], k1 = k[i + 1];
-                q[i] = fmaf(q0, cc, -q1 * ss);
-                q[i + 1] = fmaf(q0, ss, q1 * cc);
-                k[i] = fmaf(k0, cc, -k1 * ss);
-                k[i + 1] = fmaf(k0, ss, k1 * cc);
-              }
-            }
-          } else {
-            // pairs (n, n + N/2) for n < S = N/4: the partner lives N/16 lanes away (N >= 16),
-            // or in this lane (N <= 8)
-            const int half = N >> 1;
-            float qp[8], kp[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              if (half >= 8) {
-                qp[i] = __shfl_xor(q[i], half >> 3, 16);
-                kp[i] = __shfl_xor(k[i], half >> 3, 16);
-              } else {
-                qp[i] = q[i ^ half];
-                kp[i] = k[i ^ half];
-              }
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const int n = n0 + i;
-              if (n < S) {  // first quarter: x cos - partner sin
-                const float cc = F[Lay::CS + tt * kSMax + n], ss = F[Lay::SN + tt * kSMax + n];
-                q[i] = fmaf(q[i], cc, -qp[i] * ss);
-                k[i] = fmaf(k[i], cc, -kp[i] * ss);
-              } else if (n >= 2 * S && n < 3 * S) {  // third quarter: partner sin + x cos
-                const float cc = F[Lay::CS + tt * kSMax + n - 2 * S], ss = F[Lay::SN + tt * kSMax + n - 2 * S];
-                q[i] = fmaf(qp[i], ss, q[i] * cc);
-                k[i] = fmaf(kp[i], ss, k[i] * cc);
-              }
-            }
+          for (int i = 0; i < 4; ++i) {
+            const int tt = 4 * pg + i;
+            const float inc = tt < width ? m3_fmod_2pi(__fmul_rn(pa[i], SC[Lay::DTV + tt])) : 0.f;
+            run = __fadd_rn(run, inc);
+            cpre[i] = run;
           }
-        }
-        st_row8<T>(Qs + row * LQ + n0, q);
-        st_row8<T>(Ks + row * LQ + n0, k);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (n0 + i < N) st_pair<T>(KT + (n0 + i) * LR + 2 * rp, kt[0][i], kt[1][i]);
-      }
-    }
-    // (4) value / gate -> VT, VsT, ZT (transposed), tokens 2vp, 2vp+1, columns p0 .. p0+3
-    if (vz_on) {
-      float v[2][4], z[2][4];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[j][i] = raw_get<T>(rv[j], i);
-          z[j][i] = raw_get<T>(rz[j], i);
-        }
-      }
-      const float f0 = F[Lay::VSF + 2 * vp], f1 = F[Lay::VSF + 2 * vp + 1];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = p0 + i;
-        if (p >= P) continue;
-        if (R == 1) {
-          const int row = 2 * vp;
-          st_pair<T>(VT + p * LR + row, v[0][i], v[1][i]);
-          st_pair<T>(VsT + p * LR + row, v[0][i] * f0, v[1][i] * f1);
-          st_pair<T>(ZT + p * LR + row, z[0][i], z[1][i]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const float fj = j ? f1 : f0;
-#pragma unroll
-            for (int r = 0; r < R; r += 2) {
-              const int row = (2 * vp + j) * R + r;
-              const float va = mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p]);
-              const float vb = mul_r<T>(v[j][i], F[Lay::MX + (r + 1) * kPPad + p]);
-              st_pair<T>(VT + p * LR + row, va, vb);
-              st_pair<T>(VsT + p * LR + row, va * fj, vb * fj);
-              st_pair<T>(ZT + p * LR + row, mul_r<T>(z[j][i], F[Lay::MZ + r * kPPad + p]),
-                         mul_r<T>(z[j][i], F[Lay::MZ + (r + 1) * kPPad + p]));
-            }
-          }
-        }
-      }
-    }
-    // (5) the state at the start of this sub-chunk, rounded to the activation dtype -> Sb[p][n]
-#pragma unroll
-    for (int k = 0; k < kTiles; ++k) {
-      const int u = w + kWaves * k;
-      if (u < n_tiles) {
-        const int ni = u / kPT, pj = u - ni * kPT;
-        T* dst = Sb + (16 * pj + l16) * LQ + 16 * ni + 4 * lg;
-        st_pair<T>(dst, st[k][0], st[k][1]);
-        st_pair<T>(dst + 2, st[k][2], st[k][3]);
-      }
-    }
-    __syncthreads();
-
-   }  // c >= 0 (stages 1-5)
-
-   // ---- loads of sub-chunk c + 1 into registers; they fly while sub-chunk c computes
-   if (c + 1 < nsub) {
-    const int n0t = t0 + TOK;  // first token of sub-chunk c + 1
-    const int nw = min(TOK, L - n0t);
-    if (qk_on) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int row = 2 * rp + j, tt = row / R, r = row - tt * R;
-        const bool ok = tt < nw;
-        const int64_t tg = n0t + tt;
-        load_words<T, 8>(rq[j], q_row + tg * q_t + r * q_r, ok ? qk_n : 0, g.vec_qk);
-        load_words<T, 8>(rk[j], k_row + tg * k_t + r * k_r, ok ? qk_n : 0, g.vec_qk);
-        if (norm && ok) {
-          const float* pr = prep_row + tg * PW;
-          fq[j] = pr[g.prep_q + grp * R + r];
-          fk[j] = pr[g.prep_k + grp * R + r];
-        }
-      }
-    }
-    if (vz_on) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int tt = 2 * vp + j;
-        const bool ok = tt < nw;
-        const int64_t tg = n0t + tt;
-        load_words<T, 4>(rv[j], v_row + tg * v_t, ok ? vz_n : 0, g.vec_vz);
-        load_words<T, 4>(rz[j], z_row + tg * z_t, ok ? vz_n : 0, g.vec_vz);
-      }
-    }
-    if (w == 0) {
-      const int64_t tg = n0t + lane;
-      sdt = sa = str = ldt = ltr = 0.f;
-      if (lane < nw) {
-        sdt = ldx(dt_row, dt_d, tg * dt_t);
-        sa = ldx(aa_row, aa_d, tg * aa_t);
-        str = ldx(tr_row, tr_d, tg * tr_t);
-      }
-      const int64_t tn = n0t + TOK;
-      if (lane == TOK - 1 && tn < L) {
-        ldt = ldx(dt_row, dt_d, tn * dt_t);
-        ltr = ldx(tr_row, tr_d, tn * tr_t);
-      }
-    }
-    if (ph_on) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tt = 4 * pg + i;
-        const int64_t tg = n0t + tt;
-        pa[i] = 0.f;
-        if (tt < nw) {
-          pa[i] = angles ? prep_row[tg * PW + g.prep_a + ps] : ph_row[tg * ph_t];
-        }
-      }
-    }
-   }
-
-   if (c >= 0) {
-
-    // (6) outputs for query row tile `it` and P tiles pj = wp, wp + WPR, ...
-    {
-      const int it = w / WPR, wp = w - it * WPR;
-      const int trow = 16 * it + l16;
-      const int tq = trow / R;
-      const float cum_t = F[Lay::CUM + tq];
-      const float gam_t = F[Lay::GAM + tq];
-      f4 wsc[RT];
-      if constexpr (!F32) {
-        // the query rows of this tile: B operand of the scores, A operand of the inter term
-        typename M::v8 qv[4];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          if (32 * kk < NP) qv[kk] = *reinterpret_cast<const typename M::v8*>(
-                                    Qs + trow * LQ + 32 * kk + 8 * lg);
-        }
-#pragma unroll
-        for (int sj = 0; sj < RT; ++sj) {
-          wsc[sj] = zero4();
-          if (sj > it) continue;
-          f4 acc = zero4();
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) {
-            if (32 * kk < NP) {
-              const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
-                  Ks + (16 * sj + l16) * LQ + 32 * kk + 8 * lg);
-              acc = M::mma(av, qv[kk], acc);
-            }
+          const float incl = seg_incl_scan<PG>(run, lane);
+          const float excl = __fsub_rn(incl, run);
+          float base = F[Lay::PBASE + ps], off = F[Lay::POFF + ps];
+          if ((t0 & 63) == 0 && t0 > 0) {
+            off = m3_fmod_2pi(__fadd_rn(off, base));
+            base = 0.f;
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int ts = (16 * sj + 4 * lg + i) / R;
-            const float d = tq > ts ? F[Lay::SCL + ts] * __expf(cum_t - F[Lay::CUM + ts])
-                                    : (tq == ts ? gam_t : 0.f);
-            wsc[sj][i] = rnd<T>(acc[i] * d);
+            ph[i] = m3_fmod_2pi(__fadd_rn(__fadd_rn(base, __fadd_rn(excl, cpre[i])), off));
+            if (t0 + 4 * pg + i == L - 1 && fph != nullptr) *fph = ph[i];
+          }
+          if (pg == PG - 1) {
+            F[Lay::PBASE + ps] = __fadd_rn(base, incl);
+            F[Lay::POFF + ps] = off;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ph[i] = pa[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tt = 4 * pg + i;
+          float sv, cv;
+          __sincosf(ph[i], &sv, &cv);
+          F[Lay::CS + tt * CSS + ps] = cv;
+          F[Lay::SN + tt * CSS + ps] = sv;
+        }
+      }
+      __syncthreads();
+
+      // (2) q / k rows -> Qs, Ks (row-major), KT (transposed); rows 2rp, 2rp+1
+      if (qk_on) {
+        float kt[2][8];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int row = 2 * rp + j, tt = row / R;
+          const bool ok = tt < width;
+          float q[8], k[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            q[i] = ok ? fmaf(raw_get<T>(rq[j], i), fq[j] * wq[i], bq[R == 1 ? 0 : j][i]) : 0.f;
+            k[i] = ok ? fmaf(raw_get<T>(rk[j], i), fk[j] * wk[i], bk[R == 1 ? 0 : j][i]) : 0.f;
+          }
+          if (rotate && ok) {
+            if (!mimo_rot) {
+#pragma unroll
+              for (int i = 0; i < 8; i += 2) {
+                const int jn = (n0 + i) >> 1;
+                if (jn < S) {
+                  const float cc = F[Lay::CS + tt * CSS + jn], ss = F[Lay::SN + tt * CSS + jn];
+                  const float q0 = q[i], q1 = q[i + 1], k0 = k[i], k1 = k[i + 1];
+                  q[i] = fmaf(q0, cc, -q1 * ss);
+                  q[i + 1] = fmaf(q0, ss, q1 * cc);
+                  k[i] = fmaf(k0, cc, -k1 * ss);
+                  k[i + 1] = fmaf(k0, ss, k1 * cc);
+                }
+              }
+            } else {
+              // pairs (n, n + N/2) for n < S = N/4: the partner lives N/16 lanes away (N >= 16),
+              // or in this lane (N <= 8)
+              const int half = N >> 1;
+              float qp[8], kp[8];
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                if (half >= 8) {
+                  qp[i] = __shfl_xor(q[i], half >> 3, 16);
+                  kp[i] = __shfl_xor(k[i], half >> 3, 16);
+                } else {
+                  qp[i] = q[i ^ half];
+                  kp[i] = k[i ^ half];
+                }
+              }
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                const int n = n0 + i;
+                if (n < S) {  // first quarter: x cos - partner sin
+                  const float cc = F[Lay::CS + tt * CSS + n], ss = F[Lay::SN + tt * CSS + n];
+                  q[i] = fmaf(q[i], cc, -qp[i] * ss);
+                  k[i] = fmaf(k[i], cc, -kp[i] * ss);
+                } else if (n >= 2 * S && n < 3 * S) {  // third quarter: partner sin + x cos
+                  const float cc = F[Lay::CS + tt * CSS + n - 2 * S];
+                  const float ss = F[Lay::SN + tt * CSS + n - 2 * S];
+                  q[i] = fmaf(qp[i], ss, q[i] * cc);
+                  k[i] = fmaf(kp[i], ss, k[i] * cc);
+                }
+              }
+            }
+          }
+          st_row8<T>(Qs + row * LQ + n0, q);
+          st_row8<T>(Ks + row * LQ + n0, k);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int n = n0 + i;
+          if (n < N) st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> 3), kt[0][i], kt[1][i]);
+        }
+      }
+      // (3) value / gate -> VT, VsT, ZT (transposed, swizzled), tokens 2vp, 2vp+1
+      if (vz_on) {
+        float v[2][4], z[2][4];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[j][i] = raw_get<T>(rv[j], i);
+            z[j][i] = raw_get<T>(rz[j], i);
           }
         }
-        for (int pj = wp; pj < kPT; pj += WPR) {
-          const int pcol = 16 * pj + l16;
-          f4 yi = zero4(), ye = zero4();
+        const float f0 = SC[Lay::VSF + 2 * vp], f1 = SC[Lay::VSF + 2 * vp + 1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int p = p0 + i;
+          if (p >= P) continue;
+          const int key = p >> 2;
+          if (R == 1) {
+            const int row = swz<ROWS>(2 * vp, key);
+            st_pair<T>(VT + p * LR + row, v[0][i], v[1][i]);
+            st_pair<T>(VsT + p * LR + row, v[0][i] * f0, v[1][i] * f1);
+            st_pair<T>(ZT + p * LR + row, z[0][i], z[1][i]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const float fj = j ? f1 : f0;
+#pragma unroll
+              for (int r = 0; r < R; r += 2) {
+                const int row = swz<ROWS>((2 * vp + j) * R + r, key);
+                const float va = mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p]);
+                const float vb = mul_r<T>(v[j][i], F[Lay::MX + (r + 1) * kPPad + p]);
+                st_pair<T>(VT + p * LR + row, va, vb);
+                st_pair<T>(VsT + p * LR + row, va * fj, vb * fj);
+                st_pair<T>(ZT + p * LR + row, mul_r<T>(z[j][i], F[Lay::MZ + r * kPPad + p]),
+                           mul_r<T>(z[j][i], F[Lay::MZ + (r + 1) * kPPad + p]));
+              }
+            }
+          }
+        }
+      }
+      // (4) the state at the start of this sub-chunk, rounded to the activation dtype -> Sb[p][n]
+#pragma unroll
+      for (int k = 0; k < kTiles; ++k) {
+        const int u = w + kWaves * k;
+        if (u < n_tiles) {
+          const int ni = u / kPT, pj = u - ni * kPT;
+          st_quad<T>(Sb + (16 * pj + l16) * LQ + 16 * ni + 4 * lg, st[k]);
+        }
+      }
+      __syncthreads();
+    }  // c >= 0 (stages 1-4)
+
+    // ---- loads of sub-chunk c + 1 into registers; they fly while sub-chunk c computes
+    if (c + 1 < nsub) {
+      const int n0t = t0 + TOK;  // first token of sub-chunk c + 1
+      const int nw = min(TOK, L - n0t);
+      if (qk_on) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int row = 2 * rp + j, tt = row / R, r = row - tt * R;
+          const bool ok = tt < nw;
+          const int tg = n0t + tt;
+          load_words<T, 8>(rq[j], q_row + tg * q_t + r * q_r, ok ? qk_n : 0, vec_qk);
+          load_words<T, 8>(rk[j], k_row + tg * k_t + r * k_r, ok ? qk_n : 0, vec_qk);
+          if (norm && ok) {
+            const float* pr = prep_row + tg * PW;
+            fq[j] = pr[g.prep_q + grp * R + r];
+            fk[j] = pr[g.prep_k + grp * R + r];
+          }
+        }
+      }
+      if (vz_on) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int tt = 2 * vp + j;
+          const bool ok = tt < nw;
+          const int tg = n0t + tt;
+          load_words<T, 4>(rv[j], v_row + tg * v_t, ok ? vz_n : 0, vec_vz);
+          load_words<T, 4>(rz[j], z_row + tg * z_t, ok ? vz_n : 0, vec_vz);
+        }
+      }
+      if (w == 0) {
+        const int tg = n0t + lane;
+        sdt = sa = str = ldt = ltr = 0.f;
+        if (lane < nw) {
+          sdt = ldx(dt_row, dt_d, tg * dt_t);
+          sa = ldx(aa_row, aa_d, tg * aa_t);
+          str = ldx(tr_row, tr_d, tg * tr_t);
+        }
+        const int tn = n0t + TOK;
+        if (lane == TOK - 1 && tn < L) {
+          ldt = ldx(dt_row, dt_d, tn * dt_t);
+          ltr = ldx(tr_row, tr_d, tn * tr_t);
+        }
+      }
+      if (ph_on) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tt = 4 * pg + i;
+          const int tg = n0t + tt;
+          pa[i] = 0.f;
+          if (tt < nw) pa[i] = angles ? prep_row[tg * PW + g.prep_a + ps] : ph_row[tg * ph_t];
+        }
+      }
+    }
+
+    if (c >= 0) {
+      // (5) outputs for query row tile `it` and P tiles pj = wp, wp + WPR, ...
+      const int it = w / WPR, wp = w - it * WPR;
+      const int trow = 16 * it + l16;
+      const int tq = trow / R;
+      const float cum_t = SC[Lay::CUM + tq];
+      const float gam_t = SC[Lay::GAM + tq];
+      // decayed scores W[t, s] = Sc[t, s] * d[t, s] in FP32 (D-layout: rows s, column t)
+      // 16-bit: the query rows of this tile, B operand of the scores and A operand of inter
+      typename M::v8 qv[F32 ? 1 : NP / 32];
+      if constexpr (!F32) {
+#pragma unroll
+        for (int kk = 0; kk < NP / 32; ++kk) {
+          qv[kk] = *reinterpret_cast<const typename M::v8*>(Qs + trow * LQ + 32 * kk + 8 * lg);
+        }
+      }
+      f4 wsc[RT];
+#pragma unroll
+      for (int sj = 0; sj < RT; ++sj) {
+        wsc[sj] = zero4();
+        if (sj > it) continue;
+        f4 acc = zero4();
+        if constexpr (!F32) {
+#pragma unroll
+          for (int kk = 0; kk < NP / 32; ++kk) {
+            const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
+                Ks + (16 * sj + l16) * LQ + 32 * kk + 8 * lg);
+            acc = M::mma(av, qv[kk], acc);
+          }
+        } else {
+#pragma unroll 8
+          for (int kk = 0; kk < NP; kk += 4) {
+            acc = M::mma(Ks[(16 * sj + l16) * LQ + kk + lg], Qs[trow * LQ + kk + lg], acc);
+          }
+        }
+        if (sj < it) {
+          // strictly earlier tile: d = exp(cum_t - cend) * (scale_s exp(cend - cum_s)), both <= 1
+          const float at = __expf(cum_t - SC[Lay::CEND + sj]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int ts = (16 * sj + 4 * lg + i) / R;
+            wsc[sj][i] = acc[i] * (at * SC[Lay::BSC + ts]);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int ts = (16 * sj + 4 * lg + i) / R;
+            const float d = tq > ts ? SC[Lay::SCL + ts] * __expf(cum_t - SC[Lay::CUM + ts])
+                                    : (tq == ts ? gam_t : 0.f);
+            wsc[sj][i] = acc[i] * d;
+          }
+        }
+      }
+      float ecum[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ecum[i] = SC[Lay::ECUM + (16 * it + 4 * lg + i) / R];
+      for (int pj = wp; pj < kPT; pj += WPR) {
+        const int pcol = 16 * pj + l16;
+        const int key = pcol >> 2;
+        f4 yi = zero4(), ye = zero4();
+        if constexpr (!F32) {
+          // intra: W V with the K axis permuted as the D-layout of wsc
 #pragma unroll
           for (int m = 0; m < (RT + 1) / 2; ++m) {
             if (2 * m > it) continue;
             typename M::v8 av, bv;
-            const typename M::v4 b0 =
-                *reinterpret_cast<const typename M::v4*>(VT + pcol * LR + 32 * m + 4 * lg);
-            const typename M::v4 b1 =
-                *reinterpret_cast<const typename M::v4*>(VT + pcol * LR + 32 * m + 16 + 4 * lg);
+            const typename M::v4 b0 = *reinterpret_cast<const typename M::v4*>(
+                VT + pcol * LR + swz<ROWS>(32 * m + 4 * lg, key));
+            const typename M::v4 b1 = *reinterpret_cast<const typename M::v4*>(
+                VT + pcol * LR + swz<ROWS>(32 * m + 16 + 4 * lg, key));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               av[i] = from_f<T>(wsc[2 * m][i]);
@@ -815,117 +853,125 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
             }
             yi = M::mma(av, bv, yi);
           }
+          // inter: Q rnd(S)^T
 #pragma unroll
-          for (int kk = 0; kk < 4; ++kk) {
-            if (32 * kk < NP) {
-              const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
-                  Sb + pcol * LQ + 32 * kk + 8 * lg);
-              ye = M::mma(qv[kk], bv, ye);
-            }
+          for (int kk = 0; kk < NP / 32; ++kk) {
+            const typename M::v8 bv =
+                *reinterpret_cast<const typename M::v8*>(Sb + pcol * LQ + 32 * kk + 8 * lg);
+            ye = M::mma(qv[kk], bv, ye);
           }
-          if (pcol < P) {
-            const typename M::v4 vv =
-                *reinterpret_cast<const typename M::v4*>(VT + pcol * LR + 16 * it + 4 * lg);
-            const typename M::v4 zz =
-                *reinterpret_cast<const typename M::v4*>(ZT + pcol * LR + 16 * it + 4 * lg);
-            float y = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int row = 16 * it + 4 * lg + i;
-              const int tt = row / R, r = row - tt * R;
-              const float zf = to_f(zz[i]);
-              float yr = (fmaf(ye[i], F[Lay::ECUM + tt], yi[i]) + Dh * to_f(vv[i])) *
-                         __fdividef(zf, 1.f + __expf(-zf));
-              if (R > 1) yr *= F[Lay::MO + r * kPPad + pcol];
-              y = (R > 1 && r > 0) ? y + yr : yr;
-              if (r == R - 1 && tt < width) {
-                out_row[(t0 + tt) * out_t + pcol] = from_f<T>(y);
-              }
-            }
-          }
-        }
-      } else {
-#pragma unroll
-        for (int sj = 0; sj < RT; ++sj) {
-          wsc[sj] = zero4();
-          if (sj > it) continue;
-          f4 acc = zero4();
-          for (int kk = 0; kk < NP; kk += 4) {
-            acc = M::mma(Ks[(16 * sj + l16) * LQ + kk + lg], Qs[trow * LQ + kk + lg], acc);
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int ts = (16 * sj + 4 * lg + i) / R;
-            const float d = tq > ts ? F[Lay::SCL + ts] * __expf(cum_t - F[Lay::CUM + ts])
-                                    : (tq == ts ? gam_t : 0.f);
-            wsc[sj][i] = acc[i] * d;
-          }
-        }
-        for (int pj = wp; pj < kPT; pj += WPR) {
-          const int pcol = 16 * pj + l16;
-          f4 yi = zero4(), ye = zero4();
+        } else {
 #pragma unroll
           for (int sj = 0; sj < RT; ++sj) {
             if (sj > it) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              yi = M::mma(wsc[sj][i], VT[pcol * LR + 16 * sj + 4 * lg + i], yi);
+              yi = M::mma(wsc[sj][i], VT[pcol * LR + swz<ROWS>(16 * sj + 4 * lg + i, key)], yi);
             }
           }
+#pragma unroll 8
           for (int kk = 0; kk < NP; kk += 4) {
             ye = M::mma(Qs[trow * LQ + kk + lg], Sb[pcol * LQ + kk + lg], ye);
           }
-          if (pcol < P) {
-            float y = 0.f;
+        }
+        // epilogue: rows 16 it + 4 lg + i, column pcol
+        if (pcol < P) {
+          float vv[4], zz[4];
+          if constexpr (!F32) {
+            const typename M::v4 v4 = *reinterpret_cast<const typename M::v4*>(
+                VT + pcol * LR + swz<ROWS>(16 * it + 4 * lg, key));
+            const typename M::v4 z4 = *reinterpret_cast<const typename M::v4*>(
+                ZT + pcol * LR + swz<ROWS>(16 * it + 4 * lg, key));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { vv[i] = to_f(v4[i]); zz[i] = to_f(z4[i]); }
+          } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int row = 16 * it + 4 * lg + i;
-              const int tt = row / R, r = row - tt * R;
-              const float zf = ZT[pcol * LR + row];
-              float yr = (fmaf(ye[i], F[Lay::ECUM + tt], yi[i]) + Dh * VT[pcol * LR + row]) *
-                         __fdividef(zf, 1.f + __expf(-zf));
-              if (R > 1) yr *= F[Lay::MO + r * kPPad + pcol];
-              y = (R > 1 && r > 0) ? y + yr : yr;
-              if (r == R - 1 && tt < width) {
-                out_row[(t0 + tt) * out_t + pcol] = y;
-              }
+              vv[i] = VT[pcol * LR + swz<ROWS>(16 * it + 4 * lg + i, key)];
+              zz[i] = ZT[pcol * LR + swz<ROWS>(16 * it + 4 * lg + i, key)];
             }
+          }
+          float y = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int row = 16 * it + 4 * lg + i;
+            const int tt = row / R, r = row - tt * R;
+            float yr = (fmaf(ye[i], ecum[i], yi[i]) + Dh * vv[i]) *
+                       __fdividef(zz[i], 1.f + __expf(-zz[i]));
+            if (R > 1) yr *= F[Lay::MO + r * kPPad + pcol];
+            y = (R > 1 && r > 0) ? y + yr : yr;
+            if (r == R - 1 && tt < width) out_row[(t0 + tt) * out_t + pcol] = from_f<T>(y);
           }
         }
       }
-    }
 
-    // (7) state carry: S^T = exp(cum_last) S^T + K^T Vs
-    {
-      const float ecl = F[Lay::ECL];
+      // (6) state carry: S^T = exp(cum_last) S^T + K^T Vs
+      const float ecl = SC[Lay::ECL];
 #pragma unroll
       for (int k = 0; k < kTiles; ++k) {
         const int u = w + kWaves * k;
         if (u >= n_tiles) continue;
         const int ni = u / kPT, pj = u - ni * kPT;
+        const int nrow = 16 * ni + l16, prow = 16 * pj + l16;
         f4 acc = zero4();
         if constexpr (!F32) {
 #pragma unroll
           for (int kk = 0; kk < ROWS; kk += 32) {
             const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
-                KT + (16 * ni + l16) * LR + kk + 8 * lg);
+                KT + nrow * LR + swz<ROWS>(kk + 8 * lg, nrow >> 3));
             const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
-                VsT + (16 * pj + l16) * LR + kk + 8 * lg);
+                VsT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> 2));
             acc = M::mma(av, bv, acc);
           }
         } else {
 #pragma unroll
           for (int kk = 0; kk < ROWS; kk += 4) {
-            acc = M::mma(KT[(16 * ni + l16) * LR + kk + lg], VsT[(16 * pj + l16) * LR + kk + lg],
-                         acc);
+            acc = M::mma(KT[nrow * LR + swz<ROWS>(kk + lg, nrow >> 3)],
+                         VsT[prow * LR + swz<ROWS>(kk + lg, prow >> 2)], acc);
           }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) st[k][i] = fmaf(ecl, st[k][i], acc[i]);
       }
+    }  // c >= 0 (stages 5-6)
+
+    // (7) wave 0: per-token scalars of sub-chunk c + 1 (lane = token) into the other buffer
+    if (w == 0 && c + 1 < nsub) {
+      const int tb = t0 + TOK, wn = min(TOK, L - tb);
+      float* SCn = F + (((c + 1) & 1) ? Lay::SC1 : Lay::SC0);
+      const bool tv = lane < wn;
+      float dt = 0.f, adt = 0.f, tr = 0.f;
+      if (tv) {
+        dt_adt(raw_dt, sdt, sa, dt_bias, dt, adt);
+        tr = sigmoidf(str);
+      }
+      float right = __shfl_down(dt * (1.f - tr), 1);
+      if (lane == TOK - 1) {
+        right = 0.f;
+        if (tb + TOK < L) {
+          float dtn, adtn;
+          dt_adt(raw_dt, ldt, 0.f, dt_bias, dtn, adtn);
+          right = dtn * (1.f - sigmoidf(ltr));
+        }
+      }
+      if (tb + lane + 1 >= L) right = 0.f;
+      const float gamma = dt * tr;
+      const float scale = gamma + right;
+      const float cum = wave_incl_scan(tv ? adt : 0.f, lane);
+      const float cum_last = __shfl(cum, wn - 1);
+      const float cv = tv ? cum : cum_last;
+      const float cend = __shfl(cv, min(lane | (TPT - 1), wn - 1));
+      SCn[Lay::DTV + lane] = tv ? dt : 0.f;
+      SCn[Lay::CUM + lane] = cv;
+      SCn[Lay::ECUM + lane] = tv ? __expf(cv) : 0.f;
+      SCn[Lay::SCL + lane] = tv ? scale : 0.f;
+      SCn[Lay::GAM + lane] = tv ? gamma : 0.f;
+      SCn[Lay::VSF + lane] = tv ? scale * __expf(cum_last - cv) : 0.f;
+      SCn[Lay::BSC + lane] = tv ? scale * __expf(cend - cv) : 0.f;
+      if (lane < TOK && (lane & (TPT - 1)) == 0) SCn[Lay::CEND + lane / TPT] = cend;
+      if (lane == 0) SCn[Lay::ECL] = __expf(cum_last);
     }
     __syncthreads();
-   }  // c >= 0 (stages 6-7)
   }
 
   // ---- final k: the biased, rotated k of token L-1, still in Ks from the last sub-chunk
@@ -993,6 +1039,33 @@ static size_t workspace_bytes(const m3_scan_args& a, int prep_w) {
   return static_cast<size_t>(a.batch) * a.length * prep_w * sizeof(float);
 }
 
+// The model's own shape in projection form: the specialization with every shape and mode a
+// compile-time constant.
+static bool full_shape(const m3_scan_args& a, const ScanGeom& g, int R) {
+  return a.d_state == kNPad && a.head_dim == kPPad && a.num_angles == kSMax &&
+         a.q_norm_w.ptr != nullptr && a.q_bias.ptr != nullptr && a.raw_dt != 0 &&
+         a.phase_mode == M3_PHASE_ANGLES && (a.mimo_rotation != 0) == (R > 1) && g.vec_qk &&
+         g.vec_vz;
+}
+
+template <typename T, int R, bool FULL>
+static int launch_kernel(const m3_scan_args& a, const ScanGeom& g, const float* prep, dim3 grid,
+                         dim3 block, hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel<T, R, FULL>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       Layout<T>::BYTES);
+    if (e != hipSuccess) {
+      return fail(M3_ELAUNCH, "m3_scan_fwd: hipFuncSetAttribute: %s", hipGetErrorString(e));
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((scan_kernel<T, R, FULL>), grid, block, Layout<T>::BYTES, stream, a, g,
+                     prep);
+  return check_launch("m3_scan_fwd");
+}
+
 template <typename T, int R>
 static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
   const ScanGeom g = make_geom<T>(a);
@@ -1014,18 +1087,9 @@ static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
       if (rc != M3_OK) return rc;
     }
   }
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel<T, R>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) {
-      return fail(M3_ELAUNCH, "m3_scan_fwd: hipFuncSetAttribute: %s", hipGetErrorString(e));
-    }
-    attr_set = true;
-  }
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kThreads);
-  hipLaunchKernelGGL((scan_kernel<T, R>), grid, block, Layout<T>::BYTES, stream, a, g, prep);
-  return check_launch("m3_scan_fwd");
+  if (full_shape(a, g, R)) return launch_kernel<T, R, true>(a, g, prep, grid, block, stream);
+  return launch_kernel<T, R, false>(a, g, prep, grid, block, stream);
 }
 
 template <typename T>
@@ -1100,6 +1164,19 @@ static int validate_scan(const m3_scan_args& a) {
   if ((a.q_norm_w.ptr == nullptr) != (a.k_norm_w.ptr == nullptr) ||
       (a.q_bias.ptr == nullptr) != (a.k_bias.ptr == nullptr)) {
     return fail(M3_EINVAL, "m3_scan_fwd: q/k norm weights and biases come in pairs");
+  }
+  // per-token offsets within one batch row are 32-bit in the kernel
+  const int64_t lim = INT32_MAX;
+  const m3_tensor* per_token[] = {&a.q, &a.k, &a.value, &a.gate, &a.dt, &a.a, &a.trap, &a.out};
+  for (const m3_tensor* t : per_token) {
+    if (static_cast<int64_t>(a.length) * (t->stride[1] < 0 ? -t->stride[1] : t->stride[1]) >=
+        lim) {
+      return fail(M3_EUNSUPPORTED, "m3_scan_fwd: a batch row exceeds 2^31 elements");
+    }
+  }
+  if (a.phase_mode != M3_PHASE_NONE &&
+      static_cast<int64_t>(a.length) * a.phase.stride[1] >= lim) {
+    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: a batch row of phase exceeds 2^31 elements");
   }
   if (a.final_phase.ptr != nullptr && !angles) {
     return fail(M3_EINVAL, "m3_scan_fwd: final_phase needs phase_mode ANGLES");
