@@ -38,6 +38,8 @@
 #include "m3_host.hpp"
 #include "m3_math.h"
 
+#include <algorithm>
+
 namespace m3 {
 
 constexpr int kThreads = 512;
@@ -103,12 +105,14 @@ template <typename T> struct Layout {
   static constexpr int SB = al(ZT + kPPad * LR * ES);
   static constexpr int FB = al(SB + kPPad * LQ * ES);
   // float scratch, offsets in floats from FB. Per-token scalars of one sub-chunk (token-indexed,
-  // kTokMax each) form a block; two blocks alternate between consecutive sub-chunks.
+  // kTokMax each) form a block of SCB floats; three blocks rotate over consecutive sub-chunks.
   static constexpr int DTV = 0, CUM = 64, ECUM = 128, SCL = 192, GAM = 256, VSF = 320;
-  static constexpr int BSC = 384, CEND = 448, ECL = 452, SCB = 464;  // SCB: block size
-  static constexpr int SC0 = 0, SC1 = SCB;
-  static constexpr int CSS = kSMax + 1;  // token stride of the cos / sin tables (bank spread)
-  static constexpr int CS = 2 * SCB, SN = CS + kTokMax * CSS, PBASE = SN + kTokMax * CSS;
+  static constexpr int BSC = 384, CEND = 448, ECL = 452, SCB = 464;
+  static constexpr int SC0 = 0;
+  // cos / sin tables of one sub-chunk ([token][angle], token stride CSS for bank spread; sin at
+  // SNO after cos), two of them alternating
+  static constexpr int CSS = kSMax + 1, SNO = kTokMax * CSS, CSB = 2 * SNO;
+  static constexpr int CS0 = SC0 + 3 * SCB, PBASE = CS0 + 2 * CSB;
   static constexpr int POFF = PBASE + kSMax, MX = POFF + kSMax, MZ = MX + kRMax * kPPad;
   static constexpr int MO = MZ + kRMax * kPPad;
   static constexpr int BYTES = FB + 4 * (MO + kRMax * kPPad);
@@ -119,6 +123,12 @@ struct ScanGeom {
   int xcd_map;           // 1: map blocks so each XCD holds consecutive (b, h)
   int vec_qk, vec_vz;    // 1: q/k rows and v/z rows may be loaded with 16 / 8-byte vectors
   int prep_w, prep_q, prep_k, prep_a;  // workspace floats per token and field offsets (-1: none)
+  // projection form (the full-shape kernel): q, k, value, gate, dt, a, trap are slices of one
+  // projection row; byte offsets of each slice from `proj`, the batch / token strides and the
+  // group / rank / head strides of the slices, in bytes
+  const char* proj;
+  int64_t proj_b, out_b;
+  int tok_b, o_q, o_k, o_v, o_z, o_dt, o_a, o_tr, qk_g, qk_r, vz_h, sc_h, out_t, out_h;
 };
 
 __device__ __forceinline__ f4 zero4() {
@@ -329,6 +339,348 @@ __device__ __forceinline__ int swz(int row, int key) {
   return row ^ (8 * (key & (ROWS / 8 - 1)));
 }
 
+// Buffer resource over `bytes` bytes from `base` (raw, stride 0): loads at offsets beyond the
+// extent return zero, stores there are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), bytes,
+                                           0x00020000);
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// NW raw words (NW in {2, 4, 8}) from a buffer at byte offset `off`.
+template <int NW>
+__device__ __forceinline__ void bload_words(uint32_t (&w)[NW], __amdgpu_buffer_rsrc_t r, int off) {
+  if constexpr (NW == 2) {
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+    w[0] = v[0];
+    w[1] = v[1];
+  } else {
+#pragma unroll
+    for (int j = 0; j < NW; j += 4) {
+      const u32x4 v =
+          __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 4 * j, 0, 0));
+      w[j] = v[0];
+      w[j + 1] = v[1];
+      w[j + 2] = v[2];
+      w[j + 3] = v[3];
+    }
+  }
+}
+
+__device__ __forceinline__ float bload_f32(__amdgpu_buffer_rsrc_t r, int off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// One activation element from a buffer, as FP32.
+template <typename T>
+__device__ __forceinline__ float bload_elem(__amdgpu_buffer_rsrc_t r, int off) {
+  if constexpr (sizeof(T) == 4) {
+    return bload_f32(r, off);
+  } else {
+    const uint32_t bits = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    return bits_to_f(bits, static_cast<T*>(nullptr));
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void bstore_elem(float x, __amdgpu_buffer_rsrc_t r, int off) {
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f<T>(x)), r, off, 0,
+                                          0);
+  }
+}
+
+// Per-token global reads of one (batch, head). FULL: every per-token input is a slice of one
+// projection row (host-checked), read at per-lane byte offsets through one buffer resource per
+// batch row whose extent ends at token L, so rows of tokens >= L read as zero without guards;
+// the per-token prep rows likewise. Otherwise element pointers with explicit guards.
+template <typename T, int R, bool FULL>
+struct Feed {
+  static constexpr int ES = sizeof(T), W8 = Words<T>::W8, W4 = Words<T>::W4;
+  // FULL
+  __amdgpu_buffer_rsrc_t rs_p, rs_w;
+  int o_qk, o_vz, o_sc, o_pw, o_pa;  // per-lane byte offsets at token 0
+  int d_q1, d_k, d_z, d_a, d_tr, d_w1, d_fk, tok_b, pw_b;  // uniform byte deltas
+  // generic
+  const T *q_row, *k_row, *v_row, *z_row;
+  const void *dt_row, *aa_row, *tr_row;
+  const float *prep_row, *ph_row;
+  int q_t, q_r, k_t, k_r, v_t, z_t, dt_t, aa_t, tr_t, ph_t, dt_d, aa_d, tr_d;
+  int pw, fq_o, fk_o, pa_o, qk_n, vz_n;
+  bool vec_qk, vec_vz, norm, angles;
+  // lane roles
+  int rp, vp, pg, ps;
+
+  __device__ __forceinline__ void init(const m3_scan_args& a, const ScanGeom& g,
+                                       const float* prep, int b, int h, int grp, int rp_,
+                                       int n0, int vp_, int p0, int pg_, int ps_, int lane,
+                                       int N, int P, bool norm_, bool angles_) {
+    const int L = a.length;
+    rp = rp_;
+    vp = vp_;
+    pg = pg_;
+    ps = ps_;
+    pw = g.prep_w;
+    norm = norm_;
+    angles = angles_;
+    const int tt0 = (2 * rp) / R, r0 = (2 * rp) % R;
+    if constexpr (FULL) {
+      tok_b = g.tok_b;
+      pw_b = pw * 4;
+      rs_p = make_rsrc(g.proj + b * g.proj_b, L * tok_b);
+      rs_w = make_rsrc(prep + static_cast<int64_t>(b) * L * pw, L * pw_b);
+      o_qk = g.o_q + grp * g.qk_g + r0 * g.qk_r + tt0 * tok_b + n0 * ES;
+      o_vz = g.o_v + h * g.vz_h + 2 * vp * tok_b + p0 * ES;
+      o_sc = g.o_dt + h * g.sc_h + lane * tok_b;
+      o_pw = (tt0 * pw + g.prep_q + grp * R + r0) * 4;
+      o_pa = (4 * pg * pw + g.prep_a + ps) * 4;
+      d_q1 = R == 1 ? tok_b : g.qk_r;  // row 2rp + 1: the next token (R = 1) or the next rank
+      d_w1 = R == 1 ? pw_b : 4;
+      d_k = g.o_k - g.o_q;
+      d_z = g.o_z - g.o_v;
+      d_a = g.o_a - g.o_dt;
+      d_tr = g.o_tr - g.o_dt;
+      d_fk = (g.prep_k - g.prep_q) * 4;
+    } else {
+      q_row = static_cast<const T*>(a.q.ptr) + b * a.q.stride[0] + grp * a.q.stride[2] + n0;
+      k_row = static_cast<const T*>(a.k.ptr) + b * a.k.stride[0] + grp * a.k.stride[2] + n0;
+      q_t = static_cast<int>(a.q.stride[1]);
+      q_r = static_cast<int>(a.q.stride[3]);
+      k_t = static_cast<int>(a.k.stride[1]);
+      k_r = static_cast<int>(a.k.stride[3]);
+      v_row = static_cast<const T*>(a.value.ptr) + b * a.value.stride[0] +
+              h * a.value.stride[2] + p0;
+      z_row = static_cast<const T*>(a.gate.ptr) + b * a.gate.stride[0] + h * a.gate.stride[2] +
+              p0;
+      v_t = static_cast<int>(a.value.stride[1]);
+      z_t = static_cast<int>(a.gate.stride[1]);
+      dt_d = a.dt.dtype;
+      aa_d = a.a.dtype;
+      tr_d = a.trap.dtype;
+      dt_row = offx(a.dt.ptr, dt_d, b * a.dt.stride[0] + h * a.dt.stride[2]);
+      aa_row = offx(a.a.ptr, aa_d, b * a.a.stride[0] + h * a.a.stride[2]);
+      tr_row = offx(a.trap.ptr, tr_d, b * a.trap.stride[0] + h * a.trap.stride[2]);
+      dt_t = static_cast<int>(a.dt.stride[1]);
+      aa_t = static_cast<int>(a.a.stride[1]);
+      tr_t = static_cast<int>(a.trap.stride[1]);
+      prep_row = prep + static_cast<int64_t>(b) * L * pw;
+      const bool given = a.phase_mode == M3_PHASE_GIVEN;
+      ph_row = given ? static_cast<const float*>(a.phase.ptr) + b * a.phase.stride[0] +
+                           h * a.phase.stride[2] + ps * a.phase.stride[3]
+                     : nullptr;
+      ph_t = given ? static_cast<int>(a.phase.stride[1]) : 0;
+      fq_o = g.prep_q + grp * R;
+      fk_o = g.prep_k + grp * R;
+      pa_o = g.prep_a + ps;
+      qk_n = max(0, min(8, N - n0));
+      vz_n = max(0, min(4, P - p0));
+      vec_qk = g.vec_qk;
+      vec_vz = g.vec_vz;
+    }
+  }
+
+  // q / k rows 2rp, 2rp+1 and value / gate tokens 2vp, 2vp+1 of the sub-chunk at token t0
+  // (nw valid tokens), plus the RMSNorm factors of the q / k rows.
+  __device__ __forceinline__ void words(int t0, int nw, bool qk_on, bool vz_on,
+                                        uint32_t (&rq)[2][W8], uint32_t (&rk)[2][W8],
+                                        uint32_t (&rv)[2][W4], uint32_t (&rz)[2][W4],
+                                        float (&fq)[2], float (&fk)[2]) const {
+    if constexpr (FULL) {
+      const int tb = t0 * tok_b, tw = t0 * pw_b;
+      if (qk_on) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          bload_words<W8>(rq[j], rs_p, o_qk + tb + j * d_q1);
+          bload_words<W8>(rk[j], rs_p, o_qk + tb + j * d_q1 + d_k);
+          fq[j] = bload_f32(rs_w, o_pw + tw + j * d_w1);
+          fk[j] = bload_f32(rs_w, o_pw + tw + j * d_w1 + d_fk);
+        }
+      }
+      if (vz_on) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          bload_words<W4>(rv[j], rs_p, o_vz + tb + j * tok_b);
+          bload_words<W4>(rz[j], rs_p, o_vz + tb + j * tok_b + d_z);
+        }
+      }
+    } else {
+      if (qk_on) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int row = 2 * rp + j, tt = row / R, r = row - tt * R;
+          const bool ok = tt < nw;
+          const int tg = t0 + tt;
+          load_words<T, 8>(rq[j], q_row + tg * q_t + r * q_r, ok ? qk_n : 0, vec_qk);
+          load_words<T, 8>(rk[j], k_row + tg * k_t + r * k_r, ok ? qk_n : 0, vec_qk);
+          if (norm && ok) {
+            const float* pr = prep_row + static_cast<int64_t>(tg) * pw;
+            fq[j] = pr[fq_o + r];
+            fk[j] = pr[fk_o + r];
+          }
+        }
+      }
+      if (vz_on) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int tt = 2 * vp + j;
+          const bool ok = tt < nw;
+          const int tg = t0 + tt;
+          load_words<T, 4>(rv[j], v_row + tg * v_t, ok ? vz_n : 0, vec_vz);
+          load_words<T, 4>(rz[j], z_row + tg * z_t, ok ? vz_n : 0, vec_vz);
+        }
+      }
+    }
+  }
+
+  // angle inputs of tokens 4pg .. 4pg+3 (pi tanh(angle) from the prep rows, or given phases)
+  __device__ __forceinline__ void angle_in(int t0, int nw, bool ph_on, float (&pa)[4]) const {
+    if (!ph_on) return;
+    if constexpr (FULL) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pa[i] = bload_f32(rs_w, o_pa + (t0 + i) * pw_b);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tt = 4 * pg + i;
+        const int tg = t0 + tt;
+        pa[i] = 0.f;
+        if (tt < nw) {
+          pa[i] = angles ? prep_row[static_cast<int64_t>(tg) * pw + pa_o] : ph_row[tg * ph_t];
+        }
+      }
+    }
+  }
+
+  // wave 0: raw dt, a, trap of token t0 + lane
+  __device__ __forceinline__ void scalars_in(int t0, int nw, int lane, float& sdt, float& sa,
+                                             float& str) const {
+    if constexpr (FULL) {
+      const int o = o_sc + t0 * tok_b;
+      sdt = bload_elem<T>(rs_p, o);
+      sa = bload_elem<T>(rs_p, o + d_a);
+      str = bload_elem<T>(rs_p, o + d_tr);
+    } else {
+      sdt = sa = str = 0.f;
+      if (lane < nw) {
+        const int tg = t0 + lane;
+        sdt = ldx(dt_row, dt_d, static_cast<int64_t>(tg) * dt_t);
+        sa = ldx(aa_row, aa_d, static_cast<int64_t>(tg) * aa_t);
+        str = ldx(tr_row, tr_d, static_cast<int64_t>(tg) * tr_t);
+      }
+    }
+  }
+};
+
+// Per-token scalars of the sub-chunk at token tb (wave 0, lane = token) into the block SCn:
+// dt, the within-chunk cumsum of adt and exp of it, gamma = dt sigmoid(trap), the exp-trapezoid
+// scale = gamma + dt' (1 - sigmoid(trap')) of the next token (ops.py:659-671), and the
+// products with the decays the scores and the carry use. The last token's next-token term
+// belongs to the first token of the following sub-chunk: the call for that sub-chunk adds it
+// into SCp (the previous block), where exp(cum_last - cum_last) = 1 makes it a plain add.
+template <typename Lay, int TOK, int TPT>
+__device__ __forceinline__ void scalar_stage(float* SCn, float* SCp, int tb, int L, int lane,
+                                             bool raw_dt, float dt_bias, float sdt, float sa,
+                                             float str) {
+  const int wn = min(TOK, L - tb);
+  const bool tv = lane < wn;
+  float dt = 0.f, adt = 0.f, tr = 0.f;
+  if (tv) {
+    dt_adt(raw_dt, sdt, sa, dt_bias, dt, adt);
+    tr = sigmoidf(str);
+  }
+  const float lead = dt * (1.f - tr);  // this token's term of the previous token's scale
+  float right = __shfl_down(lead, 1);
+  if (lane >= wn - 1) right = 0.f;
+  if (SCp != nullptr && lane == 0) {
+    SCp[Lay::SCL + TOK - 1] += lead;
+    SCp[Lay::VSF + TOK - 1] += lead;
+    SCp[Lay::BSC + TOK - 1] += lead;
+  }
+  const float gamma = dt * tr;
+  const float scale = gamma + right;
+  const float cum = wave_incl_scan(tv ? adt : 0.f, lane);
+  const float cum_last = __shfl(cum, wn - 1);
+  const float cv = tv ? cum : cum_last;
+  const float cend = __shfl(cv, min(lane | (TPT - 1), wn - 1));
+  SCn[Lay::DTV + lane] = tv ? dt : 0.f;
+  SCn[Lay::CUM + lane] = cv;
+  SCn[Lay::ECUM + lane] = tv ? __expf(cv) : 0.f;
+  SCn[Lay::SCL + lane] = tv ? scale : 0.f;
+  SCn[Lay::GAM + lane] = tv ? gamma : 0.f;
+  SCn[Lay::VSF + lane] = tv ? scale * __expf(cum_last - cv) : 0.f;
+  SCn[Lay::BSC + lane] = tv ? scale * __expf(cend - cv) : 0.f;
+  if (lane < TOK && (lane & (TPT - 1)) == 0) SCn[Lay::CEND + lane / TPT] = cend;
+  if (lane == 0) SCn[Lay::ECL] = __expf(cum_last);
+}
+
+// Bounded phase (model.py:215-256) of tokens 4pg .. 4pg+3 of the sub-chunk at t0 for angle ps:
+// fmod-reduced increments summed within 64-token blocks, an fmod-reduced carry between blocks,
+// the running block sum and carry in pbase / poff; cos / sin into the tables.
+template <int PG, int CSS>
+__device__ __forceinline__ void phase_stage(float* cs, float* sn, float* pbase, float* poff,
+                                            const float* dtv, int t0, int L, int pg, int lane,
+                                            bool angles, const float (&pa)[4], float* fph) {
+  const int width = min(4 * PG, L - t0);
+  float ph[4];
+  if (angles) {
+    float x[4];
+    bool big = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tt = 4 * pg + i;
+      x[i] = tt < width ? __fmul_rn(pa[i], dtv[tt]) : 0.f;
+      big = big || !(fabsf(x[i]) < 1048576.0f);
+    }
+    float inc[4];
+    if (big) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) inc[i] = m3_fmod_2pi(x[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) inc[i] = m3_fmod_2pi_small(x[i]);
+    }
+    float cpre[4];
+    float run = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      run = __fadd_rn(run, inc[i]);
+      cpre[i] = run;
+    }
+    const float incl = seg_incl_scan<PG>(run, lane);
+    const float excl = __fsub_rn(incl, run);
+    float base = *pbase, off = *poff;
+    if ((t0 & 63) == 0 && t0 > 0) {
+      off = m3_fmod_2pi_small(__fadd_rn(off, base));
+      base = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // |base|, |excl + cpre| <= 64 * 2 pi and |off| < 2 pi: within the reduction's range
+      ph[i] = m3_fmod_2pi_small(__fadd_rn(__fadd_rn(base, __fadd_rn(excl, cpre[i])), off));
+      if (t0 + 4 * pg + i == L - 1 && fph != nullptr) *fph = ph[i];
+    }
+    if (pg == PG - 1) {
+      *pbase = __fadd_rn(base, incl);
+      *poff = off;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ph[i] = pa[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tt = 4 * pg + i;
+    float sv, cv;
+    __sincosf(ph[i], &sv, &cv);
+    cs[tt * CSS] = cv;
+    sn[tt * CSS] = sv;
+  }
+}
+
 template <typename T, int R, bool FULL>
 __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, const ScanGeom g,
                                                         const float* __restrict__ prep) {
@@ -341,6 +693,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   constexpr int TPT = 16 / R;          // tokens per 16-row tile
   constexpr int PG = TOK / 4;          // phase lanes per angle (4 tokens each)
   constexpr bool F32 = sizeof(T) == 4;
+  constexpr int ES = sizeof(T);
   constexpr int LQ = Lay::LQ, LR = Lay::LR, NP = kNPad, CSS = Lay::CSS;
   // FULL: the model's shape (N = 128, P = 64, S = 32) in projection form with vector loads
   const int N = FULL ? kNPad : a.d_state;
@@ -505,471 +858,387 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     }
   }
 
-  // ---- per-(b, h) bases of the per-token reads (hoisted out of the sub-chunk loop)
-  const T* q_row = static_cast<const T*>(a.q.ptr) + b * a.q.stride[0] + grp * a.q.stride[2] + n0;
-  const T* k_row = static_cast<const T*>(a.k.ptr) + b * a.k.stride[0] + grp * a.k.stride[2] + n0;
-  // token / rank strides fit 32 bits (they are strides within one batch row)
-  const int q_t = static_cast<int>(a.q.stride[1]), q_r = static_cast<int>(a.q.stride[3]);
-  const int k_t = static_cast<int>(a.k.stride[1]), k_r = static_cast<int>(a.k.stride[3]);
-  const T* v_row = static_cast<const T*>(a.value.ptr) + b * a.value.stride[0] +
-                   h * a.value.stride[2] + p0;
-  const T* z_row = static_cast<const T*>(a.gate.ptr) + b * a.gate.stride[0] +
-                   h * a.gate.stride[2] + p0;
-  const int v_t = static_cast<int>(a.value.stride[1]), z_t = static_cast<int>(a.gate.stride[1]);
-  const int dt_d = a.dt.dtype, aa_d = a.a.dtype, tr_d = a.trap.dtype;
-  const void* dt_row = offx(a.dt.ptr, dt_d, b * a.dt.stride[0] + h * a.dt.stride[2]);
-  const void* aa_row = offx(a.a.ptr, aa_d, b * a.a.stride[0] + h * a.a.stride[2]);
-  const void* tr_row = offx(a.trap.ptr, tr_d, b * a.trap.stride[0] + h * a.trap.stride[2]);
-  const int dt_t = static_cast<int>(a.dt.stride[1]), aa_t = static_cast<int>(a.a.stride[1]);
-  const int tr_t = static_cast<int>(a.trap.stride[1]);
+  // ---- per-token reads
   const float dt_bias = raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0])
                                : 0.f;
-  const float* prep_row = prep + static_cast<int64_t>(b) * L * PW;
-  const float* ph_row = (!FULL && a.phase_mode == M3_PHASE_GIVEN)
-                            ? static_cast<const float*>(a.phase.ptr) + b * a.phase.stride[0] +
-                                  h * a.phase.stride[2] + ps * a.phase.stride[3]
-                            : nullptr;
-  const int ph_t = (!FULL && a.phase_mode == M3_PHASE_GIVEN) ? static_cast<int>(a.phase.stride[1])
-                                                             : 0;
+  Feed<T, R, FULL> fd;
+  fd.init(a, g, prep, b, h, grp, rp, n0, vp, p0, pg, ps, lane, N, P, norm, angles);
   float* fph = a.final_phase.ptr != nullptr
                    ? static_cast<float*>(a.final_phase.ptr) + b * a.final_phase.stride[0] +
                          h * a.final_phase.stride[1] + ps * a.final_phase.stride[2]
                    : nullptr;
-  T* out_row = static_cast<T*>(a.out.ptr) + b * a.out.stride[0] + h * a.out.stride[2];
-  const int out_t = static_cast<int>(a.out.stride[1]);
+  const __amdgpu_buffer_rsrc_t rs_o =
+      make_rsrc(FULL ? static_cast<char*>(a.out.ptr) + b * g.out_b : nullptr, FULL ? L * g.out_t : 0);
+  T* out_row = nullptr;
+  int out_t = 0, o_out = 0;
+  if constexpr (FULL) {
+    out_t = g.out_t;
+    o_out = h * g.out_h;
+  } else {
+    out_row = static_cast<T*>(a.out.ptr) + b * a.out.stride[0] + h * a.out.stride[2];
+    out_t = static_cast<int>(a.out.stride[1]);
+  }
 
-  // ---- registers the next sub-chunk's global data is loaded into
+  // rotation roles of the q / k lane's 8 columns n0 + i: partner element, cos / sin table
+  // column and the sign of the sine term; columns outside the rotated range keep cos 1, sin 0
+  int rcol[8];
+  float rsgn[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int n = n0 + i;
+    if (!mimo_rot) {
+      const int jn = n >> 1;
+      rcol[i] = min(jn, max(S - 1, 0));
+      rsgn[i] = jn < S ? ((i & 1) ? 1.f : -1.f) : 0.f;
+    } else {
+      const bool first = n < S, third = n >= 2 * S && n < 3 * S;
+      rcol[i] = first ? n : (third ? n - 2 * S : 0);
+      rsgn[i] = first ? -1.f : (third ? 1.f : 0.f);
+    }
+  }
+
+  // ---- registers the global data of coming sub-chunks is loaded into
   constexpr int W8 = Words<T>::W8, W4 = Words<T>::W4;
   uint32_t rq[2][W8], rk[2][W8], rv[2][W4], rz[2][W4];
   float fq[2] = {1.f, 1.f}, fk[2] = {1.f, 1.f};
-  float sdt = 0.f, sa = 0.f, str = 0.f, ldt = 0.f, ltr = 0.f;
   float pa[4] = {0.f, 0.f, 0.f, 0.f};
-
-  __syncthreads();
+  float sdt = 0.f, sa = 0.f, str = 0.f;  // wave 0: raw scalars of a coming sub-chunk
   const int nsub = (L + TOK - 1) / TOK;
-  // Iteration c consumes the registers loaded for sub-chunk c, issues the loads of c + 1, then
-  // computes c while they are in flight; at its end wave 0 turns the per-token scalars of c + 1
-  // into the other half of the double-buffered scalar block. c = -1 only primes sub-chunk 0.
-  for (int c = -1; c < nsub; ++c) {
+  auto scb = [&](int c) { return F + Lay::SC0 + (c % 3) * Lay::SCB; };
+  auto csb = [&](int c) { return F + Lay::CS0 + (c & 1) * Lay::CSB; };
+
+  // Pipeline: iteration c stages sub-chunk c into LDS (interval 1), then computes its outputs
+  // and state carry while the phases of c + 1 and (wave 0) the scalars of c + 2 are computed
+  // and the loads of c + 1 (words), c + 2 (angles) and c + 3 (scalars) are in flight
+  // (interval 2). Scalar blocks rotate over 3 buffers, cos / sin tables over 2.
+  // prologue: scalars of 0 and 1, phases of 0
+  fd.words(0, min(TOK, L), qk_on, vz_on, rq, rk, rv, rz, fq, fk);
+  fd.angle_in(0, min(TOK, L), ph_on, pa);
+  if (w == 0 && nsub > 0) {
+    fd.scalars_in(0, min(TOK, L), lane, sdt, sa, str);
+    scalar_stage<Lay, TOK, TPT>(scb(0), nullptr, 0, L, lane, raw_dt, dt_bias, sdt, sa, str);
+    if (nsub > 1) {
+      fd.scalars_in(TOK, min(TOK, L - TOK), lane, sdt, sa, str);
+      scalar_stage<Lay, TOK, TPT>(scb(1), scb(0), TOK, L, lane, raw_dt, dt_bias, sdt, sa, str);
+    }
+    if (nsub > 2) fd.scalars_in(2 * TOK, min(TOK, L - 2 * TOK), lane, sdt, sa, str);
+  }
+  __syncthreads();
+  if (ph_on && nsub > 0) {
+    float* t = csb(0);
+    phase_stage<PG, CSS>(t + ps, t + Lay::SNO + ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
+                         scb(0) + Lay::DTV, 0, L, pg, lane, angles, pa, fph);
+  }
+  if (nsub > 1) fd.angle_in(TOK, min(TOK, L - TOK), ph_on, pa);
+  __syncthreads();
+
+  for (int c = 0; c < nsub; ++c) {
     const int t0 = c * TOK;
     const int width = min(TOK, L - t0);
-    const float* SC = F + ((c & 1) ? Lay::SC1 : Lay::SC0);
-    if (c >= 0) {
-      // (1) phase of (token 4pg + i, angle ps), its cos / sin
-      if (ph_on) {
-        float ph[4];
-        if (angles) {
-          float cpre[4];
-          float run = 0.f;
+    const float* SC = scb(c);
+    const float* CSt = csb(c);
+
+    // ---- interval 1: stage sub-chunk c
+    // q / k rows -> Qs, Ks (row-major), KT (transposed, swizzled); rows 2rp, 2rp+1
+    if (qk_on) {
+      float kt[2][8];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int row = 2 * rp + j, tt = row / R;
+        float q[8], k[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          q[i] = fmaf(raw_get<T>(rq[j], i), fq[j] * wq[i], bq[R == 1 ? 0 : j][i]);
+          k[i] = fmaf(raw_get<T>(rk[j], i), fk[j] * wk[i], bk[R == 1 ? 0 : j][i]);
+        }
+        if (rotate) {
+          // x' = x cos + sgn partner sin: SISO pairs (2j, 2j+1), MIMO pairs (n, n + N/2)
+          float qp[8], kp[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (!mimo_rot) {
+              qp[i] = q[i ^ 1];
+              kp[i] = k[i ^ 1];
+            } else {
+              const int half = N >> 1;
+              if (half >= 8) {
+                qp[i] = __shfl_xor(q[i], half >> 3, 16);
+                kp[i] = __shfl_xor(k[i], half >> 3, 16);
+              } else {
+                qp[i] = q[i ^ half];
+                kp[i] = k[i ^ half];
+              }
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float cr = CSt[tt * CSS + rcol[i]];
+            const float sr = CSt[Lay::SNO + tt * CSS + rcol[i]];
+            const float cc = rsgn[i] != 0.f ? cr : 1.f;
+            const float ss = rsgn[i] * sr;
+            q[i] = fmaf(qp[i], ss, q[i] * cc);
+            k[i] = fmaf(kp[i], ss, k[i] * cc);
+          }
+        }
+        st_row8<T>(Qs + row * LQ + n0, q);
+        st_row8<T>(Ks + row * LQ + n0, k);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int n = n0 + i;
+        if (FULL || n < N) {
+          st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> 3), kt[0][i], kt[1][i]);
+        }
+      }
+    }
+    // value / gate -> VT, VsT, ZT (transposed, swizzled), tokens 2vp, 2vp+1
+    if (vz_on) {
+      float v[2][4], z[2][4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[j][i] = raw_get<T>(rv[j], i);
+          z[j][i] = raw_get<T>(rz[j], i);
+        }
+      }
+      const float f0 = SC[Lay::VSF + 2 * vp], f1 = SC[Lay::VSF + 2 * vp + 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = p0 + i;
+        if (!FULL && p >= P) continue;
+        const int key = p >> 2;
+        if (R == 1) {
+          const int row = swz<ROWS>(2 * vp, key);
+          st_pair<T>(VT + p * LR + row, v[0][i], v[1][i]);
+          st_pair<T>(VsT + p * LR + row, v[0][i] * f0, v[1][i] * f1);
+          st_pair<T>(ZT + p * LR + row, z[0][i], z[1][i]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const float fj = j ? f1 : f0;
+#pragma unroll
+            for (int r = 0; r < R; r += 2) {
+              const int row = swz<ROWS>((2 * vp + j) * R + r, key);
+              const float va = mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p]);
+              const float vb = mul_r<T>(v[j][i], F[Lay::MX + (r + 1) * kPPad + p]);
+              st_pair<T>(VT + p * LR + row, va, vb);
+              st_pair<T>(VsT + p * LR + row, va * fj, vb * fj);
+              st_pair<T>(ZT + p * LR + row, mul_r<T>(z[j][i], F[Lay::MZ + r * kPPad + p]),
+                         mul_r<T>(z[j][i], F[Lay::MZ + (r + 1) * kPPad + p]));
+            }
+          }
+        }
+      }
+    }
+    // the state at the start of this sub-chunk, rounded to the activation dtype -> Sb[p][n]
+#pragma unroll
+    for (int k = 0; k < kTiles; ++k) {
+      const int u = w + kWaves * k;
+      if (u < n_tiles) {
+        const int ni = u / kPT, pj = u - ni * kPT;
+        st_quad<T>(Sb + (16 * pj + l16) * LQ + 16 * ni + 4 * lg, st[k]);
+      }
+    }
+    __syncthreads();
+
+    // ---- interval 2
+    // words of sub-chunk c + 1 into registers; they fly while sub-chunk c computes
+    if (c + 1 < nsub) {
+      fd.words(t0 + TOK, min(TOK, L - t0 - TOK), qk_on, vz_on, rq, rk, rv, rz, fq, fk);
+    }
+
+    // outputs for query row tile `it` and P tiles pj = wp, wp + WPR, ...
+    const int it = w / WPR, wp = w - it * WPR;
+    const int trow = 16 * it + l16;
+    const int tq = trow / R;
+    // 16-bit: the query rows of this tile, B operand of the scores and A operand of inter
+    typename M::v8 qv[F32 ? 1 : NP / 32];
+    if constexpr (!F32) {
+#pragma unroll
+      for (int kk = 0; kk < NP / 32; ++kk) {
+        qv[kk] = *reinterpret_cast<const typename M::v8*>(Qs + trow * LQ + 32 * kk + 8 * lg);
+      }
+    }
+    // scores Sc^T tiles (rows s, column t), issued before the phase work below
+    f4 acc[RT];
+#pragma unroll
+    for (int sj = 0; sj < RT; ++sj) {
+      acc[sj] = zero4();
+      if (sj > it) continue;
+      if constexpr (!F32) {
+#pragma unroll
+        for (int kk = 0; kk < NP / 32; ++kk) {
+          const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
+              Ks + (16 * sj + l16) * LQ + 32 * kk + 8 * lg);
+          acc[sj] = M::mma(av, qv[kk], acc[sj]);
+        }
+      } else {
+#pragma unroll 8
+        for (int kk = 0; kk < NP; kk += 4) {
+          acc[sj] = M::mma(Ks[(16 * sj + l16) * LQ + kk + lg], Qs[trow * LQ + kk + lg], acc[sj]);
+        }
+      }
+    }
+    // phases of sub-chunk c + 1 (its dt block was computed two iterations ago)
+    if (ph_on && c + 1 < nsub) {
+      float* t = csb(c + 1);
+      phase_stage<PG, CSS>(t + ps, t + Lay::SNO + ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
+                           scb(c + 1) + Lay::DTV, t0 + TOK, L, pg, lane, angles, pa, fph);
+      if (c + 2 < nsub) fd.angle_in(t0 + 2 * TOK, min(TOK, L - t0 - 2 * TOK), ph_on, pa);
+    }
+    // decayed scores W[t, s] = Sc[t, s] d[t, s] in FP32
+    const float cum_t = SC[Lay::CUM + tq];
+    const float gam_t = SC[Lay::GAM + tq];
+    f4 wsc[RT];
+#pragma unroll
+    for (int sj = 0; sj < RT; ++sj) {
+      wsc[sj] = zero4();
+      if (sj > it) continue;
+      if (sj < it) {
+        // strictly earlier tile: d = exp(cum_t - cend) * (scale_s exp(cend - cum_s)), both <= 1
+        const float at = __expf(cum_t - SC[Lay::CEND + sj]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int ts = (16 * sj + 4 * lg + i) / R;
+          wsc[sj][i] = acc[sj][i] * (at * SC[Lay::BSC + ts]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int ts = (16 * sj + 4 * lg + i) / R;
+          const float d = tq > ts ? SC[Lay::SCL + ts] * __expf(cum_t - SC[Lay::CUM + ts])
+                                  : (tq == ts ? gam_t : 0.f);
+          wsc[sj][i] = acc[sj][i] * d;
+        }
+      }
+    }
+    float ecum[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ecum[i] = SC[Lay::ECUM + (16 * it + 4 * lg + i) / R];
+    for (int pj = wp; pj < kPT; pj += WPR) {
+      const int pcol = 16 * pj + l16;
+      const int key = pcol >> 2;
+      f4 yi = zero4(), ye = zero4();
+      if constexpr (!F32) {
+        // intra: W V with the K axis permuted as the D-layout of wsc
+#pragma unroll
+        for (int m = 0; m < (RT + 1) / 2; ++m) {
+          if (2 * m > it) continue;
+          typename M::v8 av, bv;
+          const typename M::v4 b0 = *reinterpret_cast<const typename M::v4*>(
+              VT + pcol * LR + swz<ROWS>(32 * m + 4 * lg, key));
+          const typename M::v4 b1 = *reinterpret_cast<const typename M::v4*>(
+              VT + pcol * LR + swz<ROWS>(32 * m + 16 + 4 * lg, key));
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int tt = 4 * pg + i;
-            const float inc = tt < width ? m3_fmod_2pi(__fmul_rn(pa[i], SC[Lay::DTV + tt])) : 0.f;
-            run = __fadd_rn(run, inc);
-            cpre[i] = run;
+            av[i] = from_f<T>(wsc[2 * m][i]);
+            av[4 + i] = from_f<T>(2 * m + 1 < RT ? wsc[2 * m + 1][i] : 0.f);
+            bv[i] = b0[i];
+            bv[4 + i] = b1[i];
           }
-          const float incl = seg_incl_scan<PG>(run, lane);
-          const float excl = __fsub_rn(incl, run);
-          float base = F[Lay::PBASE + ps], off = F[Lay::POFF + ps];
-          if ((t0 & 63) == 0 && t0 > 0) {
-            off = m3_fmod_2pi(__fadd_rn(off, base));
-            base = 0.f;
-          }
+          yi = M::mma(av, bv, yi);
+        }
+        // inter: Q rnd(S)^T
+#pragma unroll
+        for (int kk = 0; kk < NP / 32; ++kk) {
+          const typename M::v8 bv =
+              *reinterpret_cast<const typename M::v8*>(Sb + pcol * LQ + 32 * kk + 8 * lg);
+          ye = M::mma(qv[kk], bv, ye);
+        }
+      } else {
+#pragma unroll
+        for (int sj = 0; sj < RT; ++sj) {
+          if (sj > it) continue;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            ph[i] = m3_fmod_2pi(__fadd_rn(__fadd_rn(base, __fadd_rn(excl, cpre[i])), off));
-            if (t0 + 4 * pg + i == L - 1 && fph != nullptr) *fph = ph[i];
+            yi = M::mma(wsc[sj][i], VT[pcol * LR + swz<ROWS>(16 * sj + 4 * lg + i, key)], yi);
           }
-          if (pg == PG - 1) {
-            F[Lay::PBASE + ps] = __fadd_rn(base, incl);
-            F[Lay::POFF + ps] = off;
+        }
+#pragma unroll 8
+        for (int kk = 0; kk < NP; kk += 4) {
+          ye = M::mma(Qs[trow * LQ + kk + lg], Sb[pcol * LQ + kk + lg], ye);
+        }
+      }
+      // epilogue: rows 16 it + 4 lg + i, column pcol
+      if (FULL || pcol < P) {
+        float vv[4], zz[4];
+        if constexpr (!F32) {
+          const typename M::v4 v4 = *reinterpret_cast<const typename M::v4*>(
+              VT + pcol * LR + swz<ROWS>(16 * it + 4 * lg, key));
+          const typename M::v4 z4 = *reinterpret_cast<const typename M::v4*>(
+              ZT + pcol * LR + swz<ROWS>(16 * it + 4 * lg, key));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            vv[i] = to_f(v4[i]);
+            zz[i] = to_f(z4[i]);
           }
         } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) ph[i] = pa[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tt = 4 * pg + i;
-          float sv, cv;
-          __sincosf(ph[i], &sv, &cv);
-          F[Lay::CS + tt * CSS + ps] = cv;
-          F[Lay::SN + tt * CSS + ps] = sv;
-        }
-      }
-      __syncthreads();
-
-      // (2) q / k rows -> Qs, Ks (row-major), KT (transposed); rows 2rp, 2rp+1
-      if (qk_on) {
-        float kt[2][8];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int row = 2 * rp + j, tt = row / R;
-          const bool ok = tt < width;
-          float q[8], k[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            q[i] = ok ? fmaf(raw_get<T>(rq[j], i), fq[j] * wq[i], bq[R == 1 ? 0 : j][i]) : 0.f;
-            k[i] = ok ? fmaf(raw_get<T>(rk[j], i), fk[j] * wk[i], bk[R == 1 ? 0 : j][i]) : 0.f;
-          }
-          if (rotate && ok) {
-            if (!mimo_rot) {
-#pragma unroll
-              for (int i = 0; i < 8; i += 2) {
-                const int jn = (n0 + i) >> 1;
-                if (jn < S) {
-                  const float cc = F[Lay::CS + tt * CSS + jn], ss = F[Lay::SN + tt * CSS + jn];
-                  const float q0 = q[i], q1 = q[i + 1], k0 = k[i], k1 = k[i + 1];
-                  q[i] = fmaf(q0, cc, -q1 * ss);
-                  q[i + 1] = fmaf(q0, ss, q1 * cc);
-                  k[i] = fmaf(k0, cc, -k1 * ss);
-                  k[i + 1] = fmaf(k0, ss, k1 * cc);
-                }
-              }
-            } else {
-              // pairs (n, n + N/2) for n < S = N/4: the partner lives N/16 lanes away (N >= 16),
-              // or in this lane (N <= 8)
-              const int half = N >> 1;
-              float qp[8], kp[8];
-#pragma unroll
-              for (int i = 0; i < 8; ++i) {
-                if (half >= 8) {
-                  qp[i] = __shfl_xor(q[i], half >> 3, 16);
-                  kp[i] = __shfl_xor(k[i], half >> 3, 16);
-                } else {
-                  qp[i] = q[i ^ half];
-                  kp[i] = k[i ^ half];
-                }
-              }
-#pragma unroll
-              for (int i = 0; i < 8; ++i) {
-                const int n = n0 + i;
-                if (n < S) {  // first quarter: x cos - partner sin
-                  const float cc = F[Lay::CS + tt * CSS + n], ss = F[Lay::SN + tt * CSS + n];
-                  q[i] = fmaf(q[i], cc, -qp[i] * ss);
-                  k[i] = fmaf(k[i], cc, -kp[i] * ss);
-                } else if (n >= 2 * S && n < 3 * S) {  // third quarter: partner sin + x cos
-                  const float cc = F[Lay::CS + tt * CSS + n - 2 * S];
-                  const float ss = F[Lay::SN + tt * CSS + n - 2 * S];
-                  q[i] = fmaf(qp[i], ss, q[i] * cc);
-                  k[i] = fmaf(kp[i], ss, k[i] * cc);
-                }
-              }
-            }
-          }
-          st_row8<T>(Qs + row * LQ + n0, q);
-          st_row8<T>(Ks + row * LQ + n0, k);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int n = n0 + i;
-          if (n < N) st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> 3), kt[0][i], kt[1][i]);
-        }
-      }
-      // (3) value / gate -> VT, VsT, ZT (transposed, swizzled), tokens 2vp, 2vp+1
-      if (vz_on) {
-        float v[2][4], z[2][4];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
           for (int i = 0; i < 4; ++i) {
-            v[j][i] = raw_get<T>(rv[j], i);
-            z[j][i] = raw_get<T>(rz[j], i);
+            vv[i] = VT[pcol * LR + swz<ROWS>(16 * it + 4 * lg + i, key)];
+            zz[i] = ZT[pcol * LR + swz<ROWS>(16 * it + 4 * lg + i, key)];
           }
         }
-        const float f0 = SC[Lay::VSF + 2 * vp], f1 = SC[Lay::VSF + 2 * vp + 1];
+        float y = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int p = p0 + i;
-          if (p >= P) continue;
-          const int key = p >> 2;
-          if (R == 1) {
-            const int row = swz<ROWS>(2 * vp, key);
-            st_pair<T>(VT + p * LR + row, v[0][i], v[1][i]);
-            st_pair<T>(VsT + p * LR + row, v[0][i] * f0, v[1][i] * f1);
-            st_pair<T>(ZT + p * LR + row, z[0][i], z[1][i]);
-          } else {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const float fj = j ? f1 : f0;
-#pragma unroll
-              for (int r = 0; r < R; r += 2) {
-                const int row = swz<ROWS>((2 * vp + j) * R + r, key);
-                const float va = mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p]);
-                const float vb = mul_r<T>(v[j][i], F[Lay::MX + (r + 1) * kPPad + p]);
-                st_pair<T>(VT + p * LR + row, va, vb);
-                st_pair<T>(VsT + p * LR + row, va * fj, vb * fj);
-                st_pair<T>(ZT + p * LR + row, mul_r<T>(z[j][i], F[Lay::MZ + r * kPPad + p]),
-                           mul_r<T>(z[j][i], F[Lay::MZ + (r + 1) * kPPad + p]));
-              }
+          const int row = 16 * it + 4 * lg + i;
+          const int tt = row / R, r = row - tt * R;
+          float yr = (fmaf(ye[i], ecum[i], yi[i]) + Dh * vv[i]) *
+                     __fdividef(zz[i], 1.f + __expf(-zz[i]));
+          if (R > 1) yr *= F[Lay::MO + r * kPPad + pcol];
+          y = (R > 1 && r > 0) ? y + yr : yr;
+          if (r == R - 1) {
+            if constexpr (FULL) {
+              // rows of tokens >= L fall outside the buffer extent: the store is dropped
+              bstore_elem<T>(y, rs_o, (t0 + tt) * out_t + o_out + pcol * ES);
+            } else {
+              if (tt < width) out_row[(t0 + tt) * out_t + pcol] = from_f<T>(y);
             }
           }
-        }
-      }
-      // (4) the state at the start of this sub-chunk, rounded to the activation dtype -> Sb[p][n]
-#pragma unroll
-      for (int k = 0; k < kTiles; ++k) {
-        const int u = w + kWaves * k;
-        if (u < n_tiles) {
-          const int ni = u / kPT, pj = u - ni * kPT;
-          st_quad<T>(Sb + (16 * pj + l16) * LQ + 16 * ni + 4 * lg, st[k]);
-        }
-      }
-      __syncthreads();
-    }  // c >= 0 (stages 1-4)
-
-    // ---- loads of sub-chunk c + 1 into registers; they fly while sub-chunk c computes
-    if (c + 1 < nsub) {
-      const int n0t = t0 + TOK;  // first token of sub-chunk c + 1
-      const int nw = min(TOK, L - n0t);
-      if (qk_on) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int row = 2 * rp + j, tt = row / R, r = row - tt * R;
-          const bool ok = tt < nw;
-          const int tg = n0t + tt;
-          load_words<T, 8>(rq[j], q_row + tg * q_t + r * q_r, ok ? qk_n : 0, vec_qk);
-          load_words<T, 8>(rk[j], k_row + tg * k_t + r * k_r, ok ? qk_n : 0, vec_qk);
-          if (norm && ok) {
-            const float* pr = prep_row + tg * PW;
-            fq[j] = pr[g.prep_q + grp * R + r];
-            fk[j] = pr[g.prep_k + grp * R + r];
-          }
-        }
-      }
-      if (vz_on) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int tt = 2 * vp + j;
-          const bool ok = tt < nw;
-          const int tg = n0t + tt;
-          load_words<T, 4>(rv[j], v_row + tg * v_t, ok ? vz_n : 0, vec_vz);
-          load_words<T, 4>(rz[j], z_row + tg * z_t, ok ? vz_n : 0, vec_vz);
-        }
-      }
-      if (w == 0) {
-        const int tg = n0t + lane;
-        sdt = sa = str = ldt = ltr = 0.f;
-        if (lane < nw) {
-          sdt = ldx(dt_row, dt_d, tg * dt_t);
-          sa = ldx(aa_row, aa_d, tg * aa_t);
-          str = ldx(tr_row, tr_d, tg * tr_t);
-        }
-        const int tn = n0t + TOK;
-        if (lane == TOK - 1 && tn < L) {
-          ldt = ldx(dt_row, dt_d, tn * dt_t);
-          ltr = ldx(tr_row, tr_d, tn * tr_t);
-        }
-      }
-      if (ph_on) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tt = 4 * pg + i;
-          const int tg = n0t + tt;
-          pa[i] = 0.f;
-          if (tt < nw) pa[i] = angles ? prep_row[tg * PW + g.prep_a + ps] : ph_row[tg * ph_t];
         }
       }
     }
 
-    if (c >= 0) {
-      // (5) outputs for query row tile `it` and P tiles pj = wp, wp + WPR, ...
-      const int it = w / WPR, wp = w - it * WPR;
-      const int trow = 16 * it + l16;
-      const int tq = trow / R;
-      const float cum_t = SC[Lay::CUM + tq];
-      const float gam_t = SC[Lay::GAM + tq];
-      // decayed scores W[t, s] = Sc[t, s] * d[t, s] in FP32 (D-layout: rows s, column t)
-      // 16-bit: the query rows of this tile, B operand of the scores and A operand of inter
-      typename M::v8 qv[F32 ? 1 : NP / 32];
+    // state carry: S^T = exp(cum_last) S^T + K^T Vs
+    const float ecl = SC[Lay::ECL];
+#pragma unroll
+    for (int k = 0; k < kTiles; ++k) {
+      const int u = w + kWaves * k;
+      if (u >= n_tiles) continue;
+      const int ni = u / kPT, pj = u - ni * kPT;
+      const int nrow = 16 * ni + l16, prow = 16 * pj + l16;
+      f4 cacc = zero4();
       if constexpr (!F32) {
 #pragma unroll
-        for (int kk = 0; kk < NP / 32; ++kk) {
-          qv[kk] = *reinterpret_cast<const typename M::v8*>(Qs + trow * LQ + 32 * kk + 8 * lg);
+        for (int kk = 0; kk < ROWS; kk += 32) {
+          const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
+              KT + nrow * LR + swz<ROWS>(kk + 8 * lg, nrow >> 3));
+          const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
+              VsT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> 2));
+          cacc = M::mma(av, bv, cacc);
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < ROWS; kk += 4) {
+          cacc = M::mma(KT[nrow * LR + swz<ROWS>(kk + lg, nrow >> 3)],
+                        VsT[prow * LR + swz<ROWS>(kk + lg, prow >> 2)], cacc);
         }
       }
-      f4 wsc[RT];
 #pragma unroll
-      for (int sj = 0; sj < RT; ++sj) {
-        wsc[sj] = zero4();
-        if (sj > it) continue;
-        f4 acc = zero4();
-        if constexpr (!F32) {
-#pragma unroll
-          for (int kk = 0; kk < NP / 32; ++kk) {
-            const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
-                Ks + (16 * sj + l16) * LQ + 32 * kk + 8 * lg);
-            acc = M::mma(av, qv[kk], acc);
-          }
-        } else {
-#pragma unroll 8
-          for (int kk = 0; kk < NP; kk += 4) {
-            acc = M::mma(Ks[(16 * sj + l16) * LQ + kk + lg], Qs[trow * LQ + kk + lg], acc);
-          }
-        }
-        if (sj < it) {
-          // strictly earlier tile: d = exp(cum_t - cend) * (scale_s exp(cend - cum_s)), both <= 1
-          const float at = __expf(cum_t - SC[Lay::CEND + sj]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int ts = (16 * sj + 4 * lg + i) / R;
-            wsc[sj][i] = acc[i] * (at * SC[Lay::BSC + ts]);
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int ts = (16 * sj + 4 * lg + i) / R;
-            const float d = tq > ts ? SC[Lay::SCL + ts] * __expf(cum_t - SC[Lay::CUM + ts])
-                                    : (tq == ts ? gam_t : 0.f);
-            wsc[sj][i] = acc[i] * d;
-          }
-        }
-      }
-      float ecum[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ecum[i] = SC[Lay::ECUM + (16 * it + 4 * lg + i) / R];
-      for (int pj = wp; pj < kPT; pj += WPR) {
-        const int pcol = 16 * pj + l16;
-        const int key = pcol >> 2;
-        f4 yi = zero4(), ye = zero4();
-        if constexpr (!F32) {
-          // intra: W V with the K axis permuted as the D-layout of wsc
-#pragma unroll
-          for (int m = 0; m < (RT + 1) / 2; ++m) {
-            if (2 * m > it) continue;
-            typename M::v8 av, bv;
-            const typename M::v4 b0 = *reinterpret_cast<const typename M::v4*>(
-                VT + pcol * LR + swz<ROWS>(32 * m + 4 * lg, key));
-            const typename M::v4 b1 = *reinterpret_cast<const typename M::v4*>(
-                VT + pcol * LR + swz<ROWS>(32 * m + 16 + 4 * lg, key));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              av[i] = from_f<T>(wsc[2 * m][i]);
-              av[4 + i] = from_f<T>(2 * m + 1 < RT ? wsc[2 * m + 1][i] : 0.f);
-              bv[i] = b0[i];
-              bv[4 + i] = b1[i];
-            }
-            yi = M::mma(av, bv, yi);
-          }
-          // inter: Q rnd(S)^T
-#pragma unroll
-          for (int kk = 0; kk < NP / 32; ++kk) {
-            const typename M::v8 bv =
-                *reinterpret_cast<const typename M::v8*>(Sb + pcol * LQ + 32 * kk + 8 * lg);
-            ye = M::mma(qv[kk], bv, ye);
-          }
-        } else {
-#pragma unroll
-          for (int sj = 0; sj < RT; ++sj) {
-            if (sj > it) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              yi = M::mma(wsc[sj][i], VT[pcol * LR + swz<ROWS>(16 * sj + 4 * lg + i, key)], yi);
-            }
-          }
-#pragma unroll 8
-          for (int kk = 0; kk < NP; kk += 4) {
-            ye = M::mma(Qs[trow * LQ + kk + lg], Sb[pcol * LQ + kk + lg], ye);
-          }
-        }
-        // epilogue: rows 16 it + 4 lg + i, column pcol
-        if (pcol < P) {
-          float vv[4], zz[4];
-          if constexpr (!F32) {
-            const typename M::v4 v4 = *reinterpret_cast<const typename M::v4*>(
-                VT + pcol * LR + swz<ROWS>(16 * it + 4 * lg, key));
-            const typename M::v4 z4 = *reinterpret_cast<const typename M::v4*>(
-                ZT + pcol * LR + swz<ROWS>(16 * it + 4 * lg, key));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { vv[i] = to_f(v4[i]); zz[i] = to_f(z4[i]); }
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              vv[i] = VT[pcol * LR + swz<ROWS>(16 * it + 4 * lg + i, key)];
-              zz[i] = ZT[pcol * LR + swz<ROWS>(16 * it + 4 * lg + i, key)];
-            }
-          }
-          float y = 0.f;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int row = 16 * it + 4 * lg + i;
-            const int tt = row / R, r = row - tt * R;
-            float yr = (fmaf(ye[i], ecum[i], yi[i]) + Dh * vv[i]) *
-                       __fdividef(zz[i], 1.f + __expf(-zz[i]));
-            if (R > 1) yr *= F[Lay::MO + r * kPPad + pcol];
-            y = (R > 1 && r > 0) ? y + yr : yr;
-            if (r == R - 1 && tt < width) out_row[(t0 + tt) * out_t + pcol] = from_f<T>(y);
-          }
-        }
-      }
+      for (int i = 0; i < 4; ++i) st[k][i] = fmaf(ecl, st[k][i], cacc[i]);
+    }
 
-      // (6) state carry: S^T = exp(cum_last) S^T + K^T Vs
-      const float ecl = SC[Lay::ECL];
-#pragma unroll
-      for (int k = 0; k < kTiles; ++k) {
-        const int u = w + kWaves * k;
-        if (u >= n_tiles) continue;
-        const int ni = u / kPT, pj = u - ni * kPT;
-        const int nrow = 16 * ni + l16, prow = 16 * pj + l16;
-        f4 acc = zero4();
-        if constexpr (!F32) {
-#pragma unroll
-          for (int kk = 0; kk < ROWS; kk += 32) {
-            const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
-                KT + nrow * LR + swz<ROWS>(kk + 8 * lg, nrow >> 3));
-            const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
-                VsT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> 2));
-            acc = M::mma(av, bv, acc);
-          }
-        } else {
-#pragma unroll
-          for (int kk = 0; kk < ROWS; kk += 4) {
-            acc = M::mma(KT[nrow * LR + swz<ROWS>(kk + lg, nrow >> 3)],
-                         VsT[prow * LR + swz<ROWS>(kk + lg, prow >> 2)], acc);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) st[k][i] = fmaf(ecl, st[k][i], acc[i]);
+    // wave 0: scalars of sub-chunk c + 2, then the raw scalars of c + 3
+    if (w == 0 && c + 2 < nsub) {
+      scalar_stage<Lay, TOK, TPT>(scb(c + 2), scb(c + 1), t0 + 2 * TOK, L, lane, raw_dt, dt_bias,
+                                  sdt, sa, str);
+      if (c + 3 < nsub) {
+        fd.scalars_in(t0 + 3 * TOK, min(TOK, L - t0 - 3 * TOK), lane, sdt, sa, str);
       }
-    }  // c >= 0 (stages 5-6)
-
-    // (7) wave 0: per-token scalars of sub-chunk c + 1 (lane = token) into the other buffer
-    if (w == 0 && c + 1 < nsub) {
-      const int tb = t0 + TOK, wn = min(TOK, L - tb);
-      float* SCn = F + (((c + 1) & 1) ? Lay::SC1 : Lay::SC0);
-      const bool tv = lane < wn;
-      float dt = 0.f, adt = 0.f, tr = 0.f;
-      if (tv) {
-        dt_adt(raw_dt, sdt, sa, dt_bias, dt, adt);
-        tr = sigmoidf(str);
-      }
-      float right = __shfl_down(dt * (1.f - tr), 1);
-      if (lane == TOK - 1) {
-        right = 0.f;
-        if (tb + TOK < L) {
-          float dtn, adtn;
-          dt_adt(raw_dt, ldt, 0.f, dt_bias, dtn, adtn);
-          right = dtn * (1.f - sigmoidf(ltr));
-        }
-      }
-      if (tb + lane + 1 >= L) right = 0.f;
-      const float gamma = dt * tr;
-      const float scale = gamma + right;
-      const float cum = wave_incl_scan(tv ? adt : 0.f, lane);
-      const float cum_last = __shfl(cum, wn - 1);
-      const float cv = tv ? cum : cum_last;
-      const float cend = __shfl(cv, min(lane | (TPT - 1), wn - 1));
-      SCn[Lay::DTV + lane] = tv ? dt : 0.f;
-      SCn[Lay::CUM + lane] = cv;
-      SCn[Lay::ECUM + lane] = tv ? __expf(cv) : 0.f;
-      SCn[Lay::SCL + lane] = tv ? scale : 0.f;
-      SCn[Lay::GAM + lane] = tv ? gamma : 0.f;
-      SCn[Lay::VSF + lane] = tv ? scale * __expf(cum_last - cv) : 0.f;
-      SCn[Lay::BSC + lane] = tv ? scale * __expf(cend - cv) : 0.f;
-      if (lane < TOK && (lane & (TPT - 1)) == 0) SCn[Lay::CEND + lane / TPT] = cend;
-      if (lane == 0) SCn[Lay::ECL] = __expf(cum_last);
     }
     __syncthreads();
   }
@@ -1003,6 +1272,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     }
   }
 }
+
 
 // ------------------------------------------------------------------ host side
 
@@ -1039,13 +1309,73 @@ static size_t workspace_bytes(const m3_scan_args& a, int prep_w) {
   return static_cast<size_t>(a.batch) * a.length * prep_w * sizeof(float);
 }
 
-// The model's own shape in projection form: the specialization with every shape and mode a
-// compile-time constant.
-static bool full_shape(const m3_scan_args& a, const ScanGeom& g, int R) {
+// Projection form: q, k, value, gate, dt, a, trap all of the activation dtype and slices of one
+// projection row (same batch and token strides, every slice's per-token extent inside one token
+// row), out token-major, and every offset the kernel forms below 2^31 bytes. Fills the byte
+// geometry of `g`.
+static bool projection_form(const m3_scan_args& a, ScanGeom& g, int es) {
+  const m3_tensor* ts[7] = {&a.q, &a.k, &a.value, &a.gate, &a.dt, &a.a, &a.trap};
+  for (const m3_tensor* t : ts) {
+    if (t->dtype != a.act_dtype || t->stride[0] != a.q.stride[0] ||
+        t->stride[1] != a.q.stride[1]) {
+      return false;
+    }
+  }
+  for (int i = 2; i < 5; ++i) {
+    if (a.k.stride[i] != a.q.stride[i]) return false;
+  }
+  for (int i = 2; i < 4; ++i) {
+    if (a.gate.stride[i] != a.value.stride[i]) return false;
+  }
+  if (a.a.stride[2] != a.dt.stride[2] || a.trap.stride[2] != a.dt.stride[2]) return false;
+  const int64_t lim = INT32_MAX;
+  const int64_t tok = a.q.stride[1] * es;
+  const int64_t ext_q = ((a.groups - 1) * a.q.stride[2] + (a.rank - 1) * a.q.stride[3] +
+                         a.d_state) * es;
+  const int64_t ext_v = ((a.heads - 1) * a.value.stride[2] + a.head_dim) * es;
+  const int64_t ext_s = ((a.heads - 1) * a.dt.stride[2] + 1) * es;
+  const int64_t ext[7] = {ext_q, ext_q, ext_v, ext_v, ext_s, ext_s, ext_s};
+  const char* base = static_cast<const char*>(a.q.ptr);
+  for (const m3_tensor* t : ts) base = std::min(base, static_cast<const char*>(t->ptr));
+  int64_t off[7];
+  for (int i = 0; i < 7; ++i) {
+    off[i] = static_cast<const char*>(ts[i]->ptr) - base;
+    if (off[i] + ext[i] > tok) return false;
+  }
+  const int64_t out_tok = a.out.stride[1] * es;
+  if (((a.heads - 1) * a.out.stride[2] + a.head_dim) * es > out_tok) return false;
+  const int64_t len = a.length;
+  if (len * tok >= lim || len * out_tok >= lim || len * g.prep_w * 4 >= lim) {
+    return false;
+  }
+  g.proj = base;
+  g.proj_b = a.q.stride[0] * es;
+  g.tok_b = static_cast<int>(tok);
+  g.o_q = static_cast<int>(off[0]);
+  g.o_k = static_cast<int>(off[1]);
+  g.o_v = static_cast<int>(off[2]);
+  g.o_z = static_cast<int>(off[3]);
+  g.o_dt = static_cast<int>(off[4]);
+  g.o_a = static_cast<int>(off[5]);
+  g.o_tr = static_cast<int>(off[6]);
+  g.qk_g = static_cast<int>(a.q.stride[2] * es);
+  g.qk_r = static_cast<int>(a.q.stride[3] * es);
+  g.vz_h = static_cast<int>(a.value.stride[2] * es);
+  g.sc_h = static_cast<int>(a.dt.stride[2] * es);
+  g.out_b = a.out.stride[0] * es;
+  g.out_t = static_cast<int>(out_tok);
+  g.out_h = static_cast<int>(a.out.stride[2] * es);
+  return true;
+}
+
+// The model's own shape (N = 128, P = 64, S = 32, norm, bias, raw dt, angle phases, the rank's
+// rotation) in projection form: the specialization with every shape and mode a compile-time
+// constant and guard-free buffer addressing.
+static bool full_shape(const m3_scan_args& a, ScanGeom& g, int R) {
   return a.d_state == kNPad && a.head_dim == kPPad && a.num_angles == kSMax &&
          a.q_norm_w.ptr != nullptr && a.q_bias.ptr != nullptr && a.raw_dt != 0 &&
          a.phase_mode == M3_PHASE_ANGLES && (a.mimo_rotation != 0) == (R > 1) && g.vec_qk &&
-         g.vec_vz;
+         g.vec_vz && projection_form(a, g, a.act_dtype == M3_F32 ? 4 : 2);
 }
 
 template <typename T, int R, bool FULL>
@@ -1068,7 +1398,7 @@ static int launch_kernel(const m3_scan_args& a, const ScanGeom& g, const float* 
 
 template <typename T, int R>
 static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
-  const ScanGeom g = make_geom<T>(a);
+  ScanGeom g = make_geom<T>(a);
   static_assert(Layout<T>::BYTES <= 160 * 1024, "LDS layout exceeds 160 KiB");
   const float* prep = nullptr;
   if (g.prep_w > 0) {
@@ -1088,7 +1418,9 @@ static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
     }
   }
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kThreads);
-  if (full_shape(a, g, R)) return launch_kernel<T, R, true>(a, g, prep, grid, block, stream);
+  if (full_shape(a, g, R) && prep != nullptr) {
+    return launch_kernel<T, R, true>(a, g, prep, grid, block, stream);
+  }
   return launch_kernel<T, R, false>(a, g, prep, grid, block, stream);
 }
 
