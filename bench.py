@@ -2,13 +2,15 @@
 
 Headline workload: the SISO prefill scan of
 ``Mamba3(d_model=1024, d_state=128, depth=1, mimo_rank=1)`` on ``x [8, 8192, 1024]`` under
-bf16 autocast, seed 1. A step is one pass of the fused scan kernel (``m3_scan_fwd``:
-B/C RMSNorm, dt / A, bounded phase, bias, rotation, chunked SSD, D skip, SiLU gate) over the
-whole batch, with its input, the ``in_proj`` output, already resident in HBM. ``value`` is
-prefill tokens/s of that kernel. Also reported, in the same JSON line:
+bf16 autocast, seed 1. A step is one ``m3_scan_fwd`` call (its per-token prep kernel: B/C
+RMSNorm factors and pi tanh(angle); then the scan kernel: dt / A, bounded phase, bias,
+rotation, chunked SSD, D skip, SiLU gate) over the whole batch, with its input, the
+``in_proj`` output, already resident in HBM, timed with HIP events on the launch stream.
+``value`` is prefill tokens/s of that call. Also reported, in the same JSON line:
 
-* ``roofline``: the scan kernel against the HBM roof (its binding roof: arithmetic intensity
-  ~201 flop/B at the reference chunk is below the MI355X ridge of ~315 flop/B);
+* ``roofline``: the call against the HBM roof (its binding roof: arithmetic intensity
+  ~201 flop/B at the reference chunk is below the MI355X ridge of ~315 flop/B), ``traffic``
+  from the committed PMC summary ``profiles/scan_config2_pmc.txt``;
   ``roofline_mfma``: the same kernel against dense bf16 MFMA;
 * ``forward``: tokens/s of the whole mixer forward (norm, in_proj, scan, out_proj, residual);
 * ``decode``: BASELINE.json configs[3], ``Mamba3(2048, 128, 24, 1)`` with bf16 weights and an
@@ -17,7 +19,8 @@ prefill tokens/s of that kernel. Also reported, in the same JSON line:
 * ``cpu_baseline``: the CPU oracle (a restatement of the reference's portable path) on a
   bounded sample of the same scan, on this host's cores.
 
-Usage: ``python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-decode] [--no-cpu]``.
+Usage: ``python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-decode] [--no-cpu]
+[--copy-probe]``.
 """
 
 from __future__ import annotations
@@ -68,7 +71,23 @@ def _events_time(fn, iters):
     return start.elapsed_time(end) / 1000.0
 
 
-def bench_prefill(steps, warmup, log):
+def _traffic_from_profile(path):
+    """HBM bytes per m3_scan_fwd call as recorded by the committed PMC summary (or None).
+
+    The summary holds one line ``traffic_bytes_per_call: <int>``: FETCH_SIZE and WRITE_SIZE
+    of the prep and scan kernels, each scaled by the counter's reading for a copy of known size.
+    """
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_call:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
+
+
+def bench_prefill(steps, warmup, log, copy_probe=False):
     from mamba3_amd import Mamba3, ops
 
     dev = torch.device("cuda:0")
@@ -82,15 +101,12 @@ def bench_prefill(steps, warmup, log):
     with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
         proj = mixer.in_proj(model.layers[0].norm(x))
         torch.cuda.synchronize()
-        chunk = mixer.inference_chunk_size
-
-        def scan():
-            ops.scan_projection(proj, mixer, chunk_size=chunk)
-
+        # one prepared m3_scan_fwd call (prep + scan kernels), relaunched back to back
+        call = ops.ScanCall(proj, mixer, chunk_size=mixer.inference_chunk_size)
         for _ in range(warmup):
-            scan()
+            call.launch()
         assert ops._HIP_LAST_SCAN_DISPATCH
-        t_scan = _events_time(scan, steps)
+        t_scan = _events_time(call.launch, steps)
 
         def forward():
             model(x)
@@ -99,6 +115,13 @@ def bench_prefill(steps, warmup, log):
             forward()
         fwd_iters = max(3, steps // 4)
         t_fwd = _events_time(forward, fwd_iters)
+    if copy_probe:
+        # a plain 1 GiB device copy: the reference reading for the PMC byte counters
+        src_buf = torch.ones(256 * 1024 * 1024, device=dev)
+        dst_buf = torch.empty_like(src_buf)
+        dst_buf.copy_(src_buf)
+        torch.cuda.synchronize()
+        del src_buf, dst_buf
     per_launch = t_scan / steps
     tokens = batch * length
     proj_size = mixer.in_proj.weight.shape[0]
@@ -107,13 +130,16 @@ def bench_prefill(steps, warmup, log):
     flops_own = prefill_flops(batch, length, mixer.nheads, 128, mixer.headdim, 1, 64)
     gbs = nbytes / per_launch / 1e9
     tflops = flops_ref / per_launch / 1e12
+    traffic = _traffic_from_profile(os.path.join(ROOT, "profiles", "scan_config2_pmc.txt"))
     log(f"prefill scan: {per_launch * 1e3:.3f} ms/launch, {tokens / per_launch:.4e} tok/s, "
         f"{gbs:.0f} GB/s, {tflops:.1f} TFLOP/s (C_ref=256)")
     return dict(
         per_launch=per_launch, tokens=tokens, t_total=t_scan,
         roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                      frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
-                      kernel="m3::scan_kernel<__bf16, 1>", bytes_per_launch=nbytes),
+                      frac=round(gbs / HBM_PEAK_GBS, 4), traffic=traffic,
+                      kernel="m3_scan_fwd: m3::prep_kernel<__bf16> + "
+                             "m3::scan_kernel<__bf16, 1, true>",
+                      us_per_launch=round(per_launch * 1e6, 2), bytes_per_launch=nbytes),
         roofline_mfma=dict(bound="mfma", achieved=round(tflops, 1), peak=MFMA_BF16_PEAK_TFLOPS,
                            unit="TFLOP/s", frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                            flops_per_launch_at_c256=flops_ref,
@@ -236,6 +262,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-tokens", type=int, default=8192)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 1 GiB device copy (calibrates PMC byte counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -247,7 +275,7 @@ def main() -> None:
     def log(msg):
         print(msg, file=sys.stderr, flush=True)
 
-    pre = bench_prefill(args.steps, args.warmup, log)
+    pre = bench_prefill(args.steps, args.warmup, log, copy_probe=args.copy_probe)
     decode = None
     if not args.no_decode:
         decode = bench_decode(args.decode_batch, args.decode_steps, log)

@@ -60,7 +60,21 @@ __device__ __forceinline__ float heavy_tail(float x) {
 }
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
+
+// The same with the hardware exp and reciprocal (about 2 ulp), for the scan's per-token stage.
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __expf(-x));
+}
+__device__ __forceinline__ float heavy_tail_fast(float x) {
+  return x >= 0.f ? 1.f + x : __builtin_amdgcn_rcpf(1.f - x);
+}
 __device__ __forceinline__ float siluf(float x) { return x / (1.f + expf(-x)); }
+
+// x * sigmoid(x) with the hardware exp and reciprocal (about 1 ulp each): the output gate of
+// the scan epilogue. exp(-x) = inf gives x * 0 = -0 for large negative x.
+__device__ __forceinline__ float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.f + __expf(-x));
+}
 
 // dt and adt from the raw projection (model.py:195-198) or as given.
 __device__ __forceinline__ void dt_adt(bool raw, float dt_in, float a_in, float dt_bias,

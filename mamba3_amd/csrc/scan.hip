@@ -109,9 +109,9 @@ template <typename T> struct Layout {
   static constexpr int DTV = 0, CUM = 64, ECUM = 128, SCL = 192, GAM = 256, VSF = 320;
   static constexpr int BSC = 384, CEND = 448, ECL = 452, SCB = 464;
   static constexpr int SC0 = 0;
-  // cos / sin tables of one sub-chunk ([token][angle], token stride CSS for bank spread; sin at
-  // SNO after cos), two of them alternating
-  static constexpr int CSS = kSMax + 1, SNO = kTokMax * CSS, CSB = 2 * SNO;
+  // cos / sin tables of one sub-chunk: [token][angle][cos, sin] with token stride CST (16-byte
+  // aligned rows), two of them alternating
+  static constexpr int CST = 2 * kSMax + 4, CSB = kTokMax * CST;
   static constexpr int CS0 = SC0 + 3 * SCB, PBASE = CS0 + 2 * CSB;
   static constexpr int POFF = PBASE + kSMax, MX = POFF + kSMax, MZ = MX + kRMax * kPPad;
   static constexpr int MO = MZ + kRMax * kPPad;
@@ -254,44 +254,72 @@ __device__ __forceinline__ void st_row8(T* dst, const float* x) {
 
 // ------------------------------------------------------------------ prep
 
-// One wave per token: RMSNorm factors of the raw q / k rows and pi * tanh(angle).
+// Head-independent per-token work, once per token instead of once per head. Blocks below
+// `row_blocks`: one 16-lane group per raw q / k row (token, q|k, group, rank), 8 elements per lane,
+// its RMSNorm factor 1 / sqrt(mean(x^2) + eps) (model.py:190-191). The blocks after: one lane
+// per (token, angle), pi * tanh(angle) (model.py:225-228).
 template <typename T>
 __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const ScanGeom g,
-                                                   float* __restrict__ out) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + wave;
-  if (tok >= static_cast<int64_t>(a.batch) * a.length) return;
-  const int b = static_cast<int>(tok / a.length);
-  const int t = static_cast<int>(tok - static_cast<int64_t>(b) * a.length);
-  float* o = out + tok * g.prep_w;
-  const int N = a.d_state;
-  if (g.prep_q >= 0) {
-    for (int gr = 0; gr < a.groups * a.rank; ++gr) {
-      const int gi = gr / a.rank, r = gr - gi * a.rank;
+                                                   float* __restrict__ out, int row_blocks) {
+  // every index below fits 31 bits (checked by the host)
+  const int tid = threadIdx.x;
+  const int tokens = a.batch * a.length;
+  if (static_cast<int>(blockIdx.x) < row_blocks) {
+    const int gr_n = a.groups * a.rank;
+    const int row = static_cast<int>(blockIdx.x) * 16 + (tid >> 4);
+    if (row >= tokens * 2 * gr_n) return;  // whole 16-lane groups leave together
+    const int l16 = tid & 15;
+    const int tok = row / (2 * gr_n);
+    const int rem = row - tok * 2 * gr_n;
+    const int which = rem >= gr_n, gr = rem - which * gr_n;
+    const int gi = gr / a.rank, r = gr - gi * a.rank;
+    const int b = tok / a.length, t = tok - b * a.length;
+    const m3_tensor& x = which ? a.k : a.q;
+    const T* p = static_cast<const T*>(x.ptr) + b * x.stride[0] + t * x.stride[1] +
+                 gi * x.stride[2] + r * x.stride[3] + 8 * l16;
+    const int N = a.d_state;
+    float ss = 0.f;
+    if (g.vec_qk) {
+      if (8 * l16 < N) {
+        uint32_t w8[Words<T>::W8];
 #pragma unroll
-      for (int which = 0; which < 2; ++which) {
-        const m3_tensor& x = which ? a.k : a.q;
-        const T* p = static_cast<const T*>(x.ptr) + b * x.stride[0] + t * x.stride[1] +
-                     gi * x.stride[2] + r * x.stride[3];
-        float ss = 0.f;
-        for (int n = lane; n < N; n += 64) {
-          const float v = to_f(p[n]);
-          ss += v * v;
+        for (int j = 0; j < Words<T>::W8; j += 4) {
+          const uint4 q = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(p) + j);
+          w8[j] = q.x;
+          w8[j + 1] = q.y;
+          w8[j + 2] = q.z;
+          w8[j + 3] = q.w;
         }
-        ss = wave_sum(ss);
-        if (lane == 0) {
-          o[(which ? g.prep_k : g.prep_q) + gr] =
-              1.f / sqrtf(ss / static_cast<float>(N) + a.norm_eps);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float v = raw_get<T>(w8, i);
+          ss = fmaf(v, v, ss);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (8 * l16 + i < N) {
+          const float v = to_f(p[i]);
+          ss = fmaf(v, v, ss);
         }
       }
     }
-  }
-  if (g.prep_a >= 0) {
-    for (int s = lane; s < a.num_angles; s += 64) {
-      const float th = ldx(a.phase.ptr, a.phase.dtype,
-                           b * a.phase.stride[0] + t * a.phase.stride[1] + s * a.phase.stride[2]);
-      o[g.prep_a + s] = __fmul_rn(kPi, tanhf(th));
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+    if (l16 == 0) {
+      out[static_cast<int64_t>(tok) * g.prep_w + (which ? g.prep_k : g.prep_q) + gr] =
+          1.f / sqrtf(ss / static_cast<float>(N) + a.norm_eps);
     }
+  } else {
+    const int S = a.num_angles;
+    const int i = (static_cast<int>(blockIdx.x) - row_blocks) * 256 + tid;
+    if (i >= tokens * S) return;
+    const int tok = i / S, s = i - tok * S;
+    const int b = tok / a.length, t = tok - b * a.length;
+    const float th = ldx(a.phase.ptr, a.phase.dtype,
+                         b * a.phase.stride[0] + t * a.phase.stride[1] + s * a.phase.stride[2]);
+    out[static_cast<int64_t>(tok) * g.prep_w + g.prep_a + s] = __fmul_rn(kPi, tanhf(th));
   }
 }
 
@@ -579,49 +607,78 @@ struct Feed {
 // dt, the within-chunk cumsum of adt and exp of it, gamma = dt sigmoid(trap), the exp-trapezoid
 // scale = gamma + dt' (1 - sigmoid(trap')) of the next token (ops.py:659-671), and the
 // products with the decays the scores and the carry use. The last token's next-token term
-// belongs to the first token of the following sub-chunk: the call for that sub-chunk adds it
-// into SCp (the previous block), where exp(cum_last - cum_last) = 1 makes it a plain add.
+// belongs to the first token of the following sub-chunk: the call for that sub-chunk writes
+// the previous block's last entries (SCp), gamma_last + that term, exp(cum_last - cum_last)
+// being 1; `gprev` carries gamma_last from call to call.
 template <typename Lay, int TOK, int TPT>
 __device__ __forceinline__ void scalar_stage(float* SCn, float* SCp, int tb, int L, int lane,
                                              bool raw_dt, float dt_bias, float sdt, float sa,
-                                             float str) {
+                                             float str, float& gprev) {
   const int wn = min(TOK, L - tb);
   const bool tv = lane < wn;
   float dt = 0.f, adt = 0.f, tr = 0.f;
-  if (tv) {
-    dt_adt(raw_dt, sdt, sa, dt_bias, dt, adt);
-    tr = sigmoidf(str);
+  if (raw_dt) {
+    dt = softplus(sdt + dt_bias);
+    adt = fminf(-heavy_tail_fast(sa), -kAFloor) * dt;
+  } else {
+    dt = sdt;
+    adt = sa;
   }
+  tr = sigmoid_fast(str);
+  if (!tv) dt = adt = tr = 0.f;
   const float lead = dt * (1.f - tr);  // this token's term of the previous token's scale
-  float right = __shfl_down(lead, 1);
+  // lane l + 1's value (DPP wave_shl:1; lane 63 reads 0)
+  float right = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                              0, __builtin_bit_cast(int, lead), 0x130, 0xf, 0xf,
+                                              true));
   if (lane >= wn - 1) right = 0.f;
+  const float lead0 = readlane_f(lead, 0);
   if (SCp != nullptr && lane == 0) {
-    SCp[Lay::SCL + TOK - 1] += lead;
-    SCp[Lay::VSF + TOK - 1] += lead;
-    SCp[Lay::BSC + TOK - 1] += lead;
+    const float sl = gprev + lead0;
+    SCp[Lay::SCL + TOK - 1] = sl;
+    SCp[Lay::VSF + TOK - 1] = sl;
+    SCp[Lay::BSC + TOK - 1] = sl;
   }
   const float gamma = dt * tr;
+  gprev = readlane_f(gamma, TOK - 1);
   const float scale = gamma + right;
-  const float cum = wave_incl_scan(tv ? adt : 0.f, lane);
-  const float cum_last = __shfl(cum, wn - 1);
+  const float cum = wave_incl_scan(adt, lane);
+  const float cum_last = readlane_f(cum, wn - 1);
   const float cv = tv ? cum : cum_last;
-  const float cend = __shfl(cv, min(lane | (TPT - 1), wn - 1));
-  SCn[Lay::DTV + lane] = tv ? dt : 0.f;
+  // cum at the end of this lane's 16-row tile (TPT tokens), clamped to the last valid token
+  float cend;
+  if constexpr (TPT == 16) {
+    const float e0 = readlane_f(cv, 15), e1 = readlane_f(cv, 31), e2 = readlane_f(cv, 47);
+    const float e3 = readlane_f(cv, 63);
+    const int grp = lane >> 4;
+    cend = grp == 0 ? e0 : (grp == 1 ? e1 : (grp == 2 ? e2 : e3));
+  } else {
+    cend = __shfl(cv, min(lane | (TPT - 1), wn - 1));
+  }
+  SCn[Lay::DTV + lane] = dt;
   SCn[Lay::CUM + lane] = cv;
   SCn[Lay::ECUM + lane] = tv ? __expf(cv) : 0.f;
   SCn[Lay::SCL + lane] = tv ? scale : 0.f;
-  SCn[Lay::GAM + lane] = tv ? gamma : 0.f;
+  SCn[Lay::GAM + lane] = gamma;
   SCn[Lay::VSF + lane] = tv ? scale * __expf(cum_last - cv) : 0.f;
   SCn[Lay::BSC + lane] = tv ? scale * __expf(cend - cv) : 0.f;
   if (lane < TOK && (lane & (TPT - 1)) == 0) SCn[Lay::CEND + lane / TPT] = cend;
   if (lane == 0) SCn[Lay::ECL] = __expf(cum_last);
 }
 
+// Column of angle `col` in the cos / sin table row of token tt. SWZ (64-token sub-chunks, 32
+// angles): blocks of 4 angles are XOR-swizzled by the token's 16-token block, spreading the
+// phase stage's column writes over the LDS banks while a reader's 4-angle block stays whole.
+template <bool SWZ>
+__device__ __forceinline__ int cs_col(int col, int tt) {
+  return SWZ ? col ^ (4 * ((tt >> 4) & 3)) : col;
+}
+
 // Bounded phase (model.py:215-256) of tokens 4pg .. 4pg+3 of the sub-chunk at t0 for angle ps:
 // fmod-reduced increments summed within 64-token blocks, an fmod-reduced carry between blocks,
-// the running block sum and carry in pbase / poff; cos / sin into the tables.
-template <int PG, int CSS>
-__device__ __forceinline__ void phase_stage(float* cs, float* sn, float* pbase, float* poff,
+// the running block sum and carry in pbase / poff; cos / sin into the table of angle ps.
+template <int PG, int CST, bool SWZ>
+__device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, float* poff,
                                             const float* dtv, int t0, int L, int pg, int lane,
                                             bool angles, const float (&pa)[4], float* fph) {
   const int width = min(4 * PG, L - t0);
@@ -632,7 +689,7 @@ __device__ __forceinline__ void phase_stage(float* cs, float* sn, float* pbase, 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tt = 4 * pg + i;
-      x[i] = tt < width ? __fmul_rn(pa[i], dtv[tt]) : 0.f;
+      x[i] = __fmul_rn(pa[i], dtv[tt]);  // dt is 0 past the sub-chunk's last token
       big = big || !(fabsf(x[i]) < 1048576.0f);
     }
     float inc[4];
@@ -651,7 +708,10 @@ __device__ __forceinline__ void phase_stage(float* cs, float* sn, float* pbase, 
       cpre[i] = run;
     }
     const float incl = seg_incl_scan<PG>(run, lane);
-    const float excl = __fsub_rn(incl, run);
+    // the previous lane's inclusive sum: sums of earlier tokens only (incl - run would round in
+    // the later tokens of this lane's group)
+    float excl = dpp_shr<0x111>(incl);
+    if (pg == 0) excl = 0.f;
     float base = *pbase, off = *poff;
     if ((t0 & 63) == 0 && t0 > 0) {
       off = m3_fmod_2pi_small(__fadd_rn(off, base));
@@ -674,10 +734,9 @@ __device__ __forceinline__ void phase_stage(float* cs, float* sn, float* pbase, 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int tt = 4 * pg + i;
-    float sv, cv;
-    __sincosf(ph[i], &sv, &cv);
-    cs[tt * CSS] = cv;
-    sn[tt * CSS] = sv;
+    float2 v;
+    __sincosf(ph[i], &v.y, &v.x);
+    *reinterpret_cast<float2*>(tab + tt * CST + 2 * cs_col<SWZ>(ps, tt)) = v;
   }
 }
 
@@ -694,7 +753,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   constexpr int PG = TOK / 4;          // phase lanes per angle (4 tokens each)
   constexpr bool F32 = sizeof(T) == 4;
   constexpr int ES = sizeof(T);
-  constexpr int LQ = Lay::LQ, LR = Lay::LR, NP = kNPad, CSS = Lay::CSS;
+  constexpr int LQ = Lay::LQ, LR = Lay::LR, NP = kNPad, CST = Lay::CST;
+  // SISO model shape: q / k lanes split by column half, waves 0-3 holding the rotated columns
+  constexpr bool SPLIT = FULL && R == 1 && !F32;
   // FULL: the model's shape (N = 128, P = 64, S = 32) in projection form with vector loads
   const int N = FULL ? kNPad : a.d_state;
   const int P = FULL ? kPPad : a.head_dim;
@@ -707,7 +768,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   const bool mimo_rot = FULL ? (R > 1) : (a.mimo_rotation != 0);
   const bool vec_qk = FULL || g.vec_qk, vec_vz = FULL || g.vec_vz;
   const int H = a.heads, L = a.length;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (wave-uniform)
   const int l16 = lane & 15, lg = lane >> 4;
 
   // ---- block -> (b, h): with xcd_map the blocks of one XCD (blockIdx % 8) take consecutive
@@ -733,8 +795,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   const float Dh = ldx(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
 
   // ---- lane roles
-  // q / k: row pair rp (rows 2rp, 2rp+1), columns n0 .. n0+7
-  const int rp = tid >> 4, n0 = 8 * (tid & 15);
+  // q / k: row pair rp (rows 2rp, 2rp+1), columns n0 .. n0+7 (SPLIT: waves 0-3 columns 0-63,
+  // waves 4-7 columns 64-127)
+  const int rp = SPLIT ? (tid & 255) >> 3 : tid >> 4;
+  const int n0 = SPLIT ? 64 * (tid >> 8) + 8 * (tid & 7) : 8 * (tid & 15);
   const bool qk_on = rp < ROWS / 2 && n0 < N;
   const int qk_n = min(8, N - n0);
   // v / z: token pair vp (tokens 2vp, 2vp+1), columns p0 .. p0+3
@@ -903,6 +967,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   float fq[2] = {1.f, 1.f}, fk[2] = {1.f, 1.f};
   float pa[4] = {0.f, 0.f, 0.f, 0.f};
   float sdt = 0.f, sa = 0.f, str = 0.f;  // wave 0: raw scalars of a coming sub-chunk
+  float gprev = 0.f;                      // wave 0: gamma of the last scalar block's last token
   const int nsub = (L + TOK - 1) / TOK;
   auto scb = [&](int c) { return F + Lay::SC0 + (c % 3) * Lay::SCB; };
   auto csb = [&](int c) { return F + Lay::CS0 + (c & 1) * Lay::CSB; };
@@ -916,18 +981,19 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   fd.angle_in(0, min(TOK, L), ph_on, pa);
   if (w == 0 && nsub > 0) {
     fd.scalars_in(0, min(TOK, L), lane, sdt, sa, str);
-    scalar_stage<Lay, TOK, TPT>(scb(0), nullptr, 0, L, lane, raw_dt, dt_bias, sdt, sa, str);
+    scalar_stage<Lay, TOK, TPT>(scb(0), nullptr, 0, L, lane, raw_dt, dt_bias, sdt, sa, str,
+                                gprev);
     if (nsub > 1) {
       fd.scalars_in(TOK, min(TOK, L - TOK), lane, sdt, sa, str);
-      scalar_stage<Lay, TOK, TPT>(scb(1), scb(0), TOK, L, lane, raw_dt, dt_bias, sdt, sa, str);
+      scalar_stage<Lay, TOK, TPT>(scb(1), scb(0), TOK, L, lane, raw_dt, dt_bias, sdt, sa, str,
+                                  gprev);
     }
     if (nsub > 2) fd.scalars_in(2 * TOK, min(TOK, L - 2 * TOK), lane, sdt, sa, str);
   }
   __syncthreads();
   if (ph_on && nsub > 0) {
-    float* t = csb(0);
-    phase_stage<PG, CSS>(t + ps, t + Lay::SNO + ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
-                         scb(0) + Lay::DTV, 0, L, pg, lane, angles, pa, fph);
+    phase_stage<PG, CST, SPLIT>(csb(0), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
+                                scb(0) + Lay::DTV, 0, L, pg, lane, angles, pa, fph);
   }
   if (nsub > 1) fd.angle_in(TOK, min(TOK, L - TOK), ph_on, pa);
   __syncthreads();
@@ -951,7 +1017,25 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           q[i] = fmaf(raw_get<T>(rq[j], i), fq[j] * wq[i], bq[R == 1 ? 0 : j][i]);
           k[i] = fmaf(raw_get<T>(rk[j], i), fk[j] * wk[i], bk[R == 1 ? 0 : j][i]);
         }
-        if (rotate) {
+        if constexpr (SPLIT) {
+          // pairs (2j, 2j+1), j = n0/2 .. n0/2+3: the rotated columns are waves 0-3's
+          if (w < 4) {
+            const float* tr = CSt + tt * CST + 2 * cs_col<true>(n0 >> 1, tt);
+            const f4 c01 = *reinterpret_cast<const f4*>(tr);      // c0 s0 c1 s1
+            const f4 c23 = *reinterpret_cast<const f4*>(tr + 4);  // c2 s2 c3 s3
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+              const f4& cv = pp < 2 ? c01 : c23;
+              const float cc = cv[2 * (pp & 1)], ss = cv[2 * (pp & 1) + 1];
+              const float q0 = q[2 * pp], q1 = q[2 * pp + 1];
+              const float k0 = k[2 * pp], k1 = k[2 * pp + 1];
+              q[2 * pp] = fmaf(q0, cc, -(q1 * ss));
+              q[2 * pp + 1] = fmaf(q0, ss, q1 * cc);
+              k[2 * pp] = fmaf(k0, cc, -(k1 * ss));
+              k[2 * pp + 1] = fmaf(k0, ss, k1 * cc);
+            }
+          }
+        } else if (rotate) {
           // x' = x cos + sgn partner sin: SISO pairs (2j, 2j+1), MIMO pairs (n, n + N/2)
           float qp[8], kp[8];
 #pragma unroll
@@ -972,10 +1056,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           }
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const float cr = CSt[tt * CSS + rcol[i]];
-            const float sr = CSt[Lay::SNO + tt * CSS + rcol[i]];
-            const float cc = rsgn[i] != 0.f ? cr : 1.f;
-            const float ss = rsgn[i] * sr;
+            const float2 cs = *reinterpret_cast<const float2*>(CSt + tt * CST + 2 * rcol[i]);
+            const float cc = rsgn[i] != 0.f ? cs.x : 1.f;
+            const float ss = rsgn[i] * cs.y;
             q[i] = fmaf(qp[i], ss, q[i] * cc);
             k[i] = fmaf(kp[i], ss, k[i] * cc);
           }
@@ -1082,11 +1165,36 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
       }
     }
+    // K^T Vs products of the state carry, issued early: they depend only on staged tiles
+    f4 cacc[kTiles];
+#pragma unroll
+    for (int k = 0; k < kTiles; ++k) {
+      cacc[k] = zero4();
+      const int u = w + kWaves * k;
+      if (u >= n_tiles) continue;
+      const int ni = u / kPT, pj = u - ni * kPT;
+      const int nrow = 16 * ni + l16, prow = 16 * pj + l16;
+      if constexpr (!F32) {
+#pragma unroll
+        for (int kk = 0; kk < ROWS; kk += 32) {
+          const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
+              KT + nrow * LR + swz<ROWS>(kk + 8 * lg, nrow >> 3));
+          const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
+              VsT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> 2));
+          cacc[k] = M::mma(av, bv, cacc[k]);
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < ROWS; kk += 4) {
+          cacc[k] = M::mma(KT[nrow * LR + swz<ROWS>(kk + lg, nrow >> 3)],
+                           VsT[prow * LR + swz<ROWS>(kk + lg, prow >> 2)], cacc[k]);
+        }
+      }
+    }
     // phases of sub-chunk c + 1 (its dt block was computed two iterations ago)
     if (ph_on && c + 1 < nsub) {
-      float* t = csb(c + 1);
-      phase_stage<PG, CSS>(t + ps, t + Lay::SNO + ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
-                           scb(c + 1) + Lay::DTV, t0 + TOK, L, pg, lane, angles, pa, fph);
+      phase_stage<PG, CST, SPLIT>(csb(c + 1), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
+                                  scb(c + 1) + Lay::DTV, t0 + TOK, L, pg, lane, angles, pa, fph);
       if (c + 2 < nsub) fd.angle_in(t0 + 2 * TOK, min(TOK, L - t0 - 2 * TOK), ph_on, pa);
     }
     // decayed scores W[t, s] = Sc[t, s] d[t, s] in FP32
@@ -1118,7 +1226,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     float ecum[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) ecum[i] = SC[Lay::ECUM + (16 * it + 4 * lg + i) / R];
-    for (int pj = wp; pj < kPT; pj += WPR) {
+#pragma unroll
+    for (int pq = 0; pq < kPT / WPR; ++pq) {
+      const int pj = wp + pq * WPR;
       const int pcol = 16 * pj + l16;
       const int key = pcol >> 2;
       f4 yi = zero4(), ye = zero4();
@@ -1187,8 +1297,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         for (int i = 0; i < 4; ++i) {
           const int row = 16 * it + 4 * lg + i;
           const int tt = row / R, r = row - tt * R;
-          float yr = (fmaf(ye[i], ecum[i], yi[i]) + Dh * vv[i]) *
-                     __fdividef(zz[i], 1.f + __expf(-zz[i]));
+          float yr = (fmaf(ye[i], ecum[i], yi[i]) + Dh * vv[i]) * silu_fast(zz[i]);
           if (R > 1) yr *= F[Lay::MO + r * kPPad + pcol];
           y = (R > 1 && r > 0) ? y + yr : yr;
           if (r == R - 1) {
@@ -1203,39 +1312,18 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       }
     }
 
-    // state carry: S^T = exp(cum_last) S^T + K^T Vs
+    // state carry: S^T = exp(cum_last) S^T + K^T Vs (the products were issued above)
     const float ecl = SC[Lay::ECL];
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) {
-      const int u = w + kWaves * k;
-      if (u >= n_tiles) continue;
-      const int ni = u / kPT, pj = u - ni * kPT;
-      const int nrow = 16 * ni + l16, prow = 16 * pj + l16;
-      f4 cacc = zero4();
-      if constexpr (!F32) {
 #pragma unroll
-        for (int kk = 0; kk < ROWS; kk += 32) {
-          const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
-              KT + nrow * LR + swz<ROWS>(kk + 8 * lg, nrow >> 3));
-          const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
-              VsT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> 2));
-          cacc = M::mma(av, bv, cacc);
-        }
-      } else {
-#pragma unroll
-        for (int kk = 0; kk < ROWS; kk += 4) {
-          cacc = M::mma(KT[nrow * LR + swz<ROWS>(kk + lg, nrow >> 3)],
-                        VsT[prow * LR + swz<ROWS>(kk + lg, prow >> 2)], cacc);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st[k][i] = fmaf(ecl, st[k][i], cacc[i]);
+      for (int i = 0; i < 4; ++i) st[k][i] = fmaf(ecl, st[k][i], cacc[k][i]);
     }
 
     // wave 0: scalars of sub-chunk c + 2, then the raw scalars of c + 3
     if (w == 0 && c + 2 < nsub) {
       scalar_stage<Lay, TOK, TPT>(scb(c + 2), scb(c + 1), t0 + 2 * TOK, L, lane, raw_dt, dt_bias,
-                                  sdt, sa, str);
+                                  sdt, sa, str, gprev);
       if (c + 3 < nsub) {
         fd.scalars_in(t0 + 3 * TOK, min(TOK, L - t0 - 3 * TOK), lane, sdt, sa, str);
       }
@@ -1409,10 +1497,16 @@ static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
     }
     prep = static_cast<const float*>(a.workspace);
     const int64_t tokens = static_cast<int64_t>(a.batch) * a.length;
-    if (tokens > 0) {
-      const dim3 pgrid(static_cast<unsigned>((tokens + 3) / 4)), pblock(256);
+    const int64_t rows = g.prep_q >= 0 ? tokens * 2 * a.groups * a.rank : 0;
+    const int64_t ang = g.prep_a >= 0 ? tokens * a.num_angles : 0;
+    const int64_t row_blocks = (rows + 15) / 16, ang_blocks = (ang + 255) / 256;
+    if (rows >= INT32_MAX || ang >= INT32_MAX) {
+      return fail(M3_EUNSUPPORTED, "m3_scan_fwd: too many tokens for one launch");
+    }
+    if (row_blocks + ang_blocks > 0) {
+      const dim3 pgrid(static_cast<unsigned>(row_blocks + ang_blocks)), pblock(256);
       hipLaunchKernelGGL(prep_kernel<T>, pgrid, pblock, 0, stream, a, g,
-                         static_cast<float*>(a.workspace));
+                         static_cast<float*>(a.workspace), static_cast<int>(row_blocks));
       int rc = check_launch("m3_scan_fwd (prep)");
       if (rc != M3_OK) return rc;
     }

@@ -358,6 +358,67 @@ def split_projection(proj: torch.Tensor, mixer) -> dict[str, torch.Tensor]:
         dt=ddt, a=da, trap=trap, angles=ang, lead=lead)
 
 
+class ScanCall:
+    """One ``m3_scan_fwd`` launch over the raw ``in_proj`` output ``[B, L, proj]``, prepared once.
+
+    Holds the argument block, the outputs, the workspace and references to every tensor the
+    block points at; ``launch()`` enqueues the call on the device's current stream and may be
+    repeated (each launch rewrites the outputs). Fuses ``_project`` (B/C RMSNorm, dt, adt),
+    ``_phase``, bias, rotation and the chunked SSD (reference ``model.py:282-309``).
+    """
+
+    def __init__(self, proj: torch.Tensor, mixer, *, cache=None, want_cache: bool = False,
+                 chunk_size: int = 256):
+        self.device = _require_device(proj)
+        v = split_projection(proj, mixer)
+        batch, length = proj.shape[0], proj.shape[1]
+        h, p, n, r = mixer.nheads, mixer.headdim, mixer.d_state, mixer.mimo_rank
+        s = mixer.num_angles
+        act = proj.dtype
+        if cache is not None:
+            init_phase, init_state, init_k, init_v = cache
+            if init_k.dtype != act or init_v.dtype != act:
+                raise ValueError("K/value cache dtypes must match the activations")
+        else:
+            init_phase = init_state = init_k = init_v = None
+        dev = self.device
+        self.out = torch.empty(batch, length, h, p, device=dev, dtype=act)
+        self.final_state = torch.empty(batch, h, p, n, device=dev, dtype=torch.float32)
+        self.final_phase = (torch.empty(batch, h, s, device=dev, dtype=torch.float32)
+                            if want_cache else None)
+        self.final_k = torch.empty(batch, h, r, n, device=dev, dtype=act) if want_cache else None
+        args = _hip.ScanArgs(
+            batch=batch, length=length, heads=h, groups=1, rank=r, d_state=n, head_dim=p,
+            num_angles=s, chunk=chunk_size, act_dtype=_hip.dtype_code(act),
+            mimo_rotation=int(r > 1), raw_dt=1, phase_mode=_hip.PHASE_ANGLES,
+            norm_eps=NORM_EPS)
+        params = [_param(t) for t in (mixer.C_norm.weight, mixer.B_norm.weight, mixer.C_bias,
+                                      mixer.B_bias, mixer.dt_bias, mixer.D, mixer.mimo_x,
+                                      mixer.mimo_z, mixer.mimo_out)]
+        keep = [v["q"], v["k"], v["x"], v["z"], v["dt"], v["a"], v["trap"], v["angles"],
+                init_phase, None if init_state is None else _state32(init_state),
+                _inner(init_k), _inner(init_v), *params]
+        (args.q, args.k, args.value, args.gate, args.dt, args.a, args.trap, args.phase,
+         args.initial_phase, args.initial_state, args.initial_k, args.initial_value,
+         args.q_norm_w, args.k_norm_w, args.q_bias, args.k_bias, args.dt_bias, args.D,
+         args.mimo_x, args.mimo_z, args.mimo_out) = (_hip.tensor(t) for t in keep)
+        args.out = _hip.tensor(self.out)
+        args.final_state = _hip.tensor(self.final_state)
+        args.final_phase = _hip.tensor(self.final_phase)
+        args.final_k = _hip.tensor(self.final_k)
+        with torch.cuda.device(dev):
+            keep.append(_hip.scan_workspace(args, dev))
+        self.args = args
+        self._keep = keep
+
+    def launch(self) -> None:
+        global _HIP_LAST_SCAN_DISPATCH
+        _HIP_LAST_SCAN_DISPATCH = False
+        with torch.cuda.device(self.device):
+            _hip.call("m3_scan_fwd", self.args, self.device)
+        _HIP_LAST_SCAN_DISPATCH = True
+
+
 def scan_projection(proj: torch.Tensor, mixer, *, cache=None, want_cache: bool = False,
                     chunk_size: int = 256):
     """The whole mixer scan from the raw ``in_proj`` output ``[B, L, proj]``.
@@ -366,46 +427,9 @@ def scan_projection(proj: torch.Tensor, mixer, *, cache=None, want_cache: bool =
     SSD (reference ``model.py:282-309``). Returns ``(mixed [B,L,H,P], state, final_phase,
     final_k)``; the last two are ``None`` unless ``want_cache``.
     """
-    global _HIP_LAST_SCAN_DISPATCH
-    _HIP_LAST_SCAN_DISPATCH = False
-    device = _require_device(proj)
-    v = split_projection(proj, mixer)
-    batch, length = proj.shape[0], proj.shape[1]
-    h, p, n, r, s = mixer.nheads, mixer.headdim, mixer.d_state, mixer.mimo_rank, mixer.num_angles
-    act = proj.dtype
-    if cache is not None:
-        init_phase, init_state, init_k, init_v = cache
-        if init_k.dtype != act or init_v.dtype != act:
-            raise ValueError("K/value cache dtypes must match the activations")
-    else:
-        init_phase = init_state = init_k = init_v = None
-    out = torch.empty(batch, length, h, p, device=device, dtype=act)
-    final_state = torch.empty(batch, h, p, n, device=device, dtype=torch.float32)
-    final_phase = torch.empty(batch, h, s, device=device, dtype=torch.float32) if want_cache else None
-    final_k = torch.empty(batch, h, r, n, device=device, dtype=act) if want_cache else None
-    args = _hip.ScanArgs(
-        batch=batch, length=length, heads=h, groups=1, rank=r, d_state=n, head_dim=p,
-        num_angles=s, chunk=chunk_size, act_dtype=_hip.dtype_code(act),
-        mimo_rotation=int(r > 1), raw_dt=1, phase_mode=_hip.PHASE_ANGLES, norm_eps=NORM_EPS)
-    params = [_param(t) for t in (mixer.C_norm.weight, mixer.B_norm.weight, mixer.C_bias,
-                                  mixer.B_bias, mixer.dt_bias, mixer.D, mixer.mimo_x,
-                                  mixer.mimo_z, mixer.mimo_out)]
-    keep = [v["q"], v["k"], v["x"], v["z"], v["dt"], v["a"], v["trap"], v["angles"],
-            init_phase, None if init_state is None else _state32(init_state), _inner(init_k),
-            _inner(init_v), *params]
-    (args.q, args.k, args.value, args.gate, args.dt, args.a, args.trap, args.phase,
-     args.initial_phase, args.initial_state, args.initial_k, args.initial_value,
-     args.q_norm_w, args.k_norm_w, args.q_bias, args.k_bias, args.dt_bias, args.D,
-     args.mimo_x, args.mimo_z, args.mimo_out) = (_hip.tensor(t) for t in keep)
-    args.out = _hip.tensor(out)
-    args.final_state = _hip.tensor(final_state)
-    args.final_phase = _hip.tensor(final_phase)
-    args.final_k = _hip.tensor(final_k)
-    with torch.cuda.device(device):
-        keep.append(_hip.scan_workspace(args, device))
-        _hip.call("m3_scan_fwd", args, device)
-    _HIP_LAST_SCAN_DISPATCH = True
-    return out, final_state, final_phase, final_k
+    call = ScanCall(proj, mixer, cache=cache, want_cache=want_cache, chunk_size=chunk_size)
+    call.launch()
+    return call.out, call.final_state, call.final_phase, call.final_k
 
 
 def step_projection(proj: torch.Tensor, mixer, cache, *, inplace: bool = False):
@@ -432,4 +456,4 @@ def step_projection(proj: torch.Tensor, mixer, cache, *, inplace: bool = False):
 
 
 __all__ = ["heavy_tail_activation", "mamba3_scan", "mamba3_step", "fused_step", "chunk_state",
-           "scan_projection", "step_projection", "split_projection"]
+           "ScanCall", "scan_projection", "step_projection", "split_projection"]
