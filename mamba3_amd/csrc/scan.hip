@@ -104,25 +104,36 @@ template <typename T> struct Layout {
   static constexpr int ZT = al(VS + kPPad * LR * ES);
   static constexpr int SB = al(ZT + kPPad * LR * ES);
   static constexpr int FB = al(SB + kPPad * LQ * ES);
-  // float scratch, offsets in floats from FB. Per-token scalars of one sub-chunk (token-indexed,
-  // kTokMax each) form a block of SCB floats; three blocks rotate over consecutive sub-chunks.
-  static constexpr int DTV = 0, CUM = 64, ECUM = 128, SCL = 192, GAM = 256, VSF = 320;
-  static constexpr int BSC = 384, CEND = 448, ECL = 452, SCB = 464;
-  static constexpr int SC0 = 0;
+  // float scratch, offsets in floats from FB: two per-token scalar blocks (ScBlk) alternating
+  static constexpr int SCB = 7 * kTokMax + 8, SC0 = 0;
   // cos / sin tables of one sub-chunk: [token][angle][cos, sin] with token stride CST (16-byte
   // aligned rows), two of them alternating
   static constexpr int CST = 2 * kSMax + 4, CSB = kTokMax * CST;
-  static constexpr int CS0 = SC0 + 3 * SCB, PBASE = CS0 + 2 * CSB;
+  static constexpr int CS0 = SC0 + 2 * SCB, PBASE = CS0 + 2 * CSB;
   static constexpr int POFF = PBASE + kSMax, MX = POFF + kSMax, MZ = MX + kRMax * kPPad;
   static constexpr int MO = MZ + kRMax * kPPad;
   static constexpr int BYTES = FB + 4 * (MO + kRMax * kPPad);
+};
+
+// Per-token scalar block of one sub-chunk of TOK tokens (floats, token-indexed arrays): dt, the
+// within-chunk cumsum of adt and its exp, the exp-trapezoid scale, gamma, scale * decay to the
+// sub-chunk's end (the carry), scale * decay to the end of the token's 16-row tile, the cumsum
+// at each tile end, exp of the last cumsum. The prep pass writes them; the scan copies them to LDS.
+template <int TOK> struct ScBlk {
+  static constexpr int DTV = 0, CUM = TOK, ECUM = 2 * TOK, SCL = 3 * TOK, GAM = 4 * TOK;
+  static constexpr int VSF = 5 * TOK, BSC = 6 * TOK, CEND = 7 * TOK, ECL = 7 * TOK + 4;
+  static constexpr int SIZE = 7 * TOK + 8;
 };
 
 // Per-launch values shared by host and device.
 struct ScanGeom {
   int xcd_map;           // 1: map blocks so each XCD holds consecutive (b, h)
   int vec_qk, vec_vz;    // 1: q/k rows and v/z rows may be loaded with 16 / 8-byte vectors
-  int prep_w, prep_q, prep_k, prep_a;  // workspace floats per token and field offsets (-1: none)
+  // prep workspace, float offsets of its regions (-1: absent): RMSNorm factors [B][L][G*R][2]
+  // (q, k), pi tanh(angle) [B][L4][S][4] (4 consecutive tokens of one angle together, L4 =
+  // ceil(L / 4)), scalar blocks [B*H][nsub][scw] of `tok`-token sub-chunks
+  int64_t ws_norm, ws_ang, ws_sc;
+  int L4, tok, nsub, scw;
   // projection form (the full-shape kernel): q, k, value, gate, dt, a, trap are slices of one
   // projection row; byte offsets of each slice from `proj`, the batch / token strides and the
   // group / rank / head strides of the slices, in bytes
@@ -252,77 +263,6 @@ __device__ __forceinline__ void st_row8(T* dst, const float* x) {
   }
 }
 
-// ------------------------------------------------------------------ prep
-
-// Head-independent per-token work, once per token instead of once per head. Blocks below
-// `row_blocks`: one 16-lane group per raw q / k row (token, q|k, group, rank), 8 elements per lane,
-// its RMSNorm factor 1 / sqrt(mean(x^2) + eps) (model.py:190-191). The blocks after: one lane
-// per (token, angle), pi * tanh(angle) (model.py:225-228).
-template <typename T>
-__global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const ScanGeom g,
-                                                   float* __restrict__ out, int row_blocks) {
-  // every index below fits 31 bits (checked by the host)
-  const int tid = threadIdx.x;
-  const int tokens = a.batch * a.length;
-  if (static_cast<int>(blockIdx.x) < row_blocks) {
-    const int gr_n = a.groups * a.rank;
-    const int row = static_cast<int>(blockIdx.x) * 16 + (tid >> 4);
-    if (row >= tokens * 2 * gr_n) return;  // whole 16-lane groups leave together
-    const int l16 = tid & 15;
-    const int tok = row / (2 * gr_n);
-    const int rem = row - tok * 2 * gr_n;
-    const int which = rem >= gr_n, gr = rem - which * gr_n;
-    const int gi = gr / a.rank, r = gr - gi * a.rank;
-    const int b = tok / a.length, t = tok - b * a.length;
-    const m3_tensor& x = which ? a.k : a.q;
-    const T* p = static_cast<const T*>(x.ptr) + b * x.stride[0] + t * x.stride[1] +
-                 gi * x.stride[2] + r * x.stride[3] + 8 * l16;
-    const int N = a.d_state;
-    float ss = 0.f;
-    if (g.vec_qk) {
-      if (8 * l16 < N) {
-        uint32_t w8[Words<T>::W8];
-#pragma unroll
-        for (int j = 0; j < Words<T>::W8; j += 4) {
-          const uint4 q = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(p) + j);
-          w8[j] = q.x;
-          w8[j + 1] = q.y;
-          w8[j + 2] = q.z;
-          w8[j + 3] = q.w;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float v = raw_get<T>(w8, i);
-          ss = fmaf(v, v, ss);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (8 * l16 + i < N) {
-          const float v = to_f(p[i]);
-          ss = fmaf(v, v, ss);
-        }
-      }
-    }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
-    if (l16 == 0) {
-      out[static_cast<int64_t>(tok) * g.prep_w + (which ? g.prep_k : g.prep_q) + gr] =
-          1.f / sqrtf(ss / static_cast<float>(N) + a.norm_eps);
-    }
-  } else {
-    const int S = a.num_angles;
-    const int i = (static_cast<int>(blockIdx.x) - row_blocks) * 256 + tid;
-    if (i >= tokens * S) return;
-    const int tok = i / S, s = i - tok * S;
-    const int b = tok / a.length, t = tok - b * a.length;
-    const float th = ldx(a.phase.ptr, a.phase.dtype,
-                         b * a.phase.stride[0] + t * a.phase.stride[1] + s * a.phase.stride[2]);
-    out[static_cast<int64_t>(tok) * g.prep_w + g.prep_a + s] = __fmul_rn(kPi, tanhf(th));
-  }
-}
-
 // ------------------------------------------------------------------ scan
 
 // Wave-level scans with DPP row shifts (no LDS traffic). row_shr:n = 0x110 + n; lanes whose
@@ -425,54 +365,58 @@ __device__ __forceinline__ void bstore_elem(float x, __amdgpu_buffer_rsrc_t r, i
 // Per-token global reads of one (batch, head). FULL: every per-token input is a slice of one
 // projection row (host-checked), read at per-lane byte offsets through one buffer resource per
 // batch row whose extent ends at token L, so rows of tokens >= L read as zero without guards;
-// the per-token prep rows likewise. Otherwise element pointers with explicit guards.
-template <typename T, int R, bool FULL>
+// the prep regions likewise. Otherwise element pointers with explicit guards. TPL: tokens per
+// phase lane.
+template <typename T, int R, bool FULL, int TPL>
 struct Feed {
   static constexpr int ES = sizeof(T), W8 = Words<T>::W8, W4 = Words<T>::W4;
+  static constexpr int TOK = Mma<T>::ROWS / R;
   // FULL
-  __amdgpu_buffer_rsrc_t rs_p, rs_w;
-  int o_qk, o_vz, o_sc, o_pw, o_pa;  // per-lane byte offsets at token 0
-  int d_q1, d_k, d_z, d_a, d_tr, d_w1, d_fk, tok_b, pw_b;  // uniform byte deltas
+  __amdgpu_buffer_rsrc_t rs_p, rs_n, rs_a, rs_s;
+  int o_qk, o_vz, o_fn, o_an;  // per-lane byte offsets at token 0
+  int d_q1, d_k, d_z, tok_b, fn_b, an_b;  // uniform byte deltas / strides
   // generic
   const T *q_row, *k_row, *v_row, *z_row;
-  const void *dt_row, *aa_row, *tr_row;
-  const float *prep_row, *ph_row;
-  int q_t, q_r, k_t, k_r, v_t, z_t, dt_t, aa_t, tr_t, ph_t, dt_d, aa_d, tr_d;
-  int pw, fq_o, fk_o, pa_o, qk_n, vz_n;
+  const float *norm_row, *ang_row, *ph_row;
+  int q_t, q_r, k_t, k_r, v_t, z_t, ph_t, fn_o, qk_n, vz_n, S;
   bool vec_qk, vec_vz, norm, angles;
-  // lane roles
+  // both
+  const float* sc_row;  // this (b, h)'s scalar blocks
+  int scw, nsub, L4;
   int rp, vp, pg, ps;
 
   __device__ __forceinline__ void init(const m3_scan_args& a, const ScanGeom& g,
                                        const float* prep, int b, int h, int grp, int rp_,
-                                       int n0, int vp_, int p0, int pg_, int ps_, int lane,
-                                       int N, int P, bool norm_, bool angles_) {
-    const int L = a.length;
+                                       int n0, int vp_, int p0, int pg_, int ps_, int N, int P,
+                                       bool norm_, bool angles_) {
+    const int L = a.length, GR = a.groups * a.rank;
     rp = rp_;
     vp = vp_;
     pg = pg_;
     ps = ps_;
-    pw = g.prep_w;
     norm = norm_;
     angles = angles_;
+    S = a.num_angles;
+    scw = g.scw;
+    nsub = g.nsub;
+    L4 = g.L4;
     const int tt0 = (2 * rp) / R, r0 = (2 * rp) % R;
+    sc_row = prep + g.ws_sc + static_cast<int64_t>(b * a.heads + h) * nsub * scw;
     if constexpr (FULL) {
       tok_b = g.tok_b;
-      pw_b = pw * 4;
       rs_p = make_rsrc(g.proj + b * g.proj_b, L * tok_b);
-      rs_w = make_rsrc(prep + static_cast<int64_t>(b) * L * pw, L * pw_b);
+      fn_b = GR * 8;  // bytes of one token's (q, k) factor pairs
+      rs_n = make_rsrc(prep + g.ws_norm + static_cast<int64_t>(b) * L * GR * 2, L * fn_b);
+      o_fn = (tt0 * GR + grp * R + r0) * 8;
+      an_b = S * 16;  // one 4-token group of all angles
+      rs_a = make_rsrc(prep + g.ws_ang + static_cast<int64_t>(b) * L4 * S * 4, L4 * an_b);
+      o_an = ((TPL / 4) * pg * S + ps) * 16;
+      rs_s = make_rsrc(sc_row, nsub * scw * 4);
       o_qk = g.o_q + grp * g.qk_g + r0 * g.qk_r + tt0 * tok_b + n0 * ES;
       o_vz = g.o_v + h * g.vz_h + 2 * vp * tok_b + p0 * ES;
-      o_sc = g.o_dt + h * g.sc_h + lane * tok_b;
-      o_pw = (tt0 * pw + g.prep_q + grp * R + r0) * 4;
-      o_pa = (4 * pg * pw + g.prep_a + ps) * 4;
       d_q1 = R == 1 ? tok_b : g.qk_r;  // row 2rp + 1: the next token (R = 1) or the next rank
-      d_w1 = R == 1 ? pw_b : 4;
       d_k = g.o_k - g.o_q;
       d_z = g.o_z - g.o_v;
-      d_a = g.o_a - g.o_dt;
-      d_tr = g.o_tr - g.o_dt;
-      d_fk = (g.prep_k - g.prep_q) * 4;
     } else {
       q_row = static_cast<const T*>(a.q.ptr) + b * a.q.stride[0] + grp * a.q.stride[2] + n0;
       k_row = static_cast<const T*>(a.k.ptr) + b * a.k.stride[0] + grp * a.k.stride[2] + n0;
@@ -486,24 +430,14 @@ struct Feed {
               p0;
       v_t = static_cast<int>(a.value.stride[1]);
       z_t = static_cast<int>(a.gate.stride[1]);
-      dt_d = a.dt.dtype;
-      aa_d = a.a.dtype;
-      tr_d = a.trap.dtype;
-      dt_row = offx(a.dt.ptr, dt_d, b * a.dt.stride[0] + h * a.dt.stride[2]);
-      aa_row = offx(a.a.ptr, aa_d, b * a.a.stride[0] + h * a.a.stride[2]);
-      tr_row = offx(a.trap.ptr, tr_d, b * a.trap.stride[0] + h * a.trap.stride[2]);
-      dt_t = static_cast<int>(a.dt.stride[1]);
-      aa_t = static_cast<int>(a.a.stride[1]);
-      tr_t = static_cast<int>(a.trap.stride[1]);
-      prep_row = prep + static_cast<int64_t>(b) * L * pw;
+      norm_row = norm ? prep + g.ws_norm + static_cast<int64_t>(b) * L * GR * 2 : nullptr;
+      fn_o = grp * R;
+      ang_row = angles ? prep + g.ws_ang + static_cast<int64_t>(b) * L4 * S * 4 : nullptr;
       const bool given = a.phase_mode == M3_PHASE_GIVEN;
       ph_row = given ? static_cast<const float*>(a.phase.ptr) + b * a.phase.stride[0] +
                            h * a.phase.stride[2] + ps * a.phase.stride[3]
                      : nullptr;
       ph_t = given ? static_cast<int>(a.phase.stride[1]) : 0;
-      fq_o = g.prep_q + grp * R;
-      fk_o = g.prep_k + grp * R;
-      pa_o = g.prep_a + ps;
       qk_n = max(0, min(8, N - n0));
       vz_n = max(0, min(4, P - p0));
       vec_qk = g.vec_qk;
@@ -512,28 +446,42 @@ struct Feed {
   }
 
   // q / k rows 2rp, 2rp+1 and value / gate tokens 2vp, 2vp+1 of the sub-chunk at token t0
-  // (nw valid tokens), plus the RMSNorm factors of the q / k rows.
+  // (nw valid tokens); FULL also the RMSNorm factors of the q / k rows (else factors()).
   __device__ __forceinline__ void words(int t0, int nw, bool qk_on, bool vz_on,
                                         uint32_t (&rq)[2][W8], uint32_t (&rk)[2][W8],
                                         uint32_t (&rv)[2][W4], uint32_t (&rz)[2][W4],
                                         float (&fq)[2], float (&fk)[2]) const {
     if constexpr (FULL) {
-      const int tb = t0 * tok_b, tw = t0 * pw_b;
-      if (qk_on) {
+      // unconditional, also for lanes without a q/k or v/z role: every offset stays inside a
+      // buffer or past its extent, where the load returns zero
+      const int tb = t0 * tok_b;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        bload_words<W8>(rq[j], rs_p, o_qk + tb + j * d_q1);
+        bload_words<W8>(rk[j], rs_p, o_qk + tb + j * d_q1 + d_k);
+      }
+      // (q, k) factor pairs of rows 2rp, 2rp+1: R > 1, 16 bytes of one token; R = 1, 8 bytes of
+      // each of two tokens (two loads, so a pair past token L never shares a load with one before)
+      if constexpr (R > 1) {
+        const u32x4 f = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_n, o_fn + t0 * fn_b, 0, 0));
+        fq[0] = __uint_as_float(f[0]);
+        fk[0] = __uint_as_float(f[1]);
+        fq[1] = __uint_as_float(f[2]);
+        fk[1] = __uint_as_float(f[3]);
+      } else {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          bload_words<W8>(rq[j], rs_p, o_qk + tb + j * d_q1);
-          bload_words<W8>(rk[j], rs_p, o_qk + tb + j * d_q1 + d_k);
-          fq[j] = bload_f32(rs_w, o_pw + tw + j * d_w1);
-          fk[j] = bload_f32(rs_w, o_pw + tw + j * d_w1 + d_fk);
+          const u32x2 f = __builtin_bit_cast(
+              u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_n, o_fn + (t0 + j) * fn_b, 0, 0));
+          fq[j] = __uint_as_float(f[0]);
+          fk[j] = __uint_as_float(f[1]);
         }
       }
-      if (vz_on) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          bload_words<W4>(rv[j], rs_p, o_vz + tb + j * tok_b);
-          bload_words<W4>(rz[j], rs_p, o_vz + tb + j * tok_b + d_z);
-        }
+      for (int j = 0; j < 2; ++j) {
+        bload_words<W4>(rv[j], rs_p, o_vz + tb + j * tok_b);
+        bload_words<W4>(rz[j], rs_p, o_vz + tb + j * tok_b + d_z);
       }
     } else {
       if (qk_on) {
@@ -544,11 +492,6 @@ struct Feed {
           const int tg = t0 + tt;
           load_words<T, 8>(rq[j], q_row + tg * q_t + r * q_r, ok ? qk_n : 0, vec_qk);
           load_words<T, 8>(rk[j], k_row + tg * k_t + r * k_r, ok ? qk_n : 0, vec_qk);
-          if (norm && ok) {
-            const float* pr = prep_row + static_cast<int64_t>(tg) * pw;
-            fq[j] = pr[fq_o + r];
-            fk[j] = pr[fk_o + r];
-          }
         }
       }
       if (vz_on) {
@@ -564,107 +507,58 @@ struct Feed {
     }
   }
 
-  // angle inputs of tokens 4pg .. 4pg+3 (pi tanh(angle) from the prep rows, or given phases)
-  __device__ __forceinline__ void angle_in(int t0, int nw, bool ph_on, float (&pa)[4]) const {
-    if (!ph_on) return;
-    if constexpr (FULL) {
+  // the RMSNorm factors of rows 2rp, 2rp+1 (generic path; GR = groups * rank)
+  __device__ __forceinline__ void factors(int t0, int nw, int GR, bool qk_on, float (&fq)[2],
+                                          float (&fk)[2]) const {
+    if constexpr (!FULL) {
+      if (!qk_on || !norm) return;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pa[i] = bload_f32(rs_w, o_pa + (t0 + i) * pw_b);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tt = 4 * pg + i;
-        const int tg = t0 + tt;
-        pa[i] = 0.f;
+      for (int j = 0; j < 2; ++j) {
+        const int row = 2 * rp + j, tt = row / R, r = row - tt * R;
         if (tt < nw) {
-          pa[i] = angles ? prep_row[static_cast<int64_t>(tg) * pw + pa_o] : ph_row[tg * ph_t];
+          const float* pr = norm_row + (static_cast<int64_t>(t0 + tt) * GR + fn_o + r) * 2;
+          fq[j] = pr[0];
+          fk[j] = pr[1];
         }
       }
     }
   }
 
-  // wave 0: raw dt, a, trap of token t0 + lane
-  __device__ __forceinline__ void scalars_in(int t0, int nw, int lane, float& sdt, float& sa,
-                                             float& str) const {
+  // angle inputs of tokens TPL pg .. TPL pg + TPL-1 (pi tanh(angle) from the prep region, or
+  // given phases)
+  __device__ __forceinline__ void angle_in(int t0, int nw, bool ph_on, float (&pa)[TPL]) const {
     if constexpr (FULL) {
-      const int o = o_sc + t0 * tok_b;
-      sdt = bload_elem<T>(rs_p, o);
-      sa = bload_elem<T>(rs_p, o + d_a);
-      str = bload_elem<T>(rs_p, o + d_tr);
+#pragma unroll
+      for (int q = 0; q < TPL / 4; ++q) {
+        const u32x4 v = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_a, o_an + (t0 / 4 + q) * an_b, 0, 0));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pa[4 * q + i] = __uint_as_float(v[i]);
+      }
     } else {
-      sdt = sa = str = 0.f;
-      if (lane < nw) {
-        const int tg = t0 + lane;
-        sdt = ldx(dt_row, dt_d, static_cast<int64_t>(tg) * dt_t);
-        sa = ldx(aa_row, aa_d, static_cast<int64_t>(tg) * aa_t);
-        str = ldx(tr_row, tr_d, static_cast<int64_t>(tg) * tr_t);
+      if (!ph_on) return;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        const int tt = TPL * pg + i;
+        const int tg = t0 + tt;
+        pa[i] = 0.f;
+        if (tt < nw) {
+          pa[i] = angles ? ang_row[(static_cast<int64_t>(tg >> 2) * S + ps) * 4 + (tg & 3)]
+                         : ph_row[tg * ph_t];
+        }
       }
     }
   }
-};
 
-// Per-token scalars of the sub-chunk at token tb (wave 0, lane = token) into the block SCn:
-// dt, the within-chunk cumsum of adt and exp of it, gamma = dt sigmoid(trap), the exp-trapezoid
-// scale = gamma + dt' (1 - sigmoid(trap')) of the next token (ops.py:659-671), and the
-// products with the decays the scores and the carry use. The last token's next-token term
-// belongs to the first token of the following sub-chunk: the call for that sub-chunk writes
-// the previous block's last entries (SCp), gamma_last + that term, exp(cum_last - cum_last)
-// being 1; `gprev` carries gamma_last from call to call.
-template <typename Lay, int TOK, int TPT>
-__device__ __forceinline__ void scalar_stage(float* SCn, float* SCp, int tb, int L, int lane,
-                                             bool raw_dt, float dt_bias, float sdt, float sa,
-                                             float str, float& gprev) {
-  const int wn = min(TOK, L - tb);
-  const bool tv = lane < wn;
-  float dt = 0.f, adt = 0.f, tr = 0.f;
-  if (raw_dt) {
-    dt = softplus(sdt + dt_bias);
-    adt = fminf(-heavy_tail_fast(sa), -kAFloor) * dt;
-  } else {
-    dt = sdt;
-    adt = sa;
+  // one float of sub-chunk c's scalar block (lanes below scw)
+  __device__ __forceinline__ float sc_in(int c, int tid) const {
+    if constexpr (FULL) {
+      return bload_f32(rs_s, (c * scw + tid) * 4);
+    } else {
+      return (c < nsub && tid < scw) ? sc_row[static_cast<int64_t>(c) * scw + tid] : 0.f;
+    }
   }
-  tr = sigmoid_fast(str);
-  if (!tv) dt = adt = tr = 0.f;
-  const float lead = dt * (1.f - tr);  // this token's term of the previous token's scale
-  // lane l + 1's value (DPP wave_shl:1; lane 63 reads 0)
-  float right = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                              0, __builtin_bit_cast(int, lead), 0x130, 0xf, 0xf,
-                                              true));
-  if (lane >= wn - 1) right = 0.f;
-  const float lead0 = readlane_f(lead, 0);
-  if (SCp != nullptr && lane == 0) {
-    const float sl = gprev + lead0;
-    SCp[Lay::SCL + TOK - 1] = sl;
-    SCp[Lay::VSF + TOK - 1] = sl;
-    SCp[Lay::BSC + TOK - 1] = sl;
-  }
-  const float gamma = dt * tr;
-  gprev = readlane_f(gamma, TOK - 1);
-  const float scale = gamma + right;
-  const float cum = wave_incl_scan(adt, lane);
-  const float cum_last = readlane_f(cum, wn - 1);
-  const float cv = tv ? cum : cum_last;
-  // cum at the end of this lane's 16-row tile (TPT tokens), clamped to the last valid token
-  float cend;
-  if constexpr (TPT == 16) {
-    const float e0 = readlane_f(cv, 15), e1 = readlane_f(cv, 31), e2 = readlane_f(cv, 47);
-    const float e3 = readlane_f(cv, 63);
-    const int grp = lane >> 4;
-    cend = grp == 0 ? e0 : (grp == 1 ? e1 : (grp == 2 ? e2 : e3));
-  } else {
-    cend = __shfl(cv, min(lane | (TPT - 1), wn - 1));
-  }
-  SCn[Lay::DTV + lane] = dt;
-  SCn[Lay::CUM + lane] = cv;
-  SCn[Lay::ECUM + lane] = tv ? __expf(cv) : 0.f;
-  SCn[Lay::SCL + lane] = tv ? scale : 0.f;
-  SCn[Lay::GAM + lane] = gamma;
-  SCn[Lay::VSF + lane] = tv ? scale * __expf(cum_last - cv) : 0.f;
-  SCn[Lay::BSC + lane] = tv ? scale * __expf(cend - cv) : 0.f;
-  if (lane < TOK && (lane & (TPT - 1)) == 0) SCn[Lay::CEND + lane / TPT] = cend;
-  if (lane == 0) SCn[Lay::ECL] = __expf(cum_last);
-}
+};
 
 // Column of angle `col` in the cos / sin table row of token tt. SWZ (64-token sub-chunks, 32
 // angles): blocks of 4 angles are XOR-swizzled by the token's 16-token block, spreading the
@@ -674,36 +568,34 @@ __device__ __forceinline__ int cs_col(int col, int tt) {
   return SWZ ? col ^ (4 * ((tt >> 4) & 3)) : col;
 }
 
-// Bounded phase (model.py:215-256) of tokens 4pg .. 4pg+3 of the sub-chunk at t0 for angle ps:
-// fmod-reduced increments summed within 64-token blocks, an fmod-reduced carry between blocks,
-// the running block sum and carry in pbase / poff; cos / sin into the table of angle ps.
-template <int PG, int CST, bool SWZ>
+// Bounded phase (model.py:215-256) of tokens TPL pg .. TPL pg + TPL-1 of the sub-chunk at t0 for
+// angle ps: fmod-reduced increments summed within 64-token blocks, an fmod-reduced carry between
+// blocks, the running block sum and carry in pbase / poff; cos / sin into the table of angle ps.
+template <int PG, int TPL, int CST, bool SWZ>
 __device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, float* poff,
                                             const float* dtv, int t0, int L, int pg, int lane,
-                                            bool angles, const float (&pa)[4], float* fph) {
-  const int width = min(4 * PG, L - t0);
-  float ph[4];
+                                            bool angles, const float (&pa)[TPL], float* fph) {
+  float ph[TPL];
   if (angles) {
-    float x[4];
+    float x[TPL];
     bool big = false;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tt = 4 * pg + i;
-      x[i] = __fmul_rn(pa[i], dtv[tt]);  // dt is 0 past the sub-chunk's last token
+    for (int i = 0; i < TPL; ++i) {
+      x[i] = __fmul_rn(pa[i], dtv[TPL * pg + i]);  // dt is 0 past the sub-chunk's last token
       big = big || !(fabsf(x[i]) < 1048576.0f);
     }
-    float inc[4];
+    float inc[TPL];
     if (big) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) inc[i] = m3_fmod_2pi(x[i]);
+      for (int i = 0; i < TPL; ++i) inc[i] = m3_fmod_2pi(x[i]);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) inc[i] = m3_fmod_2pi_small(x[i]);
+      for (int i = 0; i < TPL; ++i) inc[i] = m3_fmod_2pi_small(x[i]);
     }
-    float cpre[4];
+    float cpre[TPL];
     float run = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < TPL; ++i) {
       run = __fadd_rn(run, inc[i]);
       cpre[i] = run;
     }
@@ -718,10 +610,10 @@ __device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, fl
       base = 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < TPL; ++i) {
       // |base|, |excl + cpre| <= 64 * 2 pi and |off| < 2 pi: within the reduction's range
       ph[i] = m3_fmod_2pi_small(__fadd_rn(__fadd_rn(base, __fadd_rn(excl, cpre[i])), off));
-      if (t0 + 4 * pg + i == L - 1 && fph != nullptr) *fph = ph[i];
+      if (t0 + TPL * pg + i == L - 1 && fph != nullptr) *fph = ph[i];
     }
     if (pg == PG - 1) {
       *pbase = __fadd_rn(base, incl);
@@ -729,14 +621,162 @@ __device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, fl
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ph[i] = pa[i];
+    for (int i = 0; i < TPL; ++i) ph[i] = pa[i];
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int tt = 4 * pg + i;
+  for (int i = 0; i < TPL; ++i) {
+    const int tt = TPL * pg + i;
     float2 v;
     __sincosf(ph[i], &v.y, &v.x);
     *reinterpret_cast<float2*>(tab + tt * CST + 2 * cs_col<SWZ>(ps, tt)) = v;
+  }
+}
+
+// ------------------------------------------------------------------ prep
+
+// The scalar block of sub-chunk c of (batch, head) bh (one wave, lane = token): dt, adt, trap
+// from the raw projection or given (model.py:195-198), gamma = dt sigmoid(trap), scale = gamma +
+// dt' (1 - sigmoid(trap')) of the next token, 0 at the last token (ops.py:659-671), the
+// within-chunk cumsum of adt by a wave scan, and the decay products the scan uses.
+template <int TOK, int TPT>
+__device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __restrict__ o,
+                                             int b, int h, int c, int lane) {
+  using B = ScBlk<TOK>;
+  const int L = a.length;
+  const int tb = c * TOK, t = tb + lane;
+  const int wn = min(TOK, L - tb);
+  const bool tv = lane < wn;
+  const bool nv = lane < TOK && t + 1 < L;
+  const bool raw_dt = a.raw_dt != 0;
+  const float dt_bias = raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0])
+                               : 0.f;
+  const int64_t base_dt = b * a.dt.stride[0] + h * a.dt.stride[2];
+  const int64_t base_a = b * a.a.stride[0] + h * a.a.stride[2];
+  const int64_t base_tr = b * a.trap.stride[0] + h * a.trap.stride[2];
+  float dt = 0.f, adt = 0.f, tr = 0.f, right = 0.f;
+  if (tv) {
+    dt_adt(raw_dt, ldx(a.dt.ptr, a.dt.dtype, base_dt + t * a.dt.stride[1]),
+           ldx(a.a.ptr, a.a.dtype, base_a + t * a.a.stride[1]), dt_bias, dt, adt);
+    tr = sigmoidf(ldx(a.trap.ptr, a.trap.dtype, base_tr + t * a.trap.stride[1]));
+  }
+  if (nv) {
+    float dn, an;
+    dt_adt(raw_dt, ldx(a.dt.ptr, a.dt.dtype, base_dt + (t + 1) * a.dt.stride[1]), 0.f,
+           dt_bias, dn, an);
+    right = dn * (1.f - sigmoidf(ldx(a.trap.ptr, a.trap.dtype,
+                                     base_tr + (t + 1) * a.trap.stride[1])));
+  }
+  const float gamma = dt * tr;
+  const float scale = gamma + right;
+  const float cum = wave_incl_scan(adt, lane);
+  const float cum_last = readlane_f(cum, wn - 1);
+  const float cv = tv ? cum : cum_last;
+  // cum at the end of this lane's 16-row tile (TPT tokens), clamped to the last valid token
+  float cend;
+  if constexpr (TPT == 16) {
+    const float e0 = readlane_f(cv, 15), e1 = readlane_f(cv, 31), e2 = readlane_f(cv, 47);
+    const float e3 = readlane_f(cv, 63);
+    const int q = lane >> 4;
+    cend = q == 0 ? e0 : (q == 1 ? e1 : (q == 2 ? e2 : e3));
+  } else {
+    cend = __shfl(cv, min(lane | (TPT - 1), wn - 1));
+  }
+  if (lane < TOK) {
+    o[B::DTV + lane] = dt;
+    o[B::CUM + lane] = cv;
+    o[B::ECUM + lane] = tv ? __expf(cv) : 0.f;
+    o[B::SCL + lane] = tv ? scale : 0.f;
+    o[B::GAM + lane] = gamma;
+    o[B::VSF + lane] = tv ? scale * __expf(cum_last - cv) : 0.f;
+    o[B::BSC + lane] = tv ? scale * __expf(cend - cv) : 0.f;
+    if ((lane & (TPT - 1)) == 0) o[B::CEND + lane / TPT] = cend;
+  }
+  if (lane == 0) o[B::ECL] = __expf(cum_last);
+}
+
+// Head-independent and per-(head, sub-chunk) work ahead of the scan, three block ranges:
+//  [0, nb_norm)  one 16-lane group per raw q / k row (token, group, rank, q|k), 8 elements per
+//                lane: its RMSNorm factor 1 / sqrt(mean(x^2) + eps) (model.py:190-191);
+//  [.., +nb_ang) one lane per (token, angle), token padded to a multiple of 4: pi * tanh(angle)
+//                (model.py:225-228), 0 in the padding;
+//  [.., +nb_sc)  one wave per (batch, head, sub-chunk): its scalar block.
+template <typename T, int R>
+__global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const ScanGeom g,
+                                                   float* __restrict__ ws, int nb_norm,
+                                                   int nb_ang) {
+  // every index below fits 31 bits (checked by the host)
+  constexpr int TOK = Mma<T>::ROWS / R, TPT = 16 / R;
+  const int tid = threadIdx.x, blk = blockIdx.x;
+  const int L = a.length, tokens = a.batch * L;
+  if (blk < nb_norm) {
+    const int gr_n = a.groups * a.rank;
+    const int row = blk * 16 + (tid >> 4);  // (token, group-rank, q|k)
+    if (row >= tokens * gr_n * 2) return;   // whole 16-lane groups leave together
+    const int l16 = tid & 15;
+    const int tok = row / (2 * gr_n);
+    const int rem = row - tok * 2 * gr_n;
+    const int gr = rem >> 1, which = rem & 1;
+    const int gi = gr / a.rank, r = gr - gi * a.rank;
+    const int b = tok / L, t = tok - b * L;
+    const m3_tensor& x = which ? a.k : a.q;
+    const T* p = static_cast<const T*>(x.ptr) + b * x.stride[0] + t * x.stride[1] +
+                 gi * x.stride[2] + r * x.stride[3] + 8 * l16;
+    const int N = a.d_state;
+    float ss = 0.f;
+    if (g.vec_qk) {
+      if (8 * l16 < N) {
+        uint32_t w8[Words<T>::W8];
+#pragma unroll
+        for (int j = 0; j < Words<T>::W8; j += 4) {
+          const uint4 q = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(p) + j);
+          w8[j] = q.x;
+          w8[j + 1] = q.y;
+          w8[j + 2] = q.z;
+          w8[j + 3] = q.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float v = raw_get<T>(w8, i);
+          ss = fmaf(v, v, ss);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (8 * l16 + i < N) {
+          const float v = to_f(p[i]);
+          ss = fmaf(v, v, ss);
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+    if (l16 == 0) {
+      ws[g.ws_norm + static_cast<int64_t>(row)] =
+          1.f / sqrtf(ss / static_cast<float>(N) + a.norm_eps);
+    }
+  } else if (blk < nb_norm + nb_ang) {
+    // element (b, t4, s, i) of the angle region, token t = 4 t4 + i
+    const int S = a.num_angles;
+    const int e = (blk - nb_norm) * 256 + tid;
+    if (e >= a.batch * g.L4 * S * 4) return;
+    const int i = e & 3, rest = e >> 2;
+    const int s = rest % S, bt4 = rest / S;
+    const int b = bt4 / g.L4, t = 4 * (bt4 - b * g.L4) + i;
+    float v = 0.f;
+    if (t < L) {
+      const float th = ldx(a.phase.ptr, a.phase.dtype,
+                           b * a.phase.stride[0] + t * a.phase.stride[1] + s * a.phase.stride[2]);
+      v = __fmul_rn(kPi, tanhf(th));
+    }
+    ws[g.ws_ang + static_cast<int64_t>(e)] = v;
+  } else {
+    const int idx = (blk - nb_norm - nb_ang) * 4 + (tid >> 6);
+    if (idx >= a.batch * a.heads * g.nsub) return;  // whole waves leave together
+    const int bh = idx / g.nsub, c = idx - bh * g.nsub;
+    const int b = bh / a.heads, h = bh - b * a.heads;
+    scalar_block<TOK, TPT>(a, ws + g.ws_sc + static_cast<int64_t>(idx) * g.scw, b, h, c,
+                           tid & 63);
   }
 }
 
@@ -749,18 +789,20 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   constexpr int RT = ROWS / 16;        // 16-row tiles per sub-chunk
   constexpr int WPR = kWaves / RT;     // waves sharing one query row tile
   constexpr int TOK = ROWS / R;        // tokens per sub-chunk
-  constexpr int TPT = 16 / R;          // tokens per 16-row tile
-  constexpr int PG = TOK / 4;          // phase lanes per angle (4 tokens each)
   constexpr bool F32 = sizeof(T) == 4;
   constexpr int ES = sizeof(T);
   constexpr int LQ = Lay::LQ, LR = Lay::LR, NP = kNPad, CST = Lay::CST;
-  // SISO model shape: q / k lanes split by column half, waves 0-3 holding the rotated columns
+  using SB_ = ScBlk<TOK>;
+  // SISO model shape: q / k lanes split by column half, waves 0-3 holding the rotated columns;
+  // the phase on waves 0-3 only, 8 tokens per lane (their compute interval is the shorter one)
   constexpr bool SPLIT = FULL && R == 1 && !F32;
+  constexpr int TPL = SPLIT ? 8 : 4;   // tokens per phase lane
+  constexpr int PG = TOK / TPL;        // phase lanes per angle
   // FULL: the model's shape (N = 128, P = 64, S = 32) in projection form with vector loads
   const int N = FULL ? kNPad : a.d_state;
   const int P = FULL ? kPPad : a.head_dim;
   const int S = FULL ? kSMax : a.num_angles;
-  const bool norm = FULL || g.prep_q >= 0;
+  const bool norm = FULL || g.ws_norm >= 0;
   const bool bias = FULL || a.q_bias.ptr != nullptr;
   const bool rotate = FULL || a.phase_mode != M3_PHASE_NONE;
   const bool angles = FULL || a.phase_mode == M3_PHASE_ANGLES;
@@ -791,7 +833,6 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   T* ZT = lds_t<T>(smem, Lay::ZT);
   T* Sb = lds_t<T>(smem, Lay::SB);
   float* F = lds_t<float>(smem, Lay::FB);
-  const int PW = g.prep_w;
   const float Dh = ldx(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
 
   // ---- lane roles
@@ -806,7 +847,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   const int vp = tid / P4, p0 = 4 * (tid % P4);
   const bool vz_on = 2 * vp < TOK && p0 < P;
   const int vz_n = min(4, P - p0);
-  // phase: angle ps, token group pg (tokens 4pg .. 4pg+3)
+  // phase: angle ps, token group pg (tokens TPL pg .. TPL pg + TPL-1)
   const int pg = tid % PG, ps = tid / PG;
   const bool ph_on = rotate && ps < S;
 
@@ -923,10 +964,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   }
 
   // ---- per-token reads
-  const float dt_bias = raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0])
-                               : 0.f;
-  Feed<T, R, FULL> fd;
-  fd.init(a, g, prep, b, h, grp, rp, n0, vp, p0, pg, ps, lane, N, P, norm, angles);
+  Feed<T, R, FULL, TPL> fd;
+  fd.init(a, g, prep, b, h, grp, rp, n0, vp, p0, pg, ps, N, P, norm, angles);
+  const int GR = a.groups * R;
   float* fph = a.final_phase.ptr != nullptr
                    ? static_cast<float*>(a.final_phase.ptr) + b * a.final_phase.stride[0] +
                          h * a.final_phase.stride[1] + ps * a.final_phase.stride[2]
@@ -965,37 +1005,31 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   constexpr int W8 = Words<T>::W8, W4 = Words<T>::W4;
   uint32_t rq[2][W8], rk[2][W8], rv[2][W4], rz[2][W4];
   float fq[2] = {1.f, 1.f}, fk[2] = {1.f, 1.f};
-  float pa[4] = {0.f, 0.f, 0.f, 0.f};
-  float sdt = 0.f, sa = 0.f, str = 0.f;  // wave 0: raw scalars of a coming sub-chunk
-  float gprev = 0.f;                      // wave 0: gamma of the last scalar block's last token
-  const int nsub = (L + TOK - 1) / TOK;
-  auto scb = [&](int c) { return F + Lay::SC0 + (c % 3) * Lay::SCB; };
+  float pa[TPL];
+#pragma unroll
+  for (int i = 0; i < TPL; ++i) pa[i] = 0.f;
+  float scv = 0.f;  // lanes below scw: one float of a coming sub-chunk's scalar block
+  const int nsub = g.nsub, scw = g.scw;
+  auto scb = [&](int c) { return F + Lay::SC0 + (c & 1) * Lay::SCB; };
   auto csb = [&](int c) { return F + Lay::CS0 + (c & 1) * Lay::CSB; };
 
-  // Pipeline: iteration c stages sub-chunk c into LDS (interval 1), then computes its outputs
-  // and state carry while the phases of c + 1 and (wave 0) the scalars of c + 2 are computed
-  // and the loads of c + 1 (words), c + 2 (angles) and c + 3 (scalars) are in flight
-  // (interval 2). Scalar blocks rotate over 3 buffers, cos / sin tables over 2.
-  // prologue: scalars of 0 and 1, phases of 0
+  // Pipeline: iteration c stages sub-chunk c into LDS and copies the scalar block of c + 1 there
+  // (interval 1), then computes the outputs and state carry of c while the phases of c + 1 are
+  // computed and the loads of c + 1 (words), c + 2 (angles, scalar block) are in flight
+  // (interval 2). Scalar blocks and cos / sin tables alternate between two LDS buffers each.
+  // prologue: scalar block 0 to LDS, phases of 0
+  scv = fd.sc_in(0, tid);
   fd.words(0, min(TOK, L), qk_on, vz_on, rq, rk, rv, rz, fq, fk);
+  fd.factors(0, min(TOK, L), GR, qk_on, fq, fk);
   fd.angle_in(0, min(TOK, L), ph_on, pa);
-  if (w == 0 && nsub > 0) {
-    fd.scalars_in(0, min(TOK, L), lane, sdt, sa, str);
-    scalar_stage<Lay, TOK, TPT>(scb(0), nullptr, 0, L, lane, raw_dt, dt_bias, sdt, sa, str,
-                                gprev);
-    if (nsub > 1) {
-      fd.scalars_in(TOK, min(TOK, L - TOK), lane, sdt, sa, str);
-      scalar_stage<Lay, TOK, TPT>(scb(1), scb(0), TOK, L, lane, raw_dt, dt_bias, sdt, sa, str,
-                                  gprev);
-    }
-    if (nsub > 2) fd.scalars_in(2 * TOK, min(TOK, L - 2 * TOK), lane, sdt, sa, str);
-  }
+  if (tid < scw) scb(0)[tid] = scv;
+  scv = fd.sc_in(1, tid);
   __syncthreads();
   if (ph_on && nsub > 0) {
-    phase_stage<PG, CST, SPLIT>(csb(0), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
-                                scb(0) + Lay::DTV, 0, L, pg, lane, angles, pa, fph);
+    phase_stage<PG, TPL, CST, SPLIT>(csb(0), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
+                                     scb(0) + SB_::DTV, 0, L, pg, lane, angles, pa, fph);
   }
-  if (nsub > 1) fd.angle_in(TOK, min(TOK, L - TOK), ph_on, pa);
+  if (FULL || nsub > 1) fd.angle_in(TOK, min(TOK, L - TOK), ph_on, pa);
   __syncthreads();
 
   for (int c = 0; c < nsub; ++c) {
@@ -1004,7 +1038,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     const float* SC = scb(c);
     const float* CSt = csb(c);
 
-    // ---- interval 1: stage sub-chunk c
+    // ---- interval 1: stage sub-chunk c; the scalar block of c + 1 to LDS
+    if (tid < scw && c + 1 < nsub) scb(c + 1)[tid] = scv;
     // q / k rows -> Qs, Ks (row-major), KT (transposed, swizzled); rows 2rp, 2rp+1
     if (qk_on) {
       float kt[2][8];
@@ -1087,7 +1122,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           z[j][i] = raw_get<T>(rz[j], i);
         }
       }
-      const float f0 = SC[Lay::VSF + 2 * vp], f1 = SC[Lay::VSF + 2 * vp + 1];
+      const float f0 = SC[SB_::VSF + 2 * vp], f1 = SC[SB_::VSF + 2 * vp + 1];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int p = p0 + i;
@@ -1128,10 +1163,14 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     __syncthreads();
 
     // ---- interval 2
-    // words of sub-chunk c + 1 into registers; they fly while sub-chunk c computes
-    if (c + 1 < nsub) {
+    // words of sub-chunk c + 1 into registers; they fly while sub-chunk c computes. FULL issues
+    // every load of the loop unconditionally (reads past token L return zero), which keeps the
+    // compiler's in-order wait counts exact: no load is waited for before its use.
+    if (FULL || c + 1 < nsub) {
       fd.words(t0 + TOK, min(TOK, L - t0 - TOK), qk_on, vz_on, rq, rk, rv, rz, fq, fk);
+      fd.factors(t0 + TOK, min(TOK, L - t0 - TOK), GR, qk_on, fq, fk);
     }
+    scv = fd.sc_in(c + 2, tid);
 
     // outputs for query row tile `it` and P tiles pj = wp, wp + WPR, ...
     const int it = w / WPR, wp = w - it * WPR;
@@ -1193,13 +1232,16 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     }
     // phases of sub-chunk c + 1 (its dt block was computed two iterations ago)
     if (ph_on && c + 1 < nsub) {
-      phase_stage<PG, CST, SPLIT>(csb(c + 1), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
-                                  scb(c + 1) + Lay::DTV, t0 + TOK, L, pg, lane, angles, pa, fph);
-      if (c + 2 < nsub) fd.angle_in(t0 + 2 * TOK, min(TOK, L - t0 - 2 * TOK), ph_on, pa);
+      phase_stage<PG, TPL, CST, SPLIT>(csb(c + 1), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
+                                       scb(c + 1) + SB_::DTV, t0 + TOK, L, pg, lane, angles, pa,
+                                       fph);
+    }
+    if (FULL || (ph_on && c + 2 < nsub)) {
+      fd.angle_in(t0 + 2 * TOK, min(TOK, L - t0 - 2 * TOK), ph_on, pa);
     }
     // decayed scores W[t, s] = Sc[t, s] d[t, s] in FP32
-    const float cum_t = SC[Lay::CUM + tq];
-    const float gam_t = SC[Lay::GAM + tq];
+    const float cum_t = SC[SB_::CUM + tq];
+    const float gam_t = SC[SB_::GAM + tq];
     f4 wsc[RT];
 #pragma unroll
     for (int sj = 0; sj < RT; ++sj) {
@@ -1207,17 +1249,17 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       if (sj > it) continue;
       if (sj < it) {
         // strictly earlier tile: d = exp(cum_t - cend) * (scale_s exp(cend - cum_s)), both <= 1
-        const float at = __expf(cum_t - SC[Lay::CEND + sj]);
+        const float at = __expf(cum_t - SC[SB_::CEND + sj]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int ts = (16 * sj + 4 * lg + i) / R;
-          wsc[sj][i] = acc[sj][i] * (at * SC[Lay::BSC + ts]);
+          wsc[sj][i] = acc[sj][i] * (at * SC[SB_::BSC + ts]);
         }
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int ts = (16 * sj + 4 * lg + i) / R;
-          const float d = tq > ts ? SC[Lay::SCL + ts] * __expf(cum_t - SC[Lay::CUM + ts])
+          const float d = tq > ts ? SC[SB_::SCL + ts] * __expf(cum_t - SC[SB_::CUM + ts])
                                   : (tq == ts ? gam_t : 0.f);
           wsc[sj][i] = acc[sj][i] * d;
         }
@@ -1225,7 +1267,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     }
     float ecum[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ecum[i] = SC[Lay::ECUM + (16 * it + 4 * lg + i) / R];
+    for (int i = 0; i < 4; ++i) ecum[i] = SC[SB_::ECUM + (16 * it + 4 * lg + i) / R];
 #pragma unroll
     for (int pq = 0; pq < kPT / WPR; ++pq) {
       const int pj = wp + pq * WPR;
@@ -1313,20 +1355,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     }
 
     // state carry: S^T = exp(cum_last) S^T + K^T Vs (the products were issued above)
-    const float ecl = SC[Lay::ECL];
+    const float ecl = SC[SB_::ECL];
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) st[k][i] = fmaf(ecl, st[k][i], cacc[k][i]);
-    }
-
-    // wave 0: scalars of sub-chunk c + 2, then the raw scalars of c + 3
-    if (w == 0 && c + 2 < nsub) {
-      scalar_stage<Lay, TOK, TPT>(scb(c + 2), scb(c + 1), t0 + 2 * TOK, L, lane, raw_dt, dt_bias,
-                                  sdt, sa, str, gprev);
-      if (c + 3 < nsub) {
-        fd.scalars_in(t0 + 3 * TOK, min(TOK, L - t0 - 3 * TOK), lane, sdt, sa, str);
-      }
     }
     __syncthreads();
   }
@@ -1366,6 +1399,31 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Prep workspace regions (floats, each 16-byte aligned) and the sub-chunk geometry; returns the
+// workspace size in bytes.
+static size_t ws_layout(const m3_scan_args& a, ScanGeom& g) {
+  const int rows = a.act_dtype == M3_F32 ? Mma<float>::ROWS : Mma<__bf16>::ROWS;
+  const int rank = a.rank > 0 ? a.rank : 1;
+  g.tok = rows / rank > 0 ? rows / rank : 1;
+  const int64_t len = a.length > 0 ? a.length : 0;
+  g.nsub = static_cast<int>((len + g.tok - 1) / g.tok);
+  g.scw = 7 * g.tok + 8;
+  g.L4 = static_cast<int>((len + 3) / 4);
+  const bool norm = a.q_norm_w.ptr != nullptr;
+  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
+  const int64_t batch = a.batch > 0 ? a.batch : 0;
+  int64_t off = 0;
+  auto take = [&](int64_t n) {
+    const int64_t o = off;
+    off += (n + 3) / 4 * 4;
+    return o;
+  };
+  g.ws_norm = norm ? take(batch * len * a.groups * a.rank * 2) : -1;
+  g.ws_ang = angles ? take(batch * g.L4 * a.num_angles * 4) : -1;
+  g.ws_sc = take(batch * a.heads * g.nsub * g.scw);
+  return static_cast<size_t>(off) * sizeof(float);
+}
+
 template <typename T>
 static ScanGeom make_geom(const m3_scan_args& a) {
   ScanGeom g{};
@@ -1383,18 +1441,8 @@ static ScanGeom make_geom(const m3_scan_args& a) {
   g.vec_qk = (a.d_state % 8 == 0) && vec_ok(a.q, 5, 16) && vec_ok(a.k, 5, 16);
   const int vneed = es * 4;  // 4 elements per v / z load
   g.vec_vz = (a.head_dim % 4 == 0) && vec_ok(a.value, 4, vneed) && vec_ok(a.gate, 4, vneed);
-  const bool norm = a.q_norm_w.ptr != nullptr;
-  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
-  const int gr = a.groups * a.rank;
-  g.prep_q = norm ? 0 : -1;
-  g.prep_k = norm ? gr : -1;
-  g.prep_a = angles ? (norm ? 2 * gr : 0) : -1;
-  g.prep_w = (norm ? 2 * gr : 0) + (angles ? a.num_angles : 0);
+  ws_layout(a, g);
   return g;
-}
-
-static size_t workspace_bytes(const m3_scan_args& a, int prep_w) {
-  return static_cast<size_t>(a.batch) * a.length * prep_w * sizeof(float);
 }
 
 // Projection form: q, k, value, gate, dt, a, trap all of the activation dtype and slices of one
@@ -1433,7 +1481,9 @@ static bool projection_form(const m3_scan_args& a, ScanGeom& g, int es) {
   const int64_t out_tok = a.out.stride[1] * es;
   if (((a.heads - 1) * a.out.stride[2] + a.head_dim) * es > out_tok) return false;
   const int64_t len = a.length;
-  if (len * tok >= lim || len * out_tok >= lim || len * g.prep_w * 4 >= lim) {
+  if (len * tok >= lim || len * out_tok >= lim || len * a.groups * a.rank * 8 >= lim ||
+      static_cast<int64_t>(g.L4) * a.num_angles * 16 >= lim ||
+      static_cast<int64_t>(g.nsub) * g.scw * 4 >= lim) {
     return false;
   }
   g.proj = base;
@@ -1460,7 +1510,8 @@ static bool projection_form(const m3_scan_args& a, ScanGeom& g, int es) {
 // rotation) in projection form: the specialization with every shape and mode a compile-time
 // constant and guard-free buffer addressing.
 static bool full_shape(const m3_scan_args& a, ScanGeom& g, int R) {
-  return a.d_state == kNPad && a.head_dim == kPPad && a.num_angles == kSMax &&
+  return a.length > 0 && a.groups == 1 && a.d_state == kNPad && a.head_dim == kPPad &&
+         a.num_angles == kSMax &&
          a.q_norm_w.ptr != nullptr && a.q_bias.ptr != nullptr && a.raw_dt != 0 &&
          a.phase_mode == M3_PHASE_ANGLES && (a.mimo_rotation != 0) == (R > 1) && g.vec_qk &&
          g.vec_vz && projection_form(a, g, a.act_dtype == M3_F32 ? 4 : 2);
@@ -1489,24 +1540,26 @@ static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
   ScanGeom g = make_geom<T>(a);
   static_assert(Layout<T>::BYTES <= 160 * 1024, "LDS layout exceeds 160 KiB");
   const float* prep = nullptr;
-  if (g.prep_w > 0) {
-    const size_t need = workspace_bytes(a, g.prep_w);
+  const size_t need = ws_layout(a, g);
+  if (need > 0) {
     if (a.workspace == nullptr || a.workspace_bytes < need || !aligned16(a.workspace)) {
       return fail(M3_EWORKSPACE, "m3_scan_fwd: needs a 16-byte aligned workspace of %zu bytes",
                   need);
     }
     prep = static_cast<const float*>(a.workspace);
     const int64_t tokens = static_cast<int64_t>(a.batch) * a.length;
-    const int64_t rows = g.prep_q >= 0 ? tokens * 2 * a.groups * a.rank : 0;
-    const int64_t ang = g.prep_a >= 0 ? tokens * a.num_angles : 0;
-    const int64_t row_blocks = (rows + 15) / 16, ang_blocks = (ang + 255) / 256;
-    if (rows >= INT32_MAX || ang >= INT32_MAX) {
+    const int64_t rows = g.ws_norm >= 0 ? tokens * 2 * a.groups * a.rank : 0;
+    const int64_t ang = g.ws_ang >= 0 ? static_cast<int64_t>(a.batch) * g.L4 * a.num_angles * 4 : 0;
+    const int64_t blocks = static_cast<int64_t>(a.batch) * a.heads * g.nsub;
+    if (rows >= INT32_MAX || ang >= INT32_MAX || blocks >= INT32_MAX || tokens >= INT32_MAX) {
       return fail(M3_EUNSUPPORTED, "m3_scan_fwd: too many tokens for one launch");
     }
-    if (row_blocks + ang_blocks > 0) {
-      const dim3 pgrid(static_cast<unsigned>(row_blocks + ang_blocks)), pblock(256);
-      hipLaunchKernelGGL(prep_kernel<T>, pgrid, pblock, 0, stream, a, g,
-                         static_cast<float*>(a.workspace), static_cast<int>(row_blocks));
+    const int64_t nb_norm = (rows + 15) / 16, nb_ang = (ang + 255) / 256, nb_sc = (blocks + 3) / 4;
+    if (nb_norm + nb_ang + nb_sc > 0) {
+      const dim3 pgrid(static_cast<unsigned>(nb_norm + nb_ang + nb_sc)), pblock(256);
+      hipLaunchKernelGGL((prep_kernel<T, R>), pgrid, pblock, 0, stream, a, g,
+                         static_cast<float*>(a.workspace), static_cast<int>(nb_norm),
+                         static_cast<int>(nb_ang));
       int rc = check_launch("m3_scan_fwd (prep)");
       if (rc != M3_OK) return rc;
     }
@@ -1610,12 +1663,6 @@ static int validate_scan(const m3_scan_args& a) {
   return M3_OK;
 }
 
-static int prep_width(const m3_scan_args& a) {
-  const bool norm = a.q_norm_w.ptr != nullptr;
-  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
-  return (norm ? 2 * a.groups * a.rank : 0) + (angles ? a.num_angles : 0);
-}
-
 }  // namespace m3
 
 extern "C" int m3_scan_workspace_size(const m3_scan_args* args, size_t* bytes) {
@@ -1623,7 +1670,8 @@ extern "C" int m3_scan_workspace_size(const m3_scan_args* args, size_t* bytes) {
   if (args == nullptr || bytes == nullptr) {
     return m3::fail(M3_EINVAL, "m3_scan_workspace_size: NULL argument");
   }
-  *bytes = m3::workspace_bytes(*args, m3::prep_width(*args));
+  m3::ScanGeom g{};
+  *bytes = m3::ws_layout(*args, g);
   return M3_OK;
 }
 
