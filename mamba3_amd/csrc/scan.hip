@@ -88,7 +88,7 @@ template <> struct Mma<float> {
 // Compile-time LDS layout. Operand tiles are padded to N = 128 and P = 64 (the largest shapes
 // the kernel takes; every Mamba3 configuration has P <= 64), so every offset and loop bound is a
 // constant; smaller shapes run on zero padding.
-constexpr int kNPad = 128, kPPad = 64, kSMax = 32, kTokMax = 64, kRMax = 4;
+constexpr int kNPad = 128, kPPad = 64, kSMax = 32, kRMax = 4;
 constexpr int kNT = kNPad / 16, kPT = kPPad / 16;  // 16-row tiles of N and P
 
 template <typename T> struct Layout {
@@ -104,12 +104,15 @@ template <typename T> struct Layout {
   static constexpr int ZT = al(VS + kPPad * LR * ES);
   static constexpr int SB = al(ZT + kPPad * LR * ES);
   static constexpr int FB = al(SB + kPPad * LQ * ES);
-  // float scratch, offsets in floats from FB: two per-token scalar blocks (ScBlk) alternating
-  static constexpr int SCB = 7 * kTokMax + 8, SC0 = 0;
-  // cos / sin tables of one sub-chunk: [token][angle][cos, sin] with token stride CST (16-byte
-  // aligned rows), two of them alternating
-  static constexpr int CST = 2 * kSMax + 4, CSB = kTokMax * CST;
-  static constexpr int CS0 = SC0 + 2 * SCB, PBASE = CS0 + 2 * CSB;
+  // float scratch, offsets in floats from FB, sized for TM = ROWS tokens (rank 1): two side
+  // blocks alternating (a sub-chunk's scalar block, ScBlk, then the (q, k) RMSNorm factors of
+  // its rows), the angle tile, two cos / sin tables ([token][angle][cos, sin], token stride CST
+  // for 16-byte aligned rows)
+  static constexpr int TM = ROWS;
+  static constexpr int SCB = 7 * TM + 8 + 2 * ROWS, SC0 = 0;
+  static constexpr int ANG = SC0 + 2 * SCB;  // [TM / 4][kSMax][4]
+  static constexpr int CST = 2 * kSMax + 4, CSB = TM * CST;
+  static constexpr int CS0 = ANG + TM * kSMax, PBASE = CS0 + 2 * CSB;
   static constexpr int POFF = PBASE + kSMax, MX = POFF + kSMax, MZ = MX + kRMax * kPPad;
   static constexpr int MO = MZ + kRMax * kPPad;
   static constexpr int BYTES = FB + 4 * (MO + kRMax * kPPad);
@@ -134,6 +137,7 @@ struct ScanGeom {
   // ceil(L / 4)), scalar blocks [B*H][nsub][scw] of `tok`-token sub-chunks
   int64_t ws_norm, ws_ang, ws_sc;
   int L4, tok, nsub, scw;
+  int ws_bytes;  // workspace bytes when below 2^31 (the projection form addresses it in 32 bits)
   // projection form (the full-shape kernel): q, k, value, gate, dt, a, trap are slices of one
   // projection row; byte offsets of each slice from `proj`, the batch / token strides and the
   // group / rank / head strides of the slices, in bytes
@@ -362,61 +366,69 @@ __device__ __forceinline__ void bstore_elem(float x, __amdgpu_buffer_rsrc_t r, i
   }
 }
 
-// Per-token global reads of one (batch, head). FULL: every per-token input is a slice of one
-// projection row (host-checked), read at per-lane byte offsets through one buffer resource per
-// batch row whose extent ends at token L, so rows of tokens >= L read as zero without guards;
-// the prep regions likewise. Otherwise element pointers with explicit guards. TPL: tokens per
-// phase lane.
-template <typename T, int R, bool FULL, int TPL>
+// Global reads of one (batch, head). Per sub-chunk: the q / k and value / gate words of each
+// lane's rows, and the side data the block stages through LDS: its scalar block followed by the
+// RMSNorm factors of its rows (SIDE floats, one 8-byte word per lane) and its angle tile (4
+// consecutive tokens of one angle per 16-byte word, TOK * S floats). FULL: every per-token input
+// is a slice of one projection row (host-checked), read at per-lane byte offsets through one
+// buffer resource per batch row whose extent ends at token L, so rows of tokens >= L read as
+// zero without guards; the workspace likewise through one resource. Otherwise element pointers
+// with explicit guards.
+template <typename T, int R, bool FULL>
 struct Feed {
   static constexpr int ES = sizeof(T), W8 = Words<T>::W8, W4 = Words<T>::W4;
-  static constexpr int TOK = Mma<T>::ROWS / R;
+  static constexpr int ROWS = Mma<T>::ROWS, TOK = ROWS / R;
   // FULL
-  __amdgpu_buffer_rsrc_t rs_p, rs_n, rs_a, rs_s;
-  int o_qk, o_vz, o_fn, o_an;  // per-lane byte offsets at token 0
-  int d_q1, d_k, d_z, tok_b, fn_b, an_b;  // uniform byte deltas / strides
+  __amdgpu_buffer_rsrc_t rs_p, rs_w;
+  int o_qk, o_vz, d_q1, d_k, d_z, tok_b;  // per-lane byte offsets at token 0, uniform deltas
+  int side_o, side_s, ang_o, ang_s;        // per-lane workspace byte offsets at sub-chunk 0, strides
   // generic
   const T *q_row, *k_row, *v_row, *z_row;
-  const float *norm_row, *ang_row, *ph_row;
-  int q_t, q_r, k_t, k_r, v_t, z_t, ph_t, fn_o, qk_n, vz_n, S;
-  bool vec_qk, vec_vz, norm, angles;
-  // both
-  const float* sc_row;  // this (b, h)'s scalar blocks
-  int scw, nsub, L4;
-  int rp, vp, pg, ps;
+  const float *side_p, *ang_p;  // this lane's side / angle word at sub-chunk 0 (null: none)
+  const float* ph_row;          // given phases of (b, h): [L][S] with strides ph_t, ph_s
+  int64_t side_ps, ang_ps;      // per-sub-chunk strides (floats)
+  int q_t, q_r, k_t, k_r, v_t, z_t, ph_t, ph_s, qk_n, vz_n;
+  int side_tok, side_lim;       // norm words: token of the word (sub-chunk 0), last valid
+  bool vec_qk, vec_vz, given;
+  int rp, vp, nsub, L, S, L4;
 
   __device__ __forceinline__ void init(const m3_scan_args& a, const ScanGeom& g,
                                        const float* prep, int b, int h, int grp, int rp_,
-                                       int n0, int vp_, int p0, int pg_, int ps_, int N, int P,
-                                       bool norm_, bool angles_) {
-    const int L = a.length, GR = a.groups * a.rank;
+                                       int n0, int vp_, int p0, int N, int P, bool norm) {
+    L = a.length;
+    S = a.num_angles;
+    L4 = g.L4;
     rp = rp_;
     vp = vp_;
-    pg = pg_;
-    ps = ps_;
-    norm = norm_;
-    angles = angles_;
-    S = a.num_angles;
-    scw = g.scw;
     nsub = g.nsub;
-    L4 = g.L4;
+    const int GR = a.groups * a.rank, H = a.heads, tid = threadIdx.x;
     const int tt0 = (2 * rp) / R, r0 = (2 * rp) % R;
-    sc_row = prep + g.ws_sc + static_cast<int64_t>(b * a.heads + h) * nsub * scw;
+    const int scw = g.scw;
+    // side word of this lane: floats 2 tid, 2 tid + 1 of [scalar block (scw) | norms (2 ROWS)]
+    const int q2 = 2 * tid;
+    const int64_t sc0 = g.ws_sc + static_cast<int64_t>(b * H + h) * nsub * scw + q2;
+    const int nrow = (q2 - scw) >> 1;  // norm word: row of the sub-chunk (token nrow / R)
     if constexpr (FULL) {
       tok_b = g.tok_b;
       rs_p = make_rsrc(g.proj + b * g.proj_b, L * tok_b);
-      fn_b = GR * 8;  // bytes of one token's (q, k) factor pairs
-      rs_n = make_rsrc(prep + g.ws_norm + static_cast<int64_t>(b) * L * GR * 2, L * fn_b);
-      o_fn = (tt0 * GR + grp * R + r0) * 8;
-      an_b = S * 16;  // one 4-token group of all angles
-      rs_a = make_rsrc(prep + g.ws_ang + static_cast<int64_t>(b) * L4 * S * 4, L4 * an_b);
-      o_an = ((TPL / 4) * pg * S + ps) * 16;
-      rs_s = make_rsrc(sc_row, nsub * scw * 4);
+      rs_w = make_rsrc(prep, g.ws_bytes);
       o_qk = g.o_q + grp * g.qk_g + r0 * g.qk_r + tt0 * tok_b + n0 * ES;
       o_vz = g.o_v + h * g.vz_h + 2 * vp * tok_b + p0 * ES;
       d_q1 = R == 1 ? tok_b : g.qk_r;  // row 2rp + 1: the next token (R = 1) or the next rank
       d_k = g.o_k - g.o_q;
       d_z = g.o_z - g.o_v;
+      // groups == 1: the norm pairs of a sub-chunk's rows are 2 ROWS contiguous floats
+      if (q2 < scw) {
+        side_o = static_cast<int>(sc0) * 4;
+        side_s = scw * 4;
+      } else if (q2 < scw + 2 * ROWS) {
+        side_o = static_cast<int>(g.ws_norm + static_cast<int64_t>(b) * L * GR * 2 + q2 - scw) * 4;
+        side_s = TOK * GR * 2 * 4;
+      } else {
+        side_o = side_s = 0;
+      }
+      ang_o = static_cast<int>(g.ws_ang + static_cast<int64_t>(b) * g.L4 * S * 4 + 4 * tid) * 4;
+      ang_s = (TOK / 4) * S * 16;
     } else {
       q_row = static_cast<const T*>(a.q.ptr) + b * a.q.stride[0] + grp * a.q.stride[2] + n0;
       k_row = static_cast<const T*>(a.k.ptr) + b * a.k.stride[0] + grp * a.k.stride[2] + n0;
@@ -430,27 +442,44 @@ struct Feed {
               p0;
       v_t = static_cast<int>(a.value.stride[1]);
       z_t = static_cast<int>(a.gate.stride[1]);
-      norm_row = norm ? prep + g.ws_norm + static_cast<int64_t>(b) * L * GR * 2 : nullptr;
-      fn_o = grp * R;
-      ang_row = angles ? prep + g.ws_ang + static_cast<int64_t>(b) * L4 * S * 4 : nullptr;
-      const bool given = a.phase_mode == M3_PHASE_GIVEN;
-      ph_row = given ? static_cast<const float*>(a.phase.ptr) + b * a.phase.stride[0] +
-                           h * a.phase.stride[2] + ps * a.phase.stride[3]
-                     : nullptr;
-      ph_t = given ? static_cast<int>(a.phase.stride[1]) : 0;
       qk_n = max(0, min(8, N - n0));
       vz_n = max(0, min(4, P - p0));
       vec_qk = g.vec_qk;
       vec_vz = g.vec_vz;
+      side_p = nullptr;
+      side_tok = 0;
+      side_lim = INT32_MAX;
+      if (q2 < scw) {
+        side_p = prep + sc0;
+        side_ps = scw;
+      } else if (q2 < scw + 2 * ROWS && norm) {
+        // rows are (token, rank); a word holds the (q, k) pair of one row
+        const int tr = nrow / R, rr = nrow - tr * R;
+        side_p = prep + g.ws_norm + (static_cast<int64_t>(b) * L * GR + tr * GR + grp * R + rr) * 2;
+        side_ps = static_cast<int64_t>(TOK) * GR * 2;
+        side_tok = tr;
+        side_lim = L - 1;
+      }
+      given = a.phase_mode == M3_PHASE_GIVEN;
+      ang_p = nullptr;
+      ph_row = nullptr;
+      if (a.phase_mode == M3_PHASE_ANGLES && 4 * tid < TOK * S) {
+        ang_p = prep + g.ws_ang + static_cast<int64_t>(b) * g.L4 * S * 4 + 4 * tid;
+        ang_ps = (TOK / 4) * S * 4;
+      } else if (given && 4 * tid < TOK * S) {
+        ph_row = static_cast<const float*>(a.phase.ptr) + b * a.phase.stride[0] +
+                 h * a.phase.stride[2];
+        ph_t = static_cast<int>(a.phase.stride[1]);
+        ph_s = static_cast<int>(a.phase.stride[3]);
+      }
     }
   }
 
   // q / k rows 2rp, 2rp+1 and value / gate tokens 2vp, 2vp+1 of the sub-chunk at token t0
-  // (nw valid tokens); FULL also the RMSNorm factors of the q / k rows (else factors()).
+  // (nw valid tokens)
   __device__ __forceinline__ void words(int t0, int nw, bool qk_on, bool vz_on,
                                         uint32_t (&rq)[2][W8], uint32_t (&rk)[2][W8],
-                                        uint32_t (&rv)[2][W4], uint32_t (&rz)[2][W4],
-                                        float (&fq)[2], float (&fk)[2]) const {
+                                        uint32_t (&rv)[2][W4], uint32_t (&rz)[2][W4]) const {
     if constexpr (FULL) {
       // unconditional, also for lanes without a q/k or v/z role: every offset stays inside a
       // buffer or past its extent, where the load returns zero
@@ -459,24 +488,6 @@ struct Feed {
       for (int j = 0; j < 2; ++j) {
         bload_words<W8>(rq[j], rs_p, o_qk + tb + j * d_q1);
         bload_words<W8>(rk[j], rs_p, o_qk + tb + j * d_q1 + d_k);
-      }
-      // (q, k) factor pairs of rows 2rp, 2rp+1: R > 1, 16 bytes of one token; R = 1, 8 bytes of
-      // each of two tokens (two loads, so a pair past token L never shares a load with one before)
-      if constexpr (R > 1) {
-        const u32x4 f = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_n, o_fn + t0 * fn_b, 0, 0));
-        fq[0] = __uint_as_float(f[0]);
-        fk[0] = __uint_as_float(f[1]);
-        fq[1] = __uint_as_float(f[2]);
-        fk[1] = __uint_as_float(f[3]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const u32x2 f = __builtin_bit_cast(
-              u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_n, o_fn + (t0 + j) * fn_b, 0, 0));
-          fq[j] = __uint_as_float(f[0]);
-          fk[j] = __uint_as_float(f[1]);
-        }
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -507,55 +518,49 @@ struct Feed {
     }
   }
 
-  // the RMSNorm factors of rows 2rp, 2rp+1 (generic path; GR = groups * rank)
-  __device__ __forceinline__ void factors(int t0, int nw, int GR, bool qk_on, float (&fq)[2],
-                                          float (&fk)[2]) const {
-    if constexpr (!FULL) {
-      if (!qk_on || !norm) return;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int row = 2 * rp + j, tt = row / R, r = row - tt * R;
-        if (tt < nw) {
-          const float* pr = norm_row + (static_cast<int64_t>(t0 + tt) * GR + fn_o + r) * 2;
-          fq[j] = pr[0];
-          fk[j] = pr[1];
-        }
+  // this lane's side word of sub-chunk c (FULL: unconditional; unused words read anything)
+  __device__ __forceinline__ float2 side_in(int c) const {
+    if constexpr (FULL) {
+      const u32x2 v = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_w, side_o + c * side_s, 0, 0));
+      return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+    } else {
+      float2 v = make_float2(1.f, 1.f);
+      if (side_p != nullptr && c < nsub && side_tok + c * TOK <= side_lim) {
+        v = *reinterpret_cast<const float2*>(side_p + c * side_ps);
       }
+      return v;
     }
   }
 
-  // angle inputs of tokens TPL pg .. TPL pg + TPL-1 (pi tanh(angle) from the prep region, or
-  // given phases)
-  __device__ __forceinline__ void angle_in(int t0, int nw, bool ph_on, float (&pa)[TPL]) const {
+  // this lane's angle word of sub-chunk c: in the tile order [TOK/4][S][4], 4-token group
+  // tid / S of angle tid % S
+  __device__ __forceinline__ float4 ang_in(int c) const {
     if constexpr (FULL) {
-#pragma unroll
-      for (int q = 0; q < TPL / 4; ++q) {
-        const u32x4 v = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_a, o_an + (t0 / 4 + q) * an_b, 0, 0));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pa[4 * q + i] = __uint_as_float(v[i]);
-      }
+      const u32x4 v = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_w, ang_o + c * ang_s, 0, 0));
+      return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                         __uint_as_float(v[3]));
     } else {
-      if (!ph_on) return;
-#pragma unroll
-      for (int i = 0; i < TPL; ++i) {
-        const int tt = TPL * pg + i;
-        const int tg = t0 + tt;
-        pa[i] = 0.f;
-        if (tt < nw) {
-          pa[i] = angles ? ang_row[(static_cast<int64_t>(tg >> 2) * S + ps) * 4 + (tg & 3)]
-                         : ph_row[tg * ph_t];
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (c >= nsub) return v;
+      if (ang_p != nullptr) {
+        if (c * (TOK / 4) + static_cast<int>(threadIdx.x) / S < L4) {  // groups past L4: none
+          v = *reinterpret_cast<const float4*>(ang_p + c * ang_ps);
         }
+      } else if (ph_row != nullptr) {
+        // tile word tid = (group, angle): tokens 4 group .. + 3 of that angle
+        const int tid = threadIdx.x;
+        const int grp4 = tid / S, sa = tid - grp4 * S;
+        float e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = c * TOK + 4 * grp4 + i;
+          e[i] = t < L ? ph_row[static_cast<int64_t>(t) * ph_t + sa * ph_s] : 0.f;
+        }
+        v = make_float4(e[0], e[1], e[2], e[3]);
       }
-    }
-  }
-
-  // one float of sub-chunk c's scalar block (lanes below scw)
-  __device__ __forceinline__ float sc_in(int c, int tid) const {
-    if constexpr (FULL) {
-      return bload_f32(rs_s, (c * scw + tid) * 4);
-    } else {
-      return (c < nsub && tid < scw) ? sc_row[static_cast<int64_t>(c) * scw + tid] : 0.f;
+      return v;
     }
   }
 };
@@ -964,9 +969,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   }
 
   // ---- per-token reads
-  Feed<T, R, FULL, TPL> fd;
-  fd.init(a, g, prep, b, h, grp, rp, n0, vp, p0, pg, ps, N, P, norm, angles);
-  const int GR = a.groups * R;
+  Feed<T, R, FULL> fd;
+  fd.init(a, g, prep, b, h, grp, rp, n0, vp, p0, N, P, norm);
   float* fph = a.final_phase.ptr != nullptr
                    ? static_cast<float*>(a.final_phase.ptr) + b * a.final_phase.stride[0] +
                          h * a.final_phase.stride[1] + ps * a.final_phase.stride[2]
@@ -1004,32 +1008,44 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // ---- registers the global data of coming sub-chunks is loaded into
   constexpr int W8 = Words<T>::W8, W4 = Words<T>::W4;
   uint32_t rq[2][W8], rk[2][W8], rv[2][W4], rz[2][W4];
-  float fq[2] = {1.f, 1.f}, fk[2] = {1.f, 1.f};
-  float pa[TPL];
-#pragma unroll
-  for (int i = 0; i < TPL; ++i) pa[i] = 0.f;
-  float scv = 0.f;  // lanes below scw: one float of a coming sub-chunk's scalar block
+  float2 side;   // this lane's side word of a coming sub-chunk
+  float4 ang;    // this lane's angle word of a coming sub-chunk
   const int nsub = g.nsub, scw = g.scw;
+  const int side_n = scw + 2 * ROWS;  // floats of a side block
+  float* ANG = F + Lay::ANG;
+  // the angle inputs of this phase lane's tokens, from the angle tile
+  auto angles_of = [&](float (&pa)[TPL]) {
+#pragma unroll
+    for (int q = 0; q < TPL / 4; ++q) {
+      const float4 v = *reinterpret_cast<const float4*>(ANG + (((TPL / 4) * pg + q) * S + ps) * 4);
+      pa[4 * q] = v.x;
+      pa[4 * q + 1] = v.y;
+      pa[4 * q + 2] = v.z;
+      pa[4 * q + 3] = v.w;
+    }
+  };
   auto scb = [&](int c) { return F + Lay::SC0 + (c & 1) * Lay::SCB; };
   auto csb = [&](int c) { return F + Lay::CS0 + (c & 1) * Lay::CSB; };
 
-  // Pipeline: iteration c stages sub-chunk c into LDS and copies the scalar block of c + 1 there
-  // (interval 1), then computes the outputs and state carry of c while the phases of c + 1 are
-  // computed and the loads of c + 1 (words), c + 2 (angles, scalar block) are in flight
-  // (interval 2). Scalar blocks and cos / sin tables alternate between two LDS buffers each.
-  // prologue: scalar block 0 to LDS, phases of 0
-  scv = fd.sc_in(0, tid);
-  fd.words(0, min(TOK, L), qk_on, vz_on, rq, rk, rv, rz, fq, fk);
-  fd.factors(0, min(TOK, L), GR, qk_on, fq, fk);
-  fd.angle_in(0, min(TOK, L), ph_on, pa);
-  if (tid < scw) scb(0)[tid] = scv;
-  scv = fd.sc_in(1, tid);
+  // Pipeline: iteration c stages sub-chunk c into LDS and writes the side block and angle tile of
+  // c + 1 there (interval 1), then computes the outputs and state carry of c while the phases of
+  // c + 1 are computed and the loads of c + 1 (words) and c + 2 (side, angles) are in flight
+  // (interval 2). Side blocks and cos / sin tables alternate between two LDS buffers each.
+  // prologue: side block and angle tile of 0 to LDS, phases of 0
+  side = fd.side_in(0);
+  ang = fd.ang_in(0);
+  fd.words(0, min(TOK, L), qk_on, vz_on, rq, rk, rv, rz);
+  if (2 * tid < side_n) *reinterpret_cast<float2*>(scb(0) + 2 * tid) = side;
+  if (4 * tid < TOK * S) *reinterpret_cast<float4*>(ANG + 4 * tid) = ang;
+  side = fd.side_in(1);
+  ang = fd.ang_in(1);
   __syncthreads();
   if (ph_on && nsub > 0) {
+    float pa[TPL];
+    angles_of(pa);
     phase_stage<PG, TPL, CST, SPLIT>(csb(0), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
                                      scb(0) + SB_::DTV, 0, L, pg, lane, angles, pa, fph);
   }
-  if (FULL || nsub > 1) fd.angle_in(TOK, min(TOK, L - TOK), ph_on, pa);
   __syncthreads();
 
   for (int c = 0; c < nsub; ++c) {
@@ -1039,9 +1055,21 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     const float* CSt = csb(c);
 
     // ---- interval 1: stage sub-chunk c; the scalar block of c + 1 to LDS
-    if (tid < scw && c + 1 < nsub) scb(c + 1)[tid] = scv;
+    if (c + 1 < nsub) {
+      if (2 * tid < side_n) *reinterpret_cast<float2*>(scb(c + 1) + 2 * tid) = side;
+      if (4 * tid < TOK * S) *reinterpret_cast<float4*>(ANG + 4 * tid) = ang;
+    }
     // q / k rows -> Qs, Ks (row-major), KT (transposed, swizzled); rows 2rp, 2rp+1
     if (qk_on) {
+      // (q, k) RMSNorm factors of rows 2rp, 2rp+1
+      float fq[2] = {1.f, 1.f}, fk[2] = {1.f, 1.f};
+      if (norm) {
+        const float4 f = *reinterpret_cast<const float4*>(SC + scw + 4 * rp);
+        fq[0] = f.x;
+        fk[0] = f.y;
+        fq[1] = f.z;
+        fk[1] = f.w;
+      }
       float kt[2][8];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -1167,10 +1195,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     // every load of the loop unconditionally (reads past token L return zero), which keeps the
     // compiler's in-order wait counts exact: no load is waited for before its use.
     if (FULL || c + 1 < nsub) {
-      fd.words(t0 + TOK, min(TOK, L - t0 - TOK), qk_on, vz_on, rq, rk, rv, rz, fq, fk);
-      fd.factors(t0 + TOK, min(TOK, L - t0 - TOK), GR, qk_on, fq, fk);
+      fd.words(t0 + TOK, min(TOK, L - t0 - TOK), qk_on, vz_on, rq, rk, rv, rz);
     }
-    scv = fd.sc_in(c + 2, tid);
+    side = fd.side_in(c + 2);
+    ang = fd.ang_in(c + 2);
 
     // outputs for query row tile `it` and P tiles pj = wp, wp + WPR, ...
     const int it = w / WPR, wp = w - it * WPR;
@@ -1232,12 +1260,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     }
     // phases of sub-chunk c + 1 (its dt block was computed two iterations ago)
     if (ph_on && c + 1 < nsub) {
+      float pa[TPL];
+      angles_of(pa);
       phase_stage<PG, TPL, CST, SPLIT>(csb(c + 1), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
                                        scb(c + 1) + SB_::DTV, t0 + TOK, L, pg, lane, angles, pa,
                                        fph);
-    }
-    if (FULL || (ph_on && c + 2 < nsub)) {
-      fd.angle_in(t0 + 2 * TOK, min(TOK, L - t0 - 2 * TOK), ph_on, pa);
     }
     // decayed scores W[t, s] = Sc[t, s] d[t, s] in FP32
     const float cum_t = SC[SB_::CUM + tq];
@@ -1421,7 +1448,10 @@ static size_t ws_layout(const m3_scan_args& a, ScanGeom& g) {
   g.ws_norm = norm ? take(batch * len * a.groups * a.rank * 2) : -1;
   g.ws_ang = angles ? take(batch * g.L4 * a.num_angles * 4) : -1;
   g.ws_sc = take(batch * a.heads * g.nsub * g.scw);
-  return static_cast<size_t>(off) * sizeof(float);
+  const int64_t bytes = off * static_cast<int64_t>(sizeof(float));
+  // the projection form's 32-bit offsets run up to two sub-chunk strides past the end
+  g.ws_bytes = bytes < (int64_t{1} << 30) ? static_cast<int>(bytes) : -1;
+  return static_cast<size_t>(bytes);
 }
 
 template <typename T>
@@ -1510,7 +1540,8 @@ static bool projection_form(const m3_scan_args& a, ScanGeom& g, int es) {
 // rotation) in projection form: the specialization with every shape and mode a compile-time
 // constant and guard-free buffer addressing.
 static bool full_shape(const m3_scan_args& a, ScanGeom& g, int R) {
-  return a.length > 0 && a.groups == 1 && a.d_state == kNPad && a.head_dim == kPPad &&
+  return a.length > 0 && a.groups == 1 && g.ws_bytes > 0 && a.d_state == kNPad &&
+         a.head_dim == kPPad &&
          a.num_angles == kSMax &&
          a.q_norm_w.ptr != nullptr && a.q_bias.ptr != nullptr && a.raw_dt != 0 &&
          a.phase_mode == M3_PHASE_ANGLES && (a.mimo_rotation != 0) == (R > 1) && g.vec_qk &&
