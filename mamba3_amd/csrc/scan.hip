@@ -94,15 +94,16 @@ constexpr int kNT = kNPad / 16, kPT = kPPad / 16;  // 16-row tiles of N and P
 template <typename T> struct Layout {
   static constexpr int ROWS = Mma<T>::ROWS, PAD = Mma<T>::PAD, ES = sizeof(T);
   static constexpr int LQ = kNPad + PAD;   // row stride (elements) of Qs, Ks, Sb
-  static constexpr int LR = ROWS + PAD;    // row stride (elements) of KT, VT, VsT, ZT
+  static constexpr int LR = ROWS + PAD;    // row stride (elements) of KT, VT
+  static constexpr int LP = kPPad + PAD;   // row stride (elements) of VR, ZR
   static constexpr int al(int x) { return (x + 15) / 16 * 16; }
   static constexpr int QS = 0;
   static constexpr int KS = al(QS + ROWS * LQ * ES);
   static constexpr int KT = al(KS + ROWS * LQ * ES);
   static constexpr int VT = al(KT + kNPad * LR * ES);
-  static constexpr int VS = al(VT + kPPad * LR * ES);
-  static constexpr int ZT = al(VS + kPPad * LR * ES);
-  static constexpr int SB = al(ZT + kPPad * LR * ES);
+  static constexpr int VR = al(VT + kPPad * LR * ES);
+  static constexpr int ZR = al(VR + ROWS * LP * ES);
+  static constexpr int SB = al(ZR + ROWS * LP * ES);
   static constexpr int FB = al(SB + kPPad * LQ * ES);
   // float scratch, offsets in floats from FB, sized for TM = ROWS tokens (rank 1): two side
   // blocks alternating (a sub-chunk's scalar block, ScBlk, then the (q, k) RMSNorm factors of
@@ -353,6 +354,19 @@ __device__ __forceinline__ float bload_elem(__amdgpu_buffer_rsrc_t r, int off) {
   } else {
     const uint32_t bits = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
     return bits_to_f(bits, static_cast<T*>(nullptr));
+  }
+}
+
+// Four consecutive activation values stored as one vector (8 bytes for 16-bit types).
+template <typename T>
+__device__ __forceinline__ void bstore_quad(f4 x, __amdgpu_buffer_rsrc_t r, int off) {
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, off, 0, 0);
+  } else {
+    typename Mma<T>::v4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = from_f<T>(x[i]);
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, off, 0, 0);
   }
 }
 
@@ -796,7 +810,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   constexpr int TOK = ROWS / R;        // tokens per sub-chunk
   constexpr bool F32 = sizeof(T) == 4;
   constexpr int ES = sizeof(T);
-  constexpr int LQ = Lay::LQ, LR = Lay::LR, NP = kNPad, CST = Lay::CST;
+  constexpr int LQ = Lay::LQ, LR = Lay::LR, LP = Lay::LP, NP = kNPad, CST = Lay::CST;
   using SB_ = ScBlk<TOK>;
   // SISO model shape: q / k lanes split by column half, waves 0-3 holding the rotated columns;
   // the phase on waves 0-3 only, 8 tokens per lane (their compute interval is the shorter one)
@@ -833,9 +847,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   T* Qs = lds_t<T>(smem, Lay::QS);
   T* Ks = lds_t<T>(smem, Lay::KS);
   T* KT = lds_t<T>(smem, Lay::KT);
-  T* VT = lds_t<T>(smem, Lay::VT);
-  T* VsT = lds_t<T>(smem, Lay::VS);
-  T* ZT = lds_t<T>(smem, Lay::ZT);
+  T* VT = lds_t<T>(smem, Lay::VT);  // [p][row] rank values v mx_r, transposed (intra, carry)
+  T* VR = lds_t<T>(smem, Lay::VR);  // [row][p] the same, row-major (epilogue D v)
+  T* ZR = lds_t<T>(smem, Lay::ZR);  // [row][p] rank gates z mz_r, row-major (epilogue)
   T* Sb = lds_t<T>(smem, Lay::SB);
   float* F = lds_t<float>(smem, Lay::FB);
   const float Dh = ldx(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
@@ -1131,15 +1145,19 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
         for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
       }
+      // K^T for the carry, each row scaled by its token's scale * end decay (the carry's
+      // K~ e^{cum_last - cum}, ops.py:806-816)
+      const float e0 = SC[SB_::VSF + (2 * rp) / R], e1 = SC[SB_::VSF + (2 * rp + 1) / R];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int n = n0 + i;
         if (FULL || n < N) {
-          st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> 3), kt[0][i], kt[1][i]);
+          st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> 3), kt[0][i] * e0, kt[1][i] * e1);
         }
       }
     }
-    // value / gate -> VT, VsT, ZT (transposed, swizzled), tokens 2vp, 2vp+1
+    // value / gate of tokens 2vp, 2vp+1, columns p0 .. p0+3: rank values v mx_r -> VT
+    // (transposed, swizzled) and VR (row-major), rank gates z mz_r -> ZR (row-major)
     if (vz_on) {
       float v[2][4], z[2][4];
 #pragma unroll
@@ -1150,30 +1168,48 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           z[j][i] = raw_get<T>(rz[j], i);
         }
       }
-      const float f0 = SC[SB_::VSF + 2 * vp], f1 = SC[SB_::VSF + 2 * vp + 1];
+      if (R == 1) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = p0 + i;
-        if (!FULL && p >= P) continue;
-        const int key = p >> 2;
-        if (R == 1) {
-          const int row = swz<ROWS>(2 * vp, key);
-          st_pair<T>(VT + p * LR + row, v[0][i], v[1][i]);
-          st_pair<T>(VsT + p * LR + row, v[0][i] * f0, v[1][i] * f1);
-          st_pair<T>(ZT + p * LR + row, z[0][i], z[1][i]);
-        } else {
+        for (int i = 0; i < 4; ++i) {
+          const int p = p0 + i;
+          if (FULL || p < P) st_pair<T>(VT + p * LR + swz<ROWS>(2 * vp, p >> 2), v[0][i], v[1][i]);
+        }
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const float fj = j ? f1 : f0;
+        for (int j = 0; j < 2; ++j) {
+          f4 vq, zq;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            vq[i] = v[j][i];
+            zq[i] = z[j][i];
+          }
+          st_quad<T>(VR + (2 * vp + j) * LP + p0, vq);
+          st_quad<T>(ZR + (2 * vp + j) * LP + p0, zq);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const int row = (2 * vp + j) * R + r;
+            f4 vq, zq;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              vq[i] = mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p0 + i]);
+              zq[i] = mul_r<T>(z[j][i], F[Lay::MZ + r * kPPad + p0 + i]);
+            }
+            st_quad<T>(VR + row * LP + p0, vq);
+            st_quad<T>(ZR + row * LP + p0, zq);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int p = p0 + i;
+            if (!FULL && p >= P) continue;
 #pragma unroll
             for (int r = 0; r < R; r += 2) {
-              const int row = swz<ROWS>((2 * vp + j) * R + r, key);
-              const float va = mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p]);
-              const float vb = mul_r<T>(v[j][i], F[Lay::MX + (r + 1) * kPPad + p]);
-              st_pair<T>(VT + p * LR + row, va, vb);
-              st_pair<T>(VsT + p * LR + row, va * fj, vb * fj);
-              st_pair<T>(ZT + p * LR + row, mul_r<T>(z[j][i], F[Lay::MZ + r * kPPad + p]),
-                         mul_r<T>(z[j][i], F[Lay::MZ + (r + 1) * kPPad + p]));
+              const int row = (2 * vp + j) * R + r;
+              st_pair<T>(VT + p * LR + swz<ROWS>(row, p >> 2),
+                         mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p]),
+                         mul_r<T>(v[j][i], F[Lay::MX + (r + 1) * kPPad + p]));
             }
           }
         }
@@ -1232,7 +1268,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
       }
     }
-    // K^T Vs products of the state carry, issued early: they depend only on staged tiles
+    // K~^T V products of the state carry, issued early: they depend only on staged tiles
     f4 cacc[kTiles];
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) {
@@ -1247,14 +1283,14 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
               KT + nrow * LR + swz<ROWS>(kk + 8 * lg, nrow >> 3));
           const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
-              VsT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> 2));
+              VT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> 2));
           cacc[k] = M::mma(av, bv, cacc[k]);
         }
       } else {
 #pragma unroll
         for (int kk = 0; kk < ROWS; kk += 4) {
           cacc[k] = M::mma(KT[nrow * LR + swz<ROWS>(kk + lg, nrow >> 3)],
-                           VsT[prow * LR + swz<ROWS>(kk + lg, prow >> 2)], cacc[k]);
+                           VT[prow * LR + swz<ROWS>(kk + lg, prow >> 2)], cacc[k]);
         }
       }
     }
@@ -1292,17 +1328,18 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
       }
     }
-    float ecum[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ecum[i] = SC[SB_::ECUM + (16 * it + 4 * lg + i) / R];
+    // Outputs, computed transposed (Y^T tiles, rows p, columns the row tile's 16 (token, rank)
+    // rows): a lane holds 4 consecutive p of one row, stored as one vector.
+    const float ecum_t = SC[SB_::ECUM + tq];
+    const int rr = trow - tq * R;  // the lane's rank
 #pragma unroll
     for (int pq = 0; pq < kPT / WPR; ++pq) {
       const int pj = wp + pq * WPR;
-      const int pcol = 16 * pj + l16;
+      const int pcol = 16 * pj + l16;  // the A-operand row of V^T / rnd(S)
       const int key = pcol >> 2;
       f4 yi = zero4(), ye = zero4();
       if constexpr (!F32) {
-        // intra: W V with the K axis permuted as the D-layout of wsc
+        // intra: V^T W^T, the K axis permuted as the D-layout of wsc
 #pragma unroll
         for (int m = 0; m < (RT + 1) / 2; ++m) {
           if (2 * m > it) continue;
@@ -1313,19 +1350,19 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
               VT + pcol * LR + swz<ROWS>(32 * m + 16 + 4 * lg, key));
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            av[i] = from_f<T>(wsc[2 * m][i]);
-            av[4 + i] = from_f<T>(2 * m + 1 < RT ? wsc[2 * m + 1][i] : 0.f);
-            bv[i] = b0[i];
-            bv[4 + i] = b1[i];
+            bv[i] = from_f<T>(wsc[2 * m][i]);
+            bv[4 + i] = from_f<T>(2 * m + 1 < RT ? wsc[2 * m + 1][i] : 0.f);
+            av[i] = b0[i];
+            av[4 + i] = b1[i];
           }
           yi = M::mma(av, bv, yi);
         }
-        // inter: Q rnd(S)^T
+        // inter: rnd(S) Q^T
 #pragma unroll
         for (int kk = 0; kk < NP / 32; ++kk) {
-          const typename M::v8 bv =
+          const typename M::v8 av =
               *reinterpret_cast<const typename M::v8*>(Sb + pcol * LQ + 32 * kk + 8 * lg);
-          ye = M::mma(qv[kk], bv, ye);
+          ye = M::mma(av, qv[kk], ye);
         }
       } else {
 #pragma unroll
@@ -1333,55 +1370,66 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           if (sj > it) continue;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            yi = M::mma(wsc[sj][i], VT[pcol * LR + swz<ROWS>(16 * sj + 4 * lg + i, key)], yi);
+            yi = M::mma(VT[pcol * LR + swz<ROWS>(16 * sj + 4 * lg + i, key)], wsc[sj][i], yi);
           }
         }
 #pragma unroll 8
         for (int kk = 0; kk < NP; kk += 4) {
-          ye = M::mma(Qs[trow * LQ + kk + lg], Sb[pcol * LQ + kk + lg], ye);
+          ye = M::mma(Sb[pcol * LQ + kk + lg], Qs[trow * LQ + kk + lg], ye);
         }
       }
-      // epilogue: rows 16 it + 4 lg + i, column pcol
-      if (FULL || pcol < P) {
-        float vv[4], zz[4];
-        if constexpr (!F32) {
-          const typename M::v4 v4 = *reinterpret_cast<const typename M::v4*>(
-              VT + pcol * LR + swz<ROWS>(16 * it + 4 * lg, key));
-          const typename M::v4 z4 = *reinterpret_cast<const typename M::v4*>(
-              ZT + pcol * LR + swz<ROWS>(16 * it + 4 * lg, key));
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            vv[i] = to_f(v4[i]);
-            zz[i] = to_f(z4[i]);
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            vv[i] = VT[pcol * LR + swz<ROWS>(16 * it + 4 * lg + i, key)];
-            zz[i] = ZT[pcol * LR + swz<ROWS>(16 * it + 4 * lg + i, key)];
-          }
-        }
-        float y = 0.f;
+      // epilogue: row trow (token tq, rank rr), columns pb .. pb+3
+      const int pb = 16 * pj + 4 * lg;
+      float vv[4], zz[4];
+      if constexpr (!F32) {
+        const typename M::v4 v4 = *reinterpret_cast<const typename M::v4*>(VR + trow * LP + pb);
+        const typename M::v4 z4 = *reinterpret_cast<const typename M::v4*>(ZR + trow * LP + pb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int row = 16 * it + 4 * lg + i;
-          const int tt = row / R, r = row - tt * R;
-          float yr = (fmaf(ye[i], ecum[i], yi[i]) + Dh * vv[i]) * silu_fast(zz[i]);
-          if (R > 1) yr *= F[Lay::MO + r * kPPad + pcol];
-          y = (R > 1 && r > 0) ? y + yr : yr;
-          if (r == R - 1) {
-            if constexpr (FULL) {
-              // rows of tokens >= L fall outside the buffer extent: the store is dropped
-              bstore_elem<T>(y, rs_o, (t0 + tt) * out_t + o_out + pcol * ES);
-            } else {
-              if (tt < width) out_row[(t0 + tt) * out_t + pcol] = from_f<T>(y);
+          vv[i] = to_f(v4[i]);
+          zz[i] = to_f(z4[i]);
+        }
+      } else {
+        const f4 v4 = *reinterpret_cast<const f4*>(VR + trow * LP + pb);
+        const f4 z4 = *reinterpret_cast<const f4*>(ZR + trow * LP + pb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          vv[i] = v4[i];
+          zz[i] = z4[i];
+        }
+      }
+      f4 y;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        y[i] = (fmaf(ye[i], ecum_t, yi[i]) + Dh * vv[i]) * silu_fast(zz[i]);
+        if (R > 1) y[i] *= F[Lay::MO + rr * kPPad + pb + i];
+      }
+      if constexpr (R > 1) {
+        // MIMO rank sum over the R consecutive lanes of one token (within a 16-lane row)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float t = y[i];
+#pragma unroll
+          for (int o = 1; o < R; o <<= 1) t += __shfl_xor(t, o, 16);
+          y[i] = t;
+        }
+      }
+      if (rr == 0) {
+        if constexpr (FULL) {
+          // rows of tokens >= L fall outside the buffer extent: the store is dropped
+          bstore_quad<T>(y, rs_o, (t0 + tq) * out_t + o_out + pb * ES);
+        } else {
+          if (tq < width) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if (pb + i < P) out_row[(t0 + tq) * out_t + pb + i] = from_f<T>(y[i]);
             }
           }
         }
       }
     }
 
-    // state carry: S^T = exp(cum_last) S^T + K^T Vs (the products were issued above)
+    // state carry: S^T = exp(cum_last) S^T + K~^T V (the products were issued above)
     const float ecl = SC[SB_::ECL];
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) {
