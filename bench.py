@@ -205,6 +205,42 @@ def bench_decode(batch, steps, log, rank=1, prefix=2048):
                                  kernel=f"m3::step_kernel<__bf16, {rank}>"))
 
 
+def bench_prefill_config(name, d_model, depth, rank, causal, shape, seed, log, iters=5):
+    """Forward throughput of a BASELINE config under bf16 autocast (and one layer's scan call)."""
+    from mamba3_amd import Mamba3, ops
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(seed)
+    model = Mamba3(d_model, d_state=128, depth=depth, mimo_rank=rank, causal=causal).eval()
+    x = torch.randn(*shape)
+    model, x = model.to(dev), x.to(dev)
+    batch, length = shape[0], shape[1]
+    mixer = model.layers[0].mixer
+    out = {}
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        model(x)
+        t = _events_time(lambda: model(x), iters) / iters
+        out["forward_tok_s"] = round(batch * length / t, 1)
+        out["ms_per_forward"] = round(t * 1e3, 3)
+        proj = mixer.in_proj(model.layers[0].norm(x))
+        call = ops.ScanCall(proj, mixer, chunk_size=mixer.inference_chunk_size)
+        call.launch()
+        ts = _events_time(call.launch, iters) / iters
+    c_ref = 256 if rank == 1 else 32
+    flops = prefill_flops(batch, length, mixer.nheads, 128, mixer.headdim, rank, c_ref)
+    nbytes = prefill_bytes(batch, length, d_model, mixer.in_proj.weight.shape[0])
+    out["scan_call"] = dict(
+        us=round(ts * 1e6, 1), tok_s=round(batch * length / ts, 1),
+        hbm_frac=round(nbytes / ts / 1e12 / (HBM_PEAK_GBS / 1e3), 4),
+        mfma_frac_at_cref=round(flops / ts / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        directions=1 if causal else 2)
+    log(f"{name}: forward {t * 1e3:.2f} ms ({out['forward_tok_s']:.4e} tok/s); one layer's "
+        f"scan call {ts * 1e6:.1f} us")
+    del model, x, proj, call
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_cpu(log, batch=8, length=8192):
     """The CPU oracle (portable-path restatement) on the prefill scan, ``x[batch, length]``."""
     from oracle import portable as op
@@ -262,6 +298,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-tokens", type=int, default=8192)
+    ap.add_argument("--extra", action="store_true",
+                    help="also measure BASELINE configs 3, 5 and config 4 at B=1/64 and R=4")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates PMC byte counters)")
     args = ap.parse_args()
@@ -279,6 +317,18 @@ def main() -> None:
     decode = None
     if not args.no_decode:
         decode = bench_decode(args.decode_batch, args.decode_steps, log)
+    extra = None
+    if args.extra:
+        extra = {
+            "config3_mimo_prefill": bench_prefill_config(
+                "config 3", 1024, 4, 4, True, (8, 4096, 1024), 2, log),
+            "config5_bidir_16x2048": bench_prefill_config(
+                "config 5", 768, 12, 1, False, (16, 2048, 768), 4, log),
+            "config5_bidir_1x65536": bench_prefill_config(
+                "config 5 long", 768, 12, 1, False, (1, 65536, 768), 4, log, iters=2),
+            "config4_decode": [bench_decode(b, args.decode_steps, log, rank=r)
+                               for b, r in ((1, 1), (64, 1), (256, 4), (64, 4), (1, 4))],
+        }
     cpu = None if args.no_cpu else bench_cpu(log, args.cpu_batch, args.cpu_tokens)
     value = pre["tokens"] / pre["per_launch"]
     line = {
@@ -304,6 +354,8 @@ def main() -> None:
         "decode": decode,
         "cpu_baseline": cpu,
     }
+    if extra is not None:
+        line["extra_configs"] = extra
     print(json.dumps(line), flush=True)
 
 

@@ -267,14 +267,361 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const m3_step_args a
   }
 }
 
+// ------------------------------------------------------------------ model shape (N 128, P 64)
+
+// Sum over the 32 lanes of an aligned half-wave; every lane receives it. DPP rotations inside
+// each 16-lane row, then the other row of the pair by a lane swizzle (xor 16).
+__device__ __forceinline__ float allreduce32(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128,
+                                                             0xf, 0xf, false));  // row_ror:8
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x124,
+                                                             0xf, 0xf, false));  // row_ror:4
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x122,
+                                                             0xf, 0xf, false));  // row_ror:2
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x121,
+                                                             0xf, 0xf, false));  // row_ror:1
+  x += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401f));
+  return x;
+}
+
+// The value of lane (lane xor 16) (same 32-lane half-wave).
+__device__ __forceinline__ float swap16(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401f));
+}
+
+// Four consecutive activation elements (one 8-byte load for 16-bit types, 16 bytes for FP32).
+template <typename T>
+__device__ __forceinline__ f4 ld4(const void* base, int64_t i) {
+  f4 r;
+  if constexpr (sizeof(T) == 4) {
+    r = *reinterpret_cast<const f4*>(static_cast<const float*>(base) + i);
+  } else {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    const t4 v = *reinterpret_cast<const t4*>(static_cast<const T*>(base) + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = to_f(v[j]);
+  }
+  return r;
+}
+
+// Four consecutive elements of a tensor of any supported dtype (parameters: FP32 or 16-bit).
+__device__ __forceinline__ f4 ld4x(const m3_tensor& t, int64_t i) {
+  if (t.dtype == M3_F32) return ld4<float>(t.ptr, i);
+  if (t.dtype == M3_BF16) return ld4<__bf16>(t.ptr, i);
+  return ld4<_Float16>(t.ptr, i);
+}
+
+template <typename T>
+__device__ __forceinline__ void st4(void* base, int64_t i, const float (&x)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    f4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = x[j];
+    *reinterpret_cast<f4*>(static_cast<float*>(base) + i) = v;
+  } else {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    t4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = from_f<T>(x[j]);
+    *reinterpret_cast<t4*>(static_cast<T*>(base) + i) = v;
+  }
+}
+
+// The model's decode shape (N = 128, P = 64, 32 angles), one 256-thread workgroup per
+// (batch, head), with no LDS round trip before the state update: thread (row group rg = tid / 32,
+// column group c = tid % 32) owns columns 4c .. 4c+3 of the state rows rg + 8k, k < 8. Its state
+// loads are issued first; while they are in flight it computes, for every rank, the normed,
+// biased, rotated q / k of its columns (the RMSNorm sums and the MIMO rotation partner by
+// cross-lane exchange within its 32-lane half-wave) and the phases of the angles those columns
+// use. Per-row rank values and gates go through LDS behind one barrier. The readout sums over a
+// half-wave use DPP; lane c = k finishes row rg + 8k. The small cache outputs are written after a
+// final barrier, when every thread has consumed the cache inputs they may alias.
+template <typename T, int R>
+__global__ __launch_bounds__(kStepThreads) void step128_kernel(const m3_step_args a) {
+  constexpr int N = 128, P = 64, S = 32, RPT = 8;
+  const int H = a.heads;
+  const int bh = blockIdx.x;
+  const int b = bh / H, h = bh - b * H;
+  const int g = h / (H / a.groups);
+  const int tid = threadIdx.x, c = tid & 31, rg = tid >> 5, n0 = 4 * c;
+  const bool norm = a.q_norm_w.ptr != nullptr;
+  const bool bias = a.q_bias.ptr != nullptr;
+  const bool rotate = a.phase_mode != M3_PHASE_NONE;
+  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
+  const bool mimo = a.mimo_rotation != 0;
+
+  __shared__ float s_vr[R][P], s_pvr[R][P], s_zr[R][P], s_mo[R][P];
+
+  // (1) this thread's state rows
+  const float* sin_ = static_cast<const float*>(a.state_in.ptr) + b * a.state_in.stride[0] +
+                      h * a.state_in.stride[1] + n0;
+  float* sout = static_cast<float*>(a.state_out.ptr) + b * a.state_out.stride[0] +
+                h * a.state_out.stride[1] + n0;
+  const int64_t sp_in = a.state_in.stride[2], sp_out = a.state_out.stride[2];
+  f4 st[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    st[k] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(sin_ + (rg + 8 * k) * sp_in));
+  }
+
+  // (2) per-row rank values and gates (thread p < P), into LDS
+  if (tid < P) {
+    const int p = tid;
+    const float v = ld_act<T>(a.value, b * a.value.stride[0] + h * a.value.stride[1] + p);
+    const float z = ld_act<T>(a.gate, b * a.gate.stride[0] + h * a.gate.stride[1] + p);
+    const float pv = ld_act<T>(a.prev_value,
+                               b * a.prev_value.stride[0] + h * a.prev_value.stride[1] + p);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (R > 1) {
+        const float mx = rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
+                                    h * a.mimo_x.stride[0] + r * a.mimo_x.stride[1] + p));
+        const float mz = rnd<T>(ldx(a.mimo_z.ptr, a.mimo_z.dtype,
+                                    h * a.mimo_z.stride[0] + r * a.mimo_z.stride[1] + p));
+        s_vr[r][p] = mul_r<T>(v, mx);
+        s_pvr[r][p] = mul_r<T>(pv, mx);
+        s_zr[r][p] = mul_r<T>(z, mz);
+        s_mo[r][p] = ldx(a.mimo_out.ptr, a.mimo_out.dtype,
+                         h * a.mimo_out.stride[0] + r * a.mimo_out.stride[1] + p);
+      } else {
+        s_vr[r][p] = v;
+        s_pvr[r][p] = pv;
+        s_zr[r][p] = z;
+        s_mo[r][p] = 1.f;
+      }
+    }
+    // value_out may alias prev_value: only this thread touches index p
+    if (a.value_out.ptr != nullptr) {
+      static_cast<T*>(a.value_out.ptr)[b * a.value_out.stride[0] + h * a.value_out.stride[1] +
+                                       p] = from_f<T>(v);
+    }
+  }
+
+  // (3) per-(b, h) scalars
+  float dt, adt;
+  dt_adt(a.raw_dt, ldx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + h * a.dt.stride[1]),
+         ldx(a.a.ptr, a.a.dtype, b * a.a.stride[0] + h * a.a.stride[1]),
+         a.raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]) : 0.f, dt, adt);
+  const float trap = sigmoidf(ldx(a.trap.ptr, a.trap.dtype,
+                                  b * a.trap.stride[0] + h * a.trap.stride[1]));
+  const float alpha = expf(adt);
+  const float beta = (1.f - trap) * dt * alpha;
+  const float gamma = trap * dt;
+  const float Dh = ldx(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
+
+  // (4) phases of the angles this thread's columns use: SISO pairs (2j, 2j+1) -> angles 2c, 2c+1
+  // (c < 16); MIMO pairs (j, j + 2S) -> angles n0 .. n0+3 for the first (c < 8) and third
+  // (16 <= c < 24) quarters
+  int j0 = -1, nj = 0;
+  if (rotate) {
+    if (!mimo) {
+      if (c < S / 2) { j0 = 2 * c; nj = 2; }
+    } else if (c < S / 4) {
+      j0 = n0; nj = 4;
+    } else if (c >= S / 2 && c < 3 * S / 4) {
+      j0 = n0 - 2 * S; nj = 4;
+    }
+  }
+  float phn[4] = {0.f, 0.f, 0.f, 0.f}, cs[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
+  const float* ph_in = static_cast<const float*>(a.phase_in.ptr) + b * a.phase_in.stride[0] +
+                       h * a.phase_in.stride[1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i < nj) {
+      const int j = j0 + i;
+      const float old = ph_in[j * a.phase_in.stride[2]];
+      float ph = old;
+      if (angles) {
+        const float th = ldx(a.angles.ptr, a.angles.dtype,
+                             b * a.angles.stride[0] + j * a.angles.stride[1]);
+        ph = fmodf(__fadd_rn(old, phase_inc(th, dt)), kTwoPi);
+      }
+      phn[i] = ph;
+      cs[i] = rnd<T>(cosf(ph));
+      sn[i] = rnd<T>(sinf(ph));
+    }
+  }
+
+  // (5) q / k of this thread's columns, every rank: RMSNorm, weight, bias, rotation
+  f4 wq, wk;
+  if (norm) {
+    wq = ld4x(a.q_norm_w, n0);  // weights may be FP32 or the activation type
+    wk = ld4x(a.k_norm_w, n0);
+  }
+  float qr[R][4], kr[R][4], pk[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const f4 qx = ld4<T>(a.q.ptr, b * a.q.stride[0] + g * a.q.stride[1] + r * a.q.stride[2] + n0);
+    const f4 kx = ld4<T>(a.k.ptr, b * a.k.stride[0] + g * a.k.stride[1] + r * a.k.stride[2] + n0);
+    const f4 px = ld4<T>(a.prev_k.ptr, b * a.prev_k.stride[0] + h * a.prev_k.stride[1] +
+                                           r * a.prev_k.stride[2] + n0);
+    float q[4], k[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      q[j] = qx[j];
+      k[j] = kx[j];
+      pk[r][j] = px[j];
+    }
+    if (norm) {
+      float sq = 0.f, sk = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sq += q[j] * q[j];
+        sk += k[j] * k[j];
+      }
+      sq = allreduce32(sq);
+      sk = allreduce32(sk);
+      const float rq = 1.f / sqrtf(sq / static_cast<float>(N) + a.norm_eps);
+      const float rk = 1.f / sqrtf(sk / static_cast<float>(N) + a.norm_eps);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        q[j] = rnd<T>(q[j] * rq * rnd<T>(wq[j]));
+        k[j] = rnd<T>(k[j] * rk * rnd<T>(wk[j]));
+      }
+    }
+    if (bias) {
+      const f4 bq = ld4x(a.q_bias, h * a.q_bias.stride[0] + r * a.q_bias.stride[1] + n0);
+      const f4 bk = ld4x(a.k_bias, h * a.k_bias.stride[0] + r * a.k_bias.stride[1] + n0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        q[j] = add_r<T>(q[j], rnd<T>(bq[j]));
+        k[j] = add_r<T>(k[j], rnd<T>(bk[j]));
+      }
+    }
+    if (rotate && !mimo) {
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        const float lq = q[2 * pp], hq = q[2 * pp + 1], lk = k[2 * pp], hk = k[2 * pp + 1];
+        if (nj > 0) {
+          q[2 * pp] = sub_r<T>(mul_r<T>(lq, cs[pp]), mul_r<T>(hq, sn[pp]));
+          q[2 * pp + 1] = add_r<T>(mul_r<T>(lq, sn[pp]), mul_r<T>(hq, cs[pp]));
+          k[2 * pp] = sub_r<T>(mul_r<T>(lk, cs[pp]), mul_r<T>(hk, sn[pp]));
+          k[2 * pp + 1] = add_r<T>(mul_r<T>(lk, sn[pp]), mul_r<T>(hk, cs[pp]));
+        }
+      }
+    } else if (rotate) {
+      // partner columns n +- 2S = +-64 live in lane c xor 16
+      float oq[4], ok[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        oq[j] = swap16(q[j]);
+        ok[j] = swap16(k[j]);
+      }
+      if (nj > 0) {
+        const bool first = c < S / 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (first) {
+            q[j] = sub_r<T>(mul_r<T>(q[j], cs[j]), mul_r<T>(oq[j], sn[j]));
+            k[j] = sub_r<T>(mul_r<T>(k[j], cs[j]), mul_r<T>(ok[j], sn[j]));
+          } else {
+            q[j] = add_r<T>(mul_r<T>(oq[j], sn[j]), mul_r<T>(q[j], cs[j]));
+            k[j] = add_r<T>(mul_r<T>(ok[j], sn[j]), mul_r<T>(k[j], cs[j]));
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qr[r][j] = q[j];
+      kr[r][j] = k[j];
+    }
+  }
+  __syncthreads();  // the per-row LDS vectors
+
+  // (6) state update, readout and epilogue of rows rg + 8k
+  float yrow = 0.f;  // lane c = k keeps row rg + 8k's output
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int p = rg + 8 * k;
+    float po[4] = {0.f, 0.f, 0.f, 0.f}, co[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float pv = s_pvr[r][p], cv = s_vr[r][p];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        po[j] += pv * pk[r][j];
+        co[j] += cv * kr[r][j];
+      }
+    }
+    f4 ns;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ns[j] = alpha * st[k][j] + beta * po[j] + gamma * co[j];
+    __builtin_nontemporal_store(ns, reinterpret_cast<f4*>(sout + p * sp_out));
+    float y = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) part += rnd<T>(ns[j]) * qr[r][j];
+      part = allreduce32(part);
+      const float t = (part + Dh * s_vr[r][p]) * siluf(s_zr[r][p]);
+      y = R > 1 ? y + t * s_mo[r][p] : t;
+    }
+    if (c == k) yrow = y;
+  }
+  if (c < RPT) {
+    const int p = rg + 8 * c;
+    static_cast<T*>(a.out.ptr)[b * a.out.stride[0] + h * a.out.stride[1] + p] = from_f<T>(yrow);
+  }
+
+  // (7) the small cache outputs, after every thread has consumed the inputs they may alias
+  __syncthreads();
+  if (rg == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      st4<T>(a.k_out.ptr, b * a.k_out.stride[0] + h * a.k_out.stride[1] + r * a.k_out.stride[2] +
+                              n0, kr[r]);
+    }
+    float* ph_out = static_cast<float*>(a.phase_out.ptr) + b * a.phase_out.stride[0] +
+                    h * a.phase_out.stride[1];
+    if (rotate) {
+      // each angle has one writer: SISO c < 16, MIMO the first quarter (c < 8)
+      const bool writer = !mimo || c < S / 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (writer && i < nj) ph_out[(j0 + i) * a.phase_out.stride[2]] = phn[i];
+      }
+    } else if (c < S) {
+      ph_out[c * a.phase_out.stride[2]] = ph_in[c * a.phase_in.stride[2]];
+    }
+  }
+}
+
 static size_t step_lds_bytes(int R, int N, int P, int S) {
   return sizeof(float) * (static_cast<size_t>(5) * R * N + 5 * R * P + P + 3 * S + 2 * R);
+}
+
+// The model's shape with 4-element column vectors aligned for step128_kernel.
+static bool step128_ok(const m3_step_args& a) {
+  if (a.d_state != 128 || a.head_dim != 64 || a.num_angles != 32) return false;
+  for (const m3_tensor* t : {&a.q, &a.k, &a.prev_k, &a.k_out, &a.q_bias, &a.k_bias,
+                             &a.q_norm_w, &a.k_norm_w}) {
+    if (t->ptr == nullptr) continue;
+    const int es = t->dtype == M3_F32 ? 4 : 2;
+    if (reinterpret_cast<uintptr_t>(t->ptr) % (4 * es) != 0) return false;
+    const int dims = (t == &a.q_norm_w || t == &a.k_norm_w) ? 1 : (t == &a.q_bias ||
+                                                                    t == &a.k_bias) ? 3 : 4;
+    for (int i = 0; i < dims - 1; ++i) {
+      if (t->stride[i] % 4 != 0) return false;
+    }
+  }
+  return true;
 }
 
 template <typename T>
 static int launch_step(const m3_step_args& a, hipStream_t stream) {
   const size_t lds = step_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles);
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kStepThreads);
+  // ranks 1 and 2 (R = 4 and 8 keep their per-rank q / k in LDS: fewer registers per thread)
+  if (a.rank <= 2 && step128_ok(a)) {
+    if (a.rank == 1) {
+      hipLaunchKernelGGL((step128_kernel<T, 1>), grid, block, 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((step128_kernel<T, 2>), grid, block, 0, stream, a);
+    }
+    return check_launch("m3_step");
+  }
   switch (a.rank) {
     case 1: hipLaunchKernelGGL((step_kernel<T, 1>), grid, block, lds, stream, a); break;
     case 2: hipLaunchKernelGGL((step_kernel<T, 2>), grid, block, lds, stream, a); break;

@@ -145,7 +145,8 @@ def _chain_512(dtype, rank, *, fused: bool):
     ref_cache = zero_cache
     dev_cache = tuple(t.to(DEV) for t in zero_cache)
     g = torch.Generator().manual_seed(123)
-    worst_y = 0.0
+    worst_y = worst_rel = 0.0
+    max_y = 0.0
     for _ in range(512):
         step = dict(base)
         for name in ("q", "k", "value", "gate", "angle_rate"):
@@ -175,12 +176,17 @@ def _chain_512(dtype, rank, *, fused: bool):
             with torch.inference_mode():
                 y, dev_cache = ops.mamba3_step(**step_d)
         ref_cache = tuple(t.clone() for t in ref_cache)
-        worst_y = max(worst_y, (y.float().cpu() - y_ref.float()).abs().max().item())
+        dy = (y.float().cpu() - y_ref.float()).abs()
+        worst_y = max(worst_y, dy.max().item())
+        # relative to the output's magnitude (floor 1): a 16-bit output rounds to 2^-8 relative
+        worst_rel = max(worst_rel, (dy / y_ref.float().abs().clamp_min(1.0)).max().item())
+        max_y = max(max_y, y_ref.float().abs().max().item())
     err = (dev_cache[1].cpu() - ref_cache[1]).abs().max().item()
     scale = ref_cache[1].abs().max().item()
     print(f"512 steps {dtype} R={rank} fused={fused}: state max abs {err:.3e}, "
-          f"rel {err / scale:.3e}, |S|max {scale:.2f}, outputs max abs {worst_y:.3e}", flush=True)
-    return err, scale, worst_y
+          f"rel {err / scale:.3e}, |S|max {scale:.2f}, outputs max abs {worst_y:.3e} "
+          f"(|y|max {max_y:.1f}, rel {worst_rel:.3e})", flush=True)
+    return err, scale, worst_y, worst_rel
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -189,11 +195,16 @@ def test_state_after_512_steps(dtype, rank):
     """the FP32 state after 512 decode steps within 1e-4 (max abs).
 
     Teacher-forced: both sides get identical rotated q/k for every step, so the check
-    isolates the recurrence (state update, readout, gate) over 512 steps.
+    isolates the recurrence (state update, readout, gate) over 512 steps. 16-bit outputs are
+    checked relative to their magnitude (2e-2): the FP32 readout sums in another order than
+    the CPU's, so an output can round to the neighbouring 16-bit value.
     """
-    err, _, worst_y = _chain_512(dtype, rank, fused=False)
+    err, _, worst_y, worst_rel = _chain_512(dtype, rank, fused=False)
     assert err <= 1e-4
-    assert worst_y <= (1e-4 if dtype == torch.float32 else 2e-2 * 4)
+    if dtype == torch.float32:
+        assert worst_y <= 1e-4
+    else:
+        assert worst_rel <= 2e-2
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -207,8 +218,9 @@ def test_fused_state_after_512_steps(dtype, rank):
     one bf16 ulp and moves the state by about gamma * v * ulp(k) ~ 5e-4. The 16-bit bar is
     therefore relative: max |dS| / max |S| <= 1e-3.
     """
-    err, scale, _ = _chain_512(dtype, rank, fused=True)
+    err, scale, _, worst_rel = _chain_512(dtype, rank, fused=True)
     if dtype == torch.float32:
         assert err <= 1e-4
     else:
         assert err / scale <= 1e-3
+        assert worst_rel <= 2e-2
