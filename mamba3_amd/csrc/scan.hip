@@ -39,6 +39,7 @@
 #include "m3_math.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace m3 {
 
@@ -590,26 +591,31 @@ __device__ __forceinline__ int cs_col(int col, int tt) {
 // Bounded phase (model.py:215-256) of tokens TPL pg .. TPL pg + TPL-1 of the sub-chunk at t0 for
 // angle ps: fmod-reduced increments summed within 64-token blocks, an fmod-reduced carry between
 // blocks, the running block sum and carry in pbase / poff; cos / sin into the table of angle ps.
-template <int PG, int TPL, int CST, bool SWZ>
+template <int PG, int TPL, int CST, bool SWZ, bool EXACT>
 __device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, float* poff,
                                             const float* dtv, int t0, int L, int pg, int lane,
                                             bool angles, const float (&pa)[TPL], float* fph) {
   float ph[TPL];
   if (angles) {
     float x[TPL];
-    bool big = false;
+    float mx = 0.f;  // largest |increment| of the lane (NaN and inf reduce like any x below)
 #pragma unroll
     for (int i = 0; i < TPL; ++i) {
       x[i] = __fmul_rn(pa[i], dtv[TPL * pg + i]);  // dt is 0 past the sub-chunk's last token
-      big = big || !(fabsf(x[i]) < 1048576.0f);
+      mx = fmaxf(mx, fabsf(x[i]));
     }
+    // fmodf(x, 2 pi) is x itself for |x| < 2 pi (dt < 2, the usual case); the reductions are
+    // chosen per wave, so no lane branches on its own elements
     float inc[TPL];
-    if (big) {
+    if (__builtin_amdgcn_ballot_w64(!(mx < M3_TWO_PI_F)) == 0) {
 #pragma unroll
-      for (int i = 0; i < TPL; ++i) inc[i] = m3_fmod_2pi(x[i]);
-    } else {
+      for (int i = 0; i < TPL; ++i) inc[i] = x[i];
+    } else if (__builtin_amdgcn_ballot_w64(!(mx < 1048576.0f)) == 0) {
 #pragma unroll
       for (int i = 0; i < TPL; ++i) inc[i] = m3_fmod_2pi_small(x[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) inc[i] = m3_fmod_2pi(x[i]);
     }
     float cpre[TPL];
     float run = 0.f;
@@ -628,11 +634,16 @@ __device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, fl
       off = m3_fmod_2pi_small(__fadd_rn(off, base));
       base = 0.f;
     }
+    // the final phase (token L - 1), when this sub-chunk holds it (wave-uniform test)
+    const bool last = fph != nullptr && t0 <= L - 1 && L - 1 - t0 < PG * TPL;
 #pragma unroll
     for (int i = 0; i < TPL; ++i) {
-      // |base|, |excl + cpre| <= 64 * 2 pi and |off| < 2 pi: within the reduction's range
-      ph[i] = m3_fmod_2pi_small(__fadd_rn(__fadd_rn(base, __fadd_rn(excl, cpre[i])), off));
-      if (t0 + TPL * pg + i == L - 1 && fph != nullptr) *fph = ph[i];
+      // |base|, |excl + cpre| <= 64 * 2 pi and |off| < 2 pi: within the reduction's range.
+      // !EXACT (16-bit activations): sin / cos reduce the phase themselves (below 66 turns, the
+      // hardware's range), a difference far below the 16-bit rounding of the rotated values.
+      const float raw = __fadd_rn(__fadd_rn(base, __fadd_rn(excl, cpre[i])), off);
+      ph[i] = EXACT ? m3_fmod_2pi_small(raw) : raw;
+      if (last && t0 + TPL * pg + i == L - 1) *fph = EXACT ? ph[i] : m3_fmod_2pi_small(raw);
     }
     if (pg == PG - 1) {
       *pbase = __fadd_rn(base, incl);
@@ -859,12 +870,14 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // waves 4-7 columns 64-127)
   const int rp = SPLIT ? (tid & 255) >> 3 : tid >> 4;
   const int n0 = SPLIT ? 64 * (tid >> 8) + 8 * (tid & 7) : 8 * (tid & 15);
-  const bool qk_on = rp < ROWS / 2 && n0 < N;
+  // (SPLIT: every lane has both roles, 512 threads covering 64 rows x 128 columns and 64 tokens x
+  // 64 columns)
+  const bool qk_on = SPLIT || (rp < ROWS / 2 && n0 < N);
   const int qk_n = min(8, N - n0);
   // v / z: token pair vp (tokens 2vp, 2vp+1), columns p0 .. p0+3
   constexpr int P4 = kPPad / 4;
   const int vp = tid / P4, p0 = 4 * (tid % P4);
-  const bool vz_on = 2 * vp < TOK && p0 < P;
+  const bool vz_on = SPLIT || (2 * vp < TOK && p0 < P);
   const int vz_n = min(4, P - p0);
   // phase: angle ps, token group pg (tokens TPL pg .. TPL pg + TPL-1)
   const int pg = tid % PG, ps = tid / PG;
@@ -924,6 +937,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // ---- the state: S^T tiles (ni, pj), tile u = w + 8k; lane holds n = 16 ni + 4 lg + i,
   // p = 16 pj + l16.
   constexpr int n_tiles = kNT * kPT;
+  static_assert(n_tiles <= kWaves * kTiles, "state tiles exceed the waves' share");
+  constexpr bool all_tiles = n_tiles == kWaves * kTiles;  // every (wave, k) holds a tile
   f4 st[kTiles];
 #pragma unroll
   for (int k = 0; k < kTiles; ++k) {
@@ -1057,7 +1072,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   if (ph_on && nsub > 0) {
     float pa[TPL];
     angles_of(pa);
-    phase_stage<PG, TPL, CST, SPLIT>(csb(0), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
+    phase_stage<PG, TPL, CST, SPLIT, !SPLIT>(csb(0), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
                                      scb(0) + SB_::DTV, 0, L, pg, lane, angles, pa, fph);
   }
   __syncthreads();
@@ -1073,8 +1088,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       if (2 * tid < side_n) *reinterpret_cast<float2*>(scb(c + 1) + 2 * tid) = side;
       if (4 * tid < TOK * S) *reinterpret_cast<float4*>(ANG + 4 * tid) = ang;
     }
-    // q / k rows -> Qs, Ks (row-major), KT (transposed, swizzled); rows 2rp, 2rp+1
-    if (qk_on) {
+    // q / k rows -> Qs, Ks (row-major), KT (transposed, swizzled); rows 2rp, 2rp+1. SPLIT: one
+    // copy of the code per column half, rotated (waves 0-3) or not, so no values merge between
+    // the two.
+    auto stage_qk = [&](auto rot_tag) {
+      constexpr bool ROT = decltype(rot_tag)::value;
       // (q, k) RMSNorm factors of rows 2rp, 2rp+1
       float fq[2] = {1.f, 1.f}, fk[2] = {1.f, 1.f};
       if (norm) {
@@ -1096,7 +1114,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
         if constexpr (SPLIT) {
           // pairs (2j, 2j+1), j = n0/2 .. n0/2+3: the rotated columns are waves 0-3's
-          if (w < 4) {
+          if constexpr (ROT) {
             const float* tr = CSt + tt * CST + 2 * cs_col<true>(n0 >> 1, tt);
             const f4 c01 = *reinterpret_cast<const f4*>(tr);      // c0 s0 c1 s1
             const f4 c23 = *reinterpret_cast<const f4*>(tr + 4);  // c2 s2 c3 s3
@@ -1155,6 +1173,15 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> 3), kt[0][i] * e0, kt[1][i] * e1);
         }
       }
+    };
+    if constexpr (SPLIT) {
+      if (w < 4) {
+        stage_qk(std::true_type{});
+      } else {
+        stage_qk(std::false_type{});
+      }
+    } else if (qk_on) {
+      stage_qk(std::false_type{});
     }
     // value / gate of tokens 2vp, 2vp+1, columns p0 .. p0+3: rank values v mx_r -> VT
     // (transposed, swizzled) and VR (row-major), rank gates z mz_r -> ZR (row-major)
@@ -1219,9 +1246,19 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) {
       const int u = w + kWaves * k;
-      if (u < n_tiles) {
+      if (all_tiles || u < n_tiles) {
         const int ni = u / kPT, pj = u - ni * kPT;
         st_quad<T>(Sb + (16 * pj + l16) * LQ + 16 * ni + 4 * lg, st[k]);
+      }
+    }
+    // the carry's decay of the state, exp(cum_last) S^T: the carry products below accumulate
+    // onto it
+    {
+      const float ecl = SC[SB_::ECL];
+#pragma unroll
+      for (int k = 0; k < kTiles; ++k) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[k][i] *= ecl;
       }
     }
     __syncthreads();
@@ -1268,13 +1305,12 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
       }
     }
-    // K~^T V products of the state carry, issued early: they depend only on staged tiles
-    f4 cacc[kTiles];
+    // K~^T V products of the state carry, issued early (they depend only on staged tiles),
+    // accumulated onto the decayed state
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) {
-      cacc[k] = zero4();
       const int u = w + kWaves * k;
-      if (u >= n_tiles) continue;
+      if (!all_tiles && u >= n_tiles) continue;
       const int ni = u / kPT, pj = u - ni * kPT;
       const int nrow = 16 * ni + l16, prow = 16 * pj + l16;
       if constexpr (!F32) {
@@ -1284,13 +1320,13 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
               KT + nrow * LR + swz<ROWS>(kk + 8 * lg, nrow >> 3));
           const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
               VT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> 2));
-          cacc[k] = M::mma(av, bv, cacc[k]);
+          st[k] = M::mma(av, bv, st[k]);
         }
       } else {
 #pragma unroll
         for (int kk = 0; kk < ROWS; kk += 4) {
-          cacc[k] = M::mma(KT[nrow * LR + swz<ROWS>(kk + lg, nrow >> 3)],
-                           VT[prow * LR + swz<ROWS>(kk + lg, prow >> 2)], cacc[k]);
+          st[k] = M::mma(KT[nrow * LR + swz<ROWS>(kk + lg, nrow >> 3)],
+                         VT[prow * LR + swz<ROWS>(kk + lg, prow >> 2)], st[k]);
         }
       }
     }
@@ -1298,13 +1334,17 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     if (ph_on && c + 1 < nsub) {
       float pa[TPL];
       angles_of(pa);
-      phase_stage<PG, TPL, CST, SPLIT>(csb(c + 1), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
+      phase_stage<PG, TPL, CST, SPLIT, !SPLIT>(csb(c + 1), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
                                        scb(c + 1) + SB_::DTV, t0 + TOK, L, pg, lane, angles, pa,
                                        fph);
     }
     // decayed scores W[t, s] = Sc[t, s] d[t, s] in FP32
     const float cum_t = SC[SB_::CUM + tq];
     const float gam_t = SC[SB_::GAM + tq];
+    // the causal masks below compare a copy of tq the compiler cannot see through, so they are
+    // evaluated here as vector compares, not hoisted out of the loop into scalar mask registers
+    int tq_m = tq;
+    __asm__ volatile("" : "+v"(tq_m));
     f4 wsc[RT];
 #pragma unroll
     for (int sj = 0; sj < RT; ++sj) {
@@ -1319,11 +1359,29 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           wsc[sj][i] = acc[sj][i] * (at * SC[SB_::BSC + ts]);
         }
       } else {
+        // diagonal tile: every term is read and computed, then selected (no per-lane branches)
+        float cs[4], sc[4];
+        if constexpr (R == 1) {
+          const f4 c4 = *reinterpret_cast<const f4*>(SC + SB_::CUM + 16 * sj + 4 * lg);
+          const f4 s4 = *reinterpret_cast<const f4*>(SC + SB_::SCL + 16 * sj + 4 * lg);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            cs[i] = c4[i];
+            sc[i] = s4[i];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int ts = (16 * sj + 4 * lg + i) / R;
+            cs[i] = SC[SB_::CUM + ts];
+            sc[i] = SC[SB_::SCL + ts];
+          }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int ts = (16 * sj + 4 * lg + i) / R;
-          const float d = tq > ts ? SC[SB_::SCL + ts] * __expf(cum_t - SC[SB_::CUM + ts])
-                                  : (tq == ts ? gam_t : 0.f);
+          const float lower = sc[i] * __expf(cum_t - cs[i]);
+          const float d = tq_m > ts ? lower : (tq_m == ts ? gam_t : 0.f);
           wsc[sj][i] = acc[sj][i] * d;
         }
       }
@@ -1417,7 +1475,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       if (rr == 0) {
         if constexpr (FULL) {
           // rows of tokens >= L fall outside the buffer extent: the store is dropped
-          bstore_quad<T>(y, rs_o, (t0 + tq) * out_t + o_out + pb * ES);
+          bstore_quad<T>(y, rs_o,
+                         (tq * out_t + o_out + pb * ES) +
+                             __builtin_amdgcn_readfirstlane(t0 * out_t));
         } else {
           if (tq < width) {
 #pragma unroll
@@ -1429,13 +1489,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       }
     }
 
-    // state carry: S^T = exp(cum_last) S^T + K~^T V (the products were issued above)
-    const float ecl = SC[SB_::ECL];
-#pragma unroll
-    for (int k = 0; k < kTiles; ++k) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) st[k][i] = fmaf(ecl, st[k][i], cacc[k][i]);
-    }
+    // (the state carry S^T = exp(cum_last) S^T + K~^T V was accumulated above)
     __syncthreads();
   }
 
