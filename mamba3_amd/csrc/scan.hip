@@ -305,8 +305,8 @@ __device__ __forceinline__ float wave_incl_scan(float x, int lane) {
   return x;
 }
 
-// Transposed operand tiles ([n or p][row]) XOR-swizzle their 8-row groups by a per-row-of-
-// the-tile key so that the column-wise stores of the prologue spread over the LDS banks;
+// Transposed operand tiles ([n or p][row]) XOR-swizzle their 8-row groups by a key taken from
+// the tile row (n or p) so that the column-wise stores of the staging spread over the LDS banks;
 // every reader applies the same swizzle. Groups of 8 (16-bit: 16 bytes) stay contiguous.
 template <int ROWS>
 __device__ __forceinline__ int swz(int row, int key) {
@@ -495,6 +495,12 @@ struct Feed {
   __device__ __forceinline__ void words(int t0, int nw, bool qk_on, bool vz_on,
                                         uint32_t (&rq)[2][W8], uint32_t (&rk)[2][W8],
                                         uint32_t (&rv)[2][W4], uint32_t (&rz)[2][W4]) const {
+    words_qk(t0, nw, qk_on, rq, rk);
+    words_vz(t0, nw, vz_on, rv, rz);
+  }
+
+  __device__ __forceinline__ void words_qk(int t0, int nw, bool qk_on, uint32_t (&rq)[2][W8],
+                                           uint32_t (&rk)[2][W8]) const {
     if constexpr (FULL) {
       // unconditional, also for lanes without a q/k or v/z role: every offset stays inside a
       // buffer or past its extent, where the load returns zero
@@ -503,11 +509,6 @@ struct Feed {
       for (int j = 0; j < 2; ++j) {
         bload_words<W8>(rq[j], rs_p, o_qk + tb + j * d_q1);
         bload_words<W8>(rk[j], rs_p, o_qk + tb + j * d_q1 + d_k);
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        bload_words<W4>(rv[j], rs_p, o_vz + tb + j * tok_b);
-        bload_words<W4>(rz[j], rs_p, o_vz + tb + j * tok_b + d_z);
       }
     } else {
       if (qk_on) {
@@ -520,6 +521,19 @@ struct Feed {
           load_words<T, 8>(rk[j], k_row + tg * k_t + r * k_r, ok ? qk_n : 0, vec_qk);
         }
       }
+    }
+  }
+
+  __device__ __forceinline__ void words_vz(int t0, int nw, bool vz_on, uint32_t (&rv)[2][W4],
+                                           uint32_t (&rz)[2][W4]) const {
+    if constexpr (FULL) {
+      const int tb = t0 * tok_b;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        bload_words<W4>(rv[j], rs_p, o_vz + tb + j * tok_b);
+        bload_words<W4>(rz[j], rs_p, o_vz + tb + j * tok_b + d_z);
+      }
+    } else {
       if (vz_on) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -828,6 +842,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   constexpr bool SPLIT = FULL && R == 1 && !F32;
   constexpr int TPL = SPLIT ? 8 : 4;   // tokens per phase lane
   constexpr int PG = TOK / TPL;        // phase lanes per angle
+  // swizzle keys of the transposed tiles, n >> KSH for KT and p >> VSH for VT. 16-bit: constant
+  // over each 16-row tile, so the carry's and the intra product's 16-byte reads of 16 rows hit
+  // 16 distinct bank groups (8- and 16-byte LDS accesses see 64 banks)
+  constexpr int KSH = F32 ? 3 : 4, VSH = F32 ? 2 : 4;
   // FULL: the model's shape (N = 128, P = 64, S = 32) in projection form with vector loads
   const int N = FULL ? kNPad : a.d_state;
   const int P = FULL ? kPPad : a.head_dim;
@@ -1042,11 +1060,22 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   const int nsub = g.nsub, scw = g.scw;
   const int side_n = scw + 2 * ROWS;  // floats of a side block
   float* ANG = F + Lay::ANG;
+  // angle tile slot (16 bytes) of 4-token group g and angle s: rows of kSMax slots, the angle
+  // XOR-keyed by the group's phase lane, so the PG lanes reading one angle and the lanes writing
+  // one group hit distinct banks (key < 16, so s ^ key < kSMax)
+  static_assert(16 % PG == 0 && 16 / PG * (PG - 1) < kSMax, "angle tile key");
+  auto ang_slot = [&](int g, int s) { return g * kSMax + (s ^ ((g / (TPL / 4)) * (16 / PG))); };
+  auto ang_store = [&](const float4& v) {
+    if (4 * tid < TOK * S) {
+      const int g = tid / S;
+      *reinterpret_cast<float4*>(ANG + 4 * ang_slot(g, tid - g * S)) = v;
+    }
+  };
   // the angle inputs of this phase lane's tokens, from the angle tile
   auto angles_of = [&](float (&pa)[TPL]) {
 #pragma unroll
     for (int q = 0; q < TPL / 4; ++q) {
-      const float4 v = *reinterpret_cast<const float4*>(ANG + (((TPL / 4) * pg + q) * S + ps) * 4);
+      const float4 v = *reinterpret_cast<const float4*>(ANG + 4 * ang_slot((TPL / 4) * pg + q, ps));
       pa[4 * q] = v.x;
       pa[4 * q + 1] = v.y;
       pa[4 * q + 2] = v.z;
@@ -1065,7 +1094,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   ang = fd.ang_in(0);
   fd.words(0, min(TOK, L), qk_on, vz_on, rq, rk, rv, rz);
   if (2 * tid < side_n) *reinterpret_cast<float2*>(scb(0) + 2 * tid) = side;
-  if (4 * tid < TOK * S) *reinterpret_cast<float4*>(ANG + 4 * tid) = ang;
+  ang_store(ang);
   side = fd.side_in(1);
   ang = fd.ang_in(1);
   __syncthreads();
@@ -1086,7 +1115,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     // ---- interval 1: stage sub-chunk c; the scalar block of c + 1 to LDS
     if (c + 1 < nsub) {
       if (2 * tid < side_n) *reinterpret_cast<float2*>(scb(c + 1) + 2 * tid) = side;
-      if (4 * tid < TOK * S) *reinterpret_cast<float4*>(ANG + 4 * tid) = ang;
+      ang_store(ang);
     }
     // q / k rows -> Qs, Ks (row-major), KT (transposed, swizzled); rows 2rp, 2rp+1. SPLIT: one
     // copy of the code per column half, rotated (waves 0-3) or not, so no values merge between
@@ -1170,7 +1199,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       for (int i = 0; i < 8; ++i) {
         const int n = n0 + i;
         if (FULL || n < N) {
-          st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> 3), kt[0][i] * e0, kt[1][i] * e1);
+          st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> KSH), kt[0][i] * e0, kt[1][i] * e1);
         }
       }
     };
@@ -1199,7 +1228,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int p = p0 + i;
-          if (FULL || p < P) st_pair<T>(VT + p * LR + swz<ROWS>(2 * vp, p >> 2), v[0][i], v[1][i]);
+          if (FULL || p < P) st_pair<T>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH), v[0][i], v[1][i]);
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -1234,7 +1263,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
             for (int r = 0; r < R; r += 2) {
               const int row = (2 * vp + j) * R + r;
-              st_pair<T>(VT + p * LR + swz<ROWS>(row, p >> 2),
+              st_pair<T>(VT + p * LR + swz<ROWS>(row, p >> VSH),
                          mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p]),
                          mul_r<T>(v[j][i], F[Lay::MX + (r + 1) * kPPad + p]));
             }
@@ -1266,12 +1295,30 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     // ---- interval 2
     // words of sub-chunk c + 1 into registers; they fly while sub-chunk c computes. FULL issues
     // every load of the loop unconditionally (reads past token L return zero), which keeps the
-    // compiler's in-order wait counts exact: no load is waited for before its use.
-    if (FULL || c + 1 < nsub) {
-      fd.words(t0 + TOK, min(TOK, L - t0 - TOK), qk_on, vz_on, rq, rk, rv, rz);
+    // compiler's in-order wait counts exact: no load is waited for before its use. FULL spreads
+    // them over the interval in three groups (q / k, value / gate, side and angle words) pinned
+    // between the compute stages, so the eight waves do not queue all their loads at once.
+    auto loads_qk = [&] {
+      __builtin_amdgcn_sched_barrier(0);
+      fd.words_qk(t0 + TOK, min(TOK, L - t0 - TOK), qk_on, rq, rk);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto loads_vz = [&] {
+      __builtin_amdgcn_sched_barrier(0);
+      fd.words_vz(t0 + TOK, min(TOK, L - t0 - TOK), vz_on, rv, rz);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto loads_side = [&] {
+      __builtin_amdgcn_sched_barrier(0);
+      side = fd.side_in(c + 2);
+      ang = fd.ang_in(c + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    if constexpr (!FULL) {
+      if (c + 1 < nsub) fd.words(t0 + TOK, min(TOK, L - t0 - TOK), qk_on, vz_on, rq, rk, rv, rz);
+      side = fd.side_in(c + 2);
+      ang = fd.ang_in(c + 2);
     }
-    side = fd.side_in(c + 2);
-    ang = fd.ang_in(c + 2);
 
     // outputs for query row tile `it` and P tiles pj = wp, wp + WPR, ...
     const int it = w / WPR, wp = w - it * WPR;
@@ -1305,6 +1352,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
       }
     }
+    if constexpr (FULL) loads_qk();
     // K~^T V products of the state carry, issued early (they depend only on staged tiles),
     // accumulated onto the decayed state
 #pragma unroll
@@ -1317,19 +1365,20 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
         for (int kk = 0; kk < ROWS; kk += 32) {
           const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
-              KT + nrow * LR + swz<ROWS>(kk + 8 * lg, nrow >> 3));
+              KT + nrow * LR + swz<ROWS>(kk + 8 * lg, nrow >> KSH));
           const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
-              VT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> 2));
+              VT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> VSH));
           st[k] = M::mma(av, bv, st[k]);
         }
       } else {
 #pragma unroll
         for (int kk = 0; kk < ROWS; kk += 4) {
-          st[k] = M::mma(KT[nrow * LR + swz<ROWS>(kk + lg, nrow >> 3)],
-                         VT[prow * LR + swz<ROWS>(kk + lg, prow >> 2)], st[k]);
+          st[k] = M::mma(KT[nrow * LR + swz<ROWS>(kk + lg, nrow >> KSH)],
+                         VT[prow * LR + swz<ROWS>(kk + lg, prow >> VSH)], st[k]);
         }
       }
     }
+    if constexpr (FULL) loads_vz();
     // phases of sub-chunk c + 1 (its dt block was computed two iterations ago)
     if (ph_on && c + 1 < nsub) {
       float pa[TPL];
@@ -1338,6 +1387,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
                                        scb(c + 1) + SB_::DTV, t0 + TOK, L, pg, lane, angles, pa,
                                        fph);
     }
+    if constexpr (FULL) loads_side();
     // decayed scores W[t, s] = Sc[t, s] d[t, s] in FP32
     const float cum_t = SC[SB_::CUM + tq];
     const float gam_t = SC[SB_::GAM + tq];
@@ -1394,7 +1444,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     for (int pq = 0; pq < kPT / WPR; ++pq) {
       const int pj = wp + pq * WPR;
       const int pcol = 16 * pj + l16;  // the A-operand row of V^T / rnd(S)
-      const int key = pcol >> 2;
+      const int key = pcol >> VSH;
       f4 yi = zero4(), ye = zero4();
       if constexpr (!F32) {
         // intra: V^T W^T, the K axis permuted as the D-layout of wsc
