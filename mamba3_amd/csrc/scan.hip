@@ -231,13 +231,26 @@ __device__ __forceinline__ void load_words(uint32_t (&w)[NW], const T* p, int n,
   }
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Two values rounded to a 16-bit type (round to nearest even) and packed into one word, a
+// first: one packed convert for bf16.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  typedef T t2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, t2));
+}
+
 // Two adjacent activation values stored with one LDS write.
 template <typename T>
 __device__ __forceinline__ void st_pair(T* dst, float a, float b) {
-  typename Mma<T>::v2 v;
-  v[0] = from_f<T>(a);
-  v[1] = from_f<T>(b);
-  *reinterpret_cast<typename Mma<T>::v2*>(dst) = v;
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<f32x2*>(dst) = (f32x2){a, b};
+  } else {
+    *reinterpret_cast<uint32_t*>(dst) = pack2<T>(a, b);
+  }
 }
 
 // Four adjacent activation values stored with one LDS write.
@@ -246,10 +259,7 @@ __device__ __forceinline__ void st_quad(T* dst, f4 x) {
   if constexpr (sizeof(T) == 4) {
     *reinterpret_cast<f4*>(dst) = x;
   } else {
-    typename Mma<T>::v4 v;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = from_f<T>(x[i]);
-    *reinterpret_cast<typename Mma<T>::v4*>(dst) = v;
+    *reinterpret_cast<u32x2*>(dst) = (u32x2){pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3])};
   }
 }
 
@@ -262,10 +272,8 @@ __device__ __forceinline__ void st_row8(T* dst, const float* x) {
     reinterpret_cast<f4*>(dst)[0] = a;
     reinterpret_cast<f4*>(dst)[1] = b;
   } else {
-    typename Mma<T>::v8 v;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = from_f<T>(x[i]);
-    *reinterpret_cast<typename Mma<T>::v8*>(dst) = v;
+    *reinterpret_cast<u32x4*>(dst) = (u32x4){pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3]),
+                                             pack2<T>(x[4], x[5]), pack2<T>(x[6], x[7])};
   }
 }
 
@@ -319,9 +327,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), bytes,
                                            0x00020000);
 }
-
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // NW raw words (NW in {2, 4, 8}) from a buffer at byte offset `off`.
 template <int NW>
@@ -1224,7 +1229,22 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           z[j][i] = raw_get<T>(rz[j], i);
         }
       }
-      if (R == 1) {
+      if (R == 1 && !F32) {
+        // the loaded 16-bit words go to LDS unchanged: VR / ZR rows as they are, VT pairs
+        // (token 2vp, token 2vp+1) of one column by a byte permute
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int p = p0 + i;
+          const uint32_t pr = __builtin_amdgcn_perm(rv[1][i >> 1], rv[0][i >> 1],
+                                                    (i & 1) ? 0x07060302u : 0x05040100u);
+          if (FULL || p < P) *reinterpret_cast<uint32_t*>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH)) = pr;
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          *reinterpret_cast<u32x2*>(VR + (2 * vp + j) * LP + p0) = (u32x2){rv[j][0], rv[j][1]};
+          *reinterpret_cast<u32x2*>(ZR + (2 * vp + j) * LP + p0) = (u32x2){rz[j][0], rz[j][1]};
+        }
+      } else if (R == 1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int p = p0 + i;
