@@ -5,6 +5,7 @@
 // (_triton.py:564-947), and the portable ops.mamba3_step (ops.py:825-879).
 #include "m3_common.hpp"
 #include "m3_host.hpp"
+#include "m3_math.h"
 
 namespace m3 {
 
@@ -311,6 +312,54 @@ __device__ __forceinline__ f4 ld4x(const m3_tensor& t, int64_t i) {
   return ld4<_Float16>(t.ptr, i);
 }
 
+// Runtime-dtype loads split into a load of the raw bits, without control flow, and a decode by
+// selects: a kernel issues all its small loads first and decodes afterwards, so no load waits for
+// another (a load inside a dtype branch, or decoded right away, ends in a full wait). Every
+// address stays inside the element (16-bit tensors re-read their first half / first 8 bytes where
+// FP32 reads the second).
+struct RawX { uint32_t lo, hi; };
+struct Raw4 { uint32_t w[4]; };
+
+__device__ __forceinline__ RawX ldraw(const void* p, int dtype, int64_t i) {
+  const bool w = dtype == M3_F32;
+  const uint16_t* e =
+      reinterpret_cast<const uint16_t*>(static_cast<const char*>(p) + i * (w ? 4 : 2));
+  return RawX{e[0], e[w ? 1 : 0]};
+}
+
+__device__ __forceinline__ float decode_x(uint32_t lo, uint32_t hi, int dtype) {
+  const float f32 = __uint_as_float(lo | (hi << 16));
+  const float bf = __uint_as_float(lo << 16);
+  const float f16 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(lo)));
+  return dtype == M3_F32 ? f32 : (dtype == M3_BF16 ? bf : f16);
+}
+
+__device__ __forceinline__ float decode(RawX r, int dtype) { return decode_x(r.lo, r.hi, dtype); }
+
+// Four consecutive elements (8-byte aligned for 16-bit types, 16-byte for FP32).
+__device__ __forceinline__ Raw4 ldraw4(const m3_tensor& t, int64_t i) {
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  const bool w = t.dtype == M3_F32;
+  const char* base = static_cast<const char*>(t.ptr) + i * (w ? 4 : 2);
+  const u2 x = *reinterpret_cast<const u2*>(base);
+  const u2 y = *reinterpret_cast<const u2*>(base + (w ? 8 : 0));
+  return Raw4{{x[0], x[1], y[0], y[1]}};
+}
+
+__device__ __forceinline__ f4 decode4(const Raw4& r, int dtype) {
+  const uint32_t half[4] = {r.w[0] & 0xffffu, r.w[0] >> 16, r.w[1] & 0xffffu, r.w[1] >> 16};
+  f4 v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] = dtype == M3_F32 ? __uint_as_float(r.w[j]) : decode_x(half[j], 0u, dtype);
+  }
+  return v;
+}
+
+__device__ __forceinline__ float ldx_nb(const void* p, int dtype, int64_t i) {
+  return decode(ldraw(p, dtype, i), dtype);
+}
+
 template <typename T>
 __device__ __forceinline__ void st4(void* base, int64_t i, const float (&x)[4]) {
   if constexpr (sizeof(T) == 4) {
@@ -327,18 +376,21 @@ __device__ __forceinline__ void st4(void* base, int64_t i, const float (&x)[4]) 
   }
 }
 
-// The model's decode shape (N = 128, P = 64, 32 angles), one 256-thread workgroup per
-// (batch, head), with no LDS round trip before the state update: thread (row group rg = tid / 32,
-// column group c = tid % 32) owns columns 4c .. 4c+3 of the state rows rg + 8k, k < 8. Its state
+// The model's decode shape (N = 128, P = 64, 32 angles), one workgroup of 32 * 64 / RPT threads
+// per (batch, head), with no LDS round trip before the state update: thread (row group
+// rg = tid / 32, column group c = tid % 32) owns columns 4c .. 4c+3 of the state rows rg + RG k,
+// k < RPT (RG = 64 / RPT). RPT = 8 (256 threads) streams large batches; RPT = 2 (1024 threads)
+// shortens the per-row chain of each workgroup when there are few (batch, head) pairs. Its state
 // loads are issued first; while they are in flight it computes, for every rank, the normed,
 // biased, rotated q / k of its columns (the RMSNorm sums and the MIMO rotation partner by
 // cross-lane exchange within its 32-lane half-wave) and the phases of the angles those columns
 // use. Per-row rank values and gates go through LDS behind one barrier. The readout sums over a
-// half-wave use DPP; lane c = k finishes row rg + 8k. The small cache outputs are written after a
+// half-wave use DPP; lane c = k finishes row rg + RG k. The small cache outputs are written after a
 // final barrier, when every thread has consumed the cache inputs they may alias.
-template <typename T, int R>
-__global__ __launch_bounds__(kStepThreads) void step128_kernel(const m3_step_args a) {
-  constexpr int N = 128, P = 64, S = 32, RPT = 8;
+template <typename T, int R, int RPT>
+__global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_args a) {
+  constexpr int N = 128, P = 64, S = 32;
+  constexpr int RG = P / RPT;  // row groups: thread rows rg + RG k, k < RPT
   const int H = a.heads;
   const int bh = blockIdx.x;
   const int b = bh / H, h = bh - b * H;
@@ -361,10 +413,67 @@ __global__ __launch_bounds__(kStepThreads) void step128_kernel(const m3_step_arg
   f4 st[RPT];
 #pragma unroll
   for (int k = 0; k < RPT; ++k) {
-    st[k] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(sin_ + (rg + 8 * k) * sp_in));
+    st[k] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(sin_ + (rg + RG * k) * sp_in));
   }
 
-  // (2) per-row rank values and gates (thread p < P), into LDS
+  // (3) every small input of the (b, h): raw loads issued together, decoded after
+  const RawX dt_r = ldraw(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + h * a.dt.stride[1]);
+  const RawX a_r = ldraw(a.a.ptr, a.a.dtype, b * a.a.stride[0] + h * a.a.stride[1]);
+  const RawX trap_r = ldraw(a.trap.ptr, a.trap.dtype, b * a.trap.stride[0] + h * a.trap.stride[1]);
+  const RawX D_r = ldraw(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
+  RawX dtb_r{0u, 0u};
+  if (a.raw_dt) dtb_r = ldraw(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]);
+  // phase roles: SISO pairs (2j, 2j+1) -> angles 2c, 2c+1 (c < 16); MIMO pairs (j, j + 2S) ->
+  // angles n0 .. n0+3 for the first (c < 8) and third (16 <= c < 24) quarters
+  int j0 = -1, nj = 0;
+  if (rotate) {
+    if (!mimo) {
+      if (c < S / 2) { j0 = 2 * c; nj = 2; }
+    } else if (c < S / 4) {
+      j0 = n0; nj = 4;
+    } else if (c >= S / 2 && c < 3 * S / 4) {
+      j0 = n0 - 2 * S; nj = 4;
+    }
+  }
+  const float* ph_in = static_cast<const float*>(a.phase_in.ptr) + b * a.phase_in.stride[0] +
+                       h * a.phase_in.stride[1];
+  float old[4] = {0.f, 0.f, 0.f, 0.f};
+  RawX th_r[4] = {};
+  if (rotate) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = nj > 0 ? j0 + min(i, nj - 1) : 0;  // lanes without angles read angle 0
+      old[i] = ph_in[j * a.phase_in.stride[2]];
+    }
+  }
+  if (rotate && angles) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = nj > 0 ? j0 + min(i, nj - 1) : 0;
+      th_r[i] = ldraw(a.angles.ptr, a.angles.dtype, b * a.angles.stride[0] + j * a.angles.stride[1]);
+    }
+  }
+  Raw4 wq_r{}, wk_r{}, bq_r[R] = {}, bk_r[R] = {};
+  f4 qx[R], kx[R], px[R];
+  if (norm) {
+    wq_r = ldraw4(a.q_norm_w, n0);  // weights may be FP32 or the activation type
+    wk_r = ldraw4(a.k_norm_w, n0);
+  }
+  if (bias) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      bq_r[r] = ldraw4(a.q_bias, h * a.q_bias.stride[0] + r * a.q_bias.stride[1] + n0);
+      bk_r[r] = ldraw4(a.k_bias, h * a.k_bias.stride[0] + r * a.k_bias.stride[1] + n0);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    qx[r] = ld4<T>(a.q.ptr, b * a.q.stride[0] + g * a.q.stride[1] + r * a.q.stride[2] + n0);
+    kx[r] = ld4<T>(a.k.ptr, b * a.k.stride[0] + g * a.k.stride[1] + r * a.k.stride[2] + n0);
+    px[r] = ld4<T>(a.prev_k.ptr, b * a.prev_k.stride[0] + h * a.prev_k.stride[1] +
+                                     r * a.prev_k.stride[2] + n0);
+  }
+  // (2) per-row rank values and gates (thread p < P), into LDS, after the loads above are issued
   if (tid < P) {
     const int p = tid;
     const float v = ld_act<T>(a.value, b * a.value.stride[0] + h * a.value.stride[1] + p);
@@ -374,15 +483,15 @@ __global__ __launch_bounds__(kStepThreads) void step128_kernel(const m3_step_arg
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (R > 1) {
-        const float mx = rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
-                                    h * a.mimo_x.stride[0] + r * a.mimo_x.stride[1] + p));
-        const float mz = rnd<T>(ldx(a.mimo_z.ptr, a.mimo_z.dtype,
-                                    h * a.mimo_z.stride[0] + r * a.mimo_z.stride[1] + p));
+        const float mx = rnd<T>(ldx_nb(a.mimo_x.ptr, a.mimo_x.dtype,
+                                       h * a.mimo_x.stride[0] + r * a.mimo_x.stride[1] + p));
+        const float mz = rnd<T>(ldx_nb(a.mimo_z.ptr, a.mimo_z.dtype,
+                                       h * a.mimo_z.stride[0] + r * a.mimo_z.stride[1] + p));
         s_vr[r][p] = mul_r<T>(v, mx);
         s_pvr[r][p] = mul_r<T>(pv, mx);
         s_zr[r][p] = mul_r<T>(z, mz);
-        s_mo[r][p] = ldx(a.mimo_out.ptr, a.mimo_out.dtype,
-                         h * a.mimo_out.stride[0] + r * a.mimo_out.stride[1] + p);
+        s_mo[r][p] = ldx_nb(a.mimo_out.ptr, a.mimo_out.dtype,
+                            h * a.mimo_out.stride[0] + r * a.mimo_out.stride[1] + p);
       } else {
         s_vr[r][p] = v;
         s_pvr[r][p] = pv;
@@ -397,70 +506,54 @@ __global__ __launch_bounds__(kStepThreads) void step128_kernel(const m3_step_arg
     }
   }
 
-  // (3) per-(b, h) scalars
+  const float dt_in = decode(dt_r, a.dt.dtype), a_in = decode(a_r, a.a.dtype);
+  const float trap_in = decode(trap_r, a.trap.dtype), Dh = decode(D_r, a.D.dtype);
+  const float dtb_in = a.raw_dt ? decode(dtb_r, a.dt_bias.dtype) : 0.f;
+  float th[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) th[i] = decode(th_r[i], a.angles.dtype);
+  f4 wq, wk, bq[R], bk[R];
+  wq = decode4(wq_r, a.q_norm_w.dtype);
+  wk = decode4(wk_r, a.k_norm_w.dtype);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    bq[r] = decode4(bq_r[r], a.q_bias.dtype);
+    bk[r] = decode4(bk_r[r], a.k_bias.dtype);
+  }
+
+  // per-(b, h) scalars
   float dt, adt;
-  dt_adt(a.raw_dt, ldx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + h * a.dt.stride[1]),
-         ldx(a.a.ptr, a.a.dtype, b * a.a.stride[0] + h * a.a.stride[1]),
-         a.raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]) : 0.f, dt, adt);
-  const float trap = sigmoidf(ldx(a.trap.ptr, a.trap.dtype,
-                                  b * a.trap.stride[0] + h * a.trap.stride[1]));
+  dt_adt(a.raw_dt, dt_in, a_in, dtb_in, dt, adt);
+  const float trap = sigmoidf(trap_in);
   const float alpha = expf(adt);
   const float beta = (1.f - trap) * dt * alpha;
   const float gamma = trap * dt;
-  const float Dh = ldx(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
 
-  // (4) phases of the angles this thread's columns use: SISO pairs (2j, 2j+1) -> angles 2c, 2c+1
-  // (c < 16); MIMO pairs (j, j + 2S) -> angles n0 .. n0+3 for the first (c < 8) and third
-  // (16 <= c < 24) quarters
-  int j0 = -1, nj = 0;
-  if (rotate) {
-    if (!mimo) {
-      if (c < S / 2) { j0 = 2 * c; nj = 2; }
-    } else if (c < S / 4) {
-      j0 = n0; nj = 4;
-    } else if (c >= S / 2 && c < 3 * S / 4) {
-      j0 = n0 - 2 * S; nj = 4;
-    }
-  }
+  // (4) phases of the angles this thread's columns use
   float phn[4] = {0.f, 0.f, 0.f, 0.f}, cs[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
-  const float* ph_in = static_cast<const float*>(a.phase_in.ptr) + b * a.phase_in.stride[0] +
-                       h * a.phase_in.stride[1];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (i < nj) {
-      const int j = j0 + i;
-      const float old = ph_in[j * a.phase_in.stride[2]];
-      float ph = old;
-      if (angles) {
-        const float th = ldx(a.angles.ptr, a.angles.dtype,
-                             b * a.angles.stride[0] + j * a.angles.stride[1]);
-        ph = fmodf(__fadd_rn(old, phase_inc(th, dt)), kTwoPi);
-      }
+      float ph = old[i];
+      if (angles) ph = m3_fmod_2pi(__fadd_rn(old[i], phase_inc(th[i], dt)));
       phn[i] = ph;
-      cs[i] = rnd<T>(cosf(ph));
-      sn[i] = rnd<T>(sinf(ph));
+      float sv, cv;
+      sincosf(ph, &sv, &cv);
+      cs[i] = rnd<T>(cv);
+      sn[i] = rnd<T>(sv);
     }
   }
 
   // (5) q / k of this thread's columns, every rank: RMSNorm, weight, bias, rotation
-  f4 wq, wk;
-  if (norm) {
-    wq = ld4x(a.q_norm_w, n0);  // weights may be FP32 or the activation type
-    wk = ld4x(a.k_norm_w, n0);
-  }
   float qr[R][4], kr[R][4], pk[R][4];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const f4 qx = ld4<T>(a.q.ptr, b * a.q.stride[0] + g * a.q.stride[1] + r * a.q.stride[2] + n0);
-    const f4 kx = ld4<T>(a.k.ptr, b * a.k.stride[0] + g * a.k.stride[1] + r * a.k.stride[2] + n0);
-    const f4 px = ld4<T>(a.prev_k.ptr, b * a.prev_k.stride[0] + h * a.prev_k.stride[1] +
-                                           r * a.prev_k.stride[2] + n0);
     float q[4], k[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      q[j] = qx[j];
-      k[j] = kx[j];
-      pk[r][j] = px[j];
+      q[j] = qx[r][j];
+      k[j] = kx[r][j];
+      pk[r][j] = px[r][j];
     }
     if (norm) {
       float sq = 0.f, sk = 0.f;
@@ -480,12 +573,10 @@ __global__ __launch_bounds__(kStepThreads) void step128_kernel(const m3_step_arg
       }
     }
     if (bias) {
-      const f4 bq = ld4x(a.q_bias, h * a.q_bias.stride[0] + r * a.q_bias.stride[1] + n0);
-      const f4 bk = ld4x(a.k_bias, h * a.k_bias.stride[0] + r * a.k_bias.stride[1] + n0);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        q[j] = add_r<T>(q[j], rnd<T>(bq[j]));
-        k[j] = add_r<T>(k[j], rnd<T>(bk[j]));
+        q[j] = add_r<T>(q[j], rnd<T>(bq[r][j]));
+        k[j] = add_r<T>(k[j], rnd<T>(bk[r][j]));
       }
     }
     if (rotate && !mimo) {
@@ -529,11 +620,11 @@ __global__ __launch_bounds__(kStepThreads) void step128_kernel(const m3_step_arg
   }
   __syncthreads();  // the per-row LDS vectors
 
-  // (6) state update, readout and epilogue of rows rg + 8k
-  float yrow = 0.f;  // lane c = k keeps row rg + 8k's output
+  // (6) state update, readout and epilogue of rows rg + RG k
+  float yrow = 0.f;  // lane c = k keeps row rg + RG k's output
 #pragma unroll
   for (int k = 0; k < RPT; ++k) {
-    const int p = rg + 8 * k;
+    const int p = rg + RG * k;
     float po[4] = {0.f, 0.f, 0.f, 0.f}, co[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -561,7 +652,7 @@ __global__ __launch_bounds__(kStepThreads) void step128_kernel(const m3_step_arg
     if (c == k) yrow = y;
   }
   if (c < RPT) {
-    const int p = rg + 8 * c;
+    const int p = rg + RG * c;
     static_cast<T*>(a.out.ptr)[b * a.out.stride[0] + h * a.out.stride[1] + p] = from_f<T>(yrow);
   }
 
@@ -613,12 +704,27 @@ template <typename T>
 static int launch_step(const m3_step_args& a, hipStream_t stream) {
   const size_t lds = step_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles);
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kStepThreads);
-  // ranks 1 and 2 (R = 4 and 8 keep their per-rank q / k in LDS: fewer registers per thread)
-  if (a.rank <= 2 && step128_ok(a)) {
+  // Ranks 1 and 2; rank 4 only below 1024 (batch, head) pairs (with many, its four readout
+  // reductions per row make the LDS-staged step_kernel faster; rank 8 always uses that one).
+  // Below 1024 pairs the grid holds at most four waves per SIMD: ranks 1 and 2 take the
+  // 1024-thread form, whose per-row chain is shorter.
+  const bool few = static_cast<int64_t>(a.batch) * a.heads < 1024;
+  if ((a.rank <= 2 || (a.rank == 4 && few)) && step128_ok(a)) {
+    const dim3 wide(32 * 64 / 2);
     if (a.rank == 1) {
-      hipLaunchKernelGGL((step128_kernel<T, 1>), grid, block, 0, stream, a);
+      if (few) {
+        hipLaunchKernelGGL((step128_kernel<T, 1, 2>), grid, wide, 0, stream, a);
+      } else {
+        hipLaunchKernelGGL((step128_kernel<T, 1, 8>), grid, block, 0, stream, a);
+      }
+    } else if (a.rank == 2) {
+      if (few) {
+        hipLaunchKernelGGL((step128_kernel<T, 2, 2>), grid, wide, 0, stream, a);
+      } else {
+        hipLaunchKernelGGL((step128_kernel<T, 2, 8>), grid, block, 0, stream, a);
+      }
     } else {
-      hipLaunchKernelGGL((step128_kernel<T, 2>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((step128_kernel<T, 4, 8>), grid, block, 0, stream, a);
     }
     return check_launch("m3_step");
   }

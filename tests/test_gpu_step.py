@@ -95,6 +95,40 @@ def test_fused_step_matches_oracle(dtype, rank, dims):
                                else 2e-3)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rank", [1, 2, 4])
+def test_fused_step_many_heads_matches_oracle(dtype, rank):
+    """1088 (batch, head) pairs: the launch shape of large decode batches (256 threads per
+    pair, 8 state rows per thread for ranks 1 and 2; the LDS-staged kernel for rank 4), at the
+    model's head shape, both out of place and with the outputs aliasing the cache."""
+    inp = _inputs(rank, dtype, batch=17, heads=64, seed=20 + rank)
+    y_ref, (ph_ref, s_ref, k_ref, _) = _oracle_fused(inp)
+    d = _dev(inp)
+    with torch.inference_mode():
+        y, (ph, s, k, v) = ops.fused_step(**d)
+    torch.cuda.synchronize()
+    print(f"step B=17 H=64 {dtype} R={rank}: "
+          f"y {(y.float().cpu() - y_ref.float()).abs().max():.2e} "
+          f"S {(s.cpu() - s_ref).abs().max():.2e}", flush=True)
+    torch.testing.assert_close(y.float().cpu(), y_ref.float(), **_tol(dtype))
+    torch.testing.assert_close(ph.cpu(), ph_ref, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(k.float().cpu(), k_ref.float(), **_tol(dtype))
+    s_tol = 1e-4 if dtype == torch.float32 else 2e-3
+    torch.testing.assert_close(s.cpu(), s_ref, rtol=1e-4, atol=s_tol)
+    cache = tuple(t.clone() for t in d["cache"])
+    with torch.inference_mode():
+        y2, nxt = ops._step_call(d["q"], d["k"], d["value"], d["gate"], d["adt"], d["dt"],
+                                 d["trap_logits"], d["angle_rate"], d["D"], cache,
+                                 mimo_x=d["mimo_x"], mimo_z=d["mimo_z"],
+                                 mimo_out=d["mimo_out"], phase_mode=2, out_cache=cache)
+    assert all(a.data_ptr() == b.data_ptr() for a, b in zip(nxt, cache))
+    torch.testing.assert_close(y2, y)
+    torch.testing.assert_close(cache[1], s)
+    torch.testing.assert_close(cache[0], ph)
+    torch.testing.assert_close(cache[2], k)
+    torch.testing.assert_close(cache[3].cpu(), inp["value"])
+
+
 @pytest.mark.parametrize("rank", [1, 4])
 def test_mamba3_step_uses_rotated_inputs_and_passes_phase(rank):
     inp = _inputs(rank, torch.float32, seed=11)
