@@ -111,7 +111,7 @@ template <typename T> struct Layout {
   // its rows), the angle tile, two cos / sin tables ([token][angle][cos, sin], token stride CST
   // for 16-byte aligned rows)
   static constexpr int TM = ROWS;
-  static constexpr int SCB = 7 * TM + 8 + 2 * ROWS, SC0 = 0;
+  static constexpr int SCB = 5 * TM + 8 + 2 * ROWS, SC0 = 0;
   static constexpr int ANG = SC0 + 2 * SCB;  // [TM / 4][kSMax][4]
   static constexpr int CST = 2 * kSMax + 4, CSB = TM * CST;
   static constexpr int CS0 = ANG + TM * kSMax, PBASE = CS0 + 2 * CSB;
@@ -121,13 +121,14 @@ template <typename T> struct Layout {
 };
 
 // Per-token scalar block of one sub-chunk of TOK tokens (floats, token-indexed arrays): dt, the
-// within-chunk cumsum of adt and its exp, the exp-trapezoid scale, gamma, scale * decay to the
-// sub-chunk's end (the carry), scale * decay to the end of the token's 16-row tile, the cumsum
-// at each tile end, exp of the last cumsum. The prep pass writes them; the scan copies them to LDS.
+// within-chunk cumsum of adt, the exp-trapezoid scale, gamma, scale * decay to the end of the
+// token's 16-row tile; then the cumsum at each tile end, exp of the last cumsum and the last
+// cumsum itself. The prep pass writes them; the scan copies them to LDS (and takes exp(cum) and
+// scale * exp(cum_last - cum) from them itself, an exp per lane).
 template <int TOK> struct ScBlk {
-  static constexpr int DTV = 0, CUM = TOK, ECUM = 2 * TOK, SCL = 3 * TOK, GAM = 4 * TOK;
-  static constexpr int VSF = 5 * TOK, BSC = 6 * TOK, CEND = 7 * TOK, ECL = 7 * TOK + 4;
-  static constexpr int SIZE = 7 * TOK + 8;
+  static constexpr int DTV = 0, CUM = TOK, SCL = 2 * TOK, GAM = 3 * TOK, BSC = 4 * TOK;
+  static constexpr int CEND = 5 * TOK, ECL = 5 * TOK + 4, CL = 5 * TOK + 5;
+  static constexpr int SIZE = 5 * TOK + 8;
 };
 
 // Per-launch values shared by host and device.
@@ -697,24 +698,37 @@ __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __res
   const bool tv = lane < wn;
   const bool nv = lane < TOK && t + 1 < L;
   const bool raw_dt = a.raw_dt != 0;
-  const float dt_bias = raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0])
-                               : 0.f;
-  const int64_t base_dt = b * a.dt.stride[0] + h * a.dt.stride[2];
-  const int64_t base_a = b * a.a.stride[0] + h * a.a.stride[2];
-  const int64_t base_tr = b * a.trap.stride[0] + h * a.trap.stride[2];
-  float dt = 0.f, adt = 0.f, tr = 0.f, right = 0.f;
+  // (b, h, c) are wave-uniform: the row bases are scalar; per-token offsets fit 31 bits
+  const void* row_dt = offx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + h * a.dt.stride[2]);
+  const void* row_a = offx(a.a.ptr, a.a.dtype, b * a.a.stride[0] + h * a.a.stride[2]);
+  const void* row_tr = offx(a.trap.ptr, a.trap.dtype, b * a.trap.stride[0] + h * a.trap.stride[2]);
+  const int st_dt = static_cast<int>(a.dt.stride[1]), st_a = static_cast<int>(a.a.stride[1]);
+  const int st_tr = static_cast<int>(a.trap.stride[1]);
+  // raw loads first, all in flight together: this lane's token (clamped to L - 1; masked below)
+  // and the token after the sub-chunk, whose dt (1 - sigmoid(trap)) the last token needs
+  const int tl = min(t, L - 1), tn = min(tb + TOK, L - 1);
+  const RawX dt_r = ldraw(row_dt, a.dt.dtype, tl * st_dt);
+  const RawX a_r = ldraw(row_a, a.a.dtype, tl * st_a);
+  const RawX tr_r = ldraw(row_tr, a.trap.dtype, tl * st_tr);
+  const RawX dtn_r = ldraw(row_dt, a.dt.dtype, tn * st_dt);
+  const RawX trn_r = ldraw(row_tr, a.trap.dtype, tn * st_tr);
+  RawX dtb_r{0u, 0u};
+  if (raw_dt) dtb_r = ldraw(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]);
+  const float dt_bias = raw_dt ? decode(dtb_r, a.dt_bias.dtype) : 0.f;
+  float dt = 0.f, adt = 0.f, tr = 0.f;
   if (tv) {
-    dt_adt(raw_dt, ldx(a.dt.ptr, a.dt.dtype, base_dt + t * a.dt.stride[1]),
-           ldx(a.a.ptr, a.a.dtype, base_a + t * a.a.stride[1]), dt_bias, dt, adt);
-    tr = sigmoidf(ldx(a.trap.ptr, a.trap.dtype, base_tr + t * a.trap.stride[1]));
+    dt_adt_fast(raw_dt, decode(dt_r, a.dt.dtype), decode(a_r, a.a.dtype), dt_bias, dt, adt);
+    tr = sigmoid_fast(decode(tr_r, a.trap.dtype));
   }
-  if (nv) {
+  // right = dt' (1 - sigmoid(trap')) of the next token: lane + 1's, the last lane's from tn
+  const float own = dt * (1.f - tr);
+  float right = __shfl_down(own, 1);
+  if (lane == TOK - 1) {
     float dn, an;
-    dt_adt(raw_dt, ldx(a.dt.ptr, a.dt.dtype, base_dt + (t + 1) * a.dt.stride[1]), 0.f,
-           dt_bias, dn, an);
-    right = dn * (1.f - sigmoidf(ldx(a.trap.ptr, a.trap.dtype,
-                                     base_tr + (t + 1) * a.trap.stride[1])));
+    dt_adt_fast(raw_dt, decode(dtn_r, a.dt.dtype), 0.f, dt_bias, dn, an);
+    right = dn * (1.f - sigmoid_fast(decode(trn_r, a.trap.dtype)));
   }
+  if (!nv) right = 0.f;
   const float gamma = dt * tr;
   const float scale = gamma + right;
   const float cum = wave_incl_scan(adt, lane);
@@ -733,14 +747,15 @@ __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __res
   if (lane < TOK) {
     o[B::DTV + lane] = dt;
     o[B::CUM + lane] = cv;
-    o[B::ECUM + lane] = tv ? __expf(cv) : 0.f;
     o[B::SCL + lane] = tv ? scale : 0.f;
     o[B::GAM + lane] = gamma;
-    o[B::VSF + lane] = tv ? scale * __expf(cum_last - cv) : 0.f;
     o[B::BSC + lane] = tv ? scale * __expf(cend - cv) : 0.f;
     if ((lane & (TPT - 1)) == 0) o[B::CEND + lane / TPT] = cend;
   }
-  if (lane == 0) o[B::ECL] = __expf(cum_last);
+  if (lane == 0) {
+    o[B::ECL] = __expf(cum_last);
+    o[B::CL] = cum_last;
+  }
 }
 
 // Head-independent and per-(head, sub-chunk) work ahead of the scan, three block ranges:
@@ -814,13 +829,14 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
     const int b = bt4 / g.L4, t = 4 * (bt4 - b * g.L4) + i;
     float v = 0.f;
     if (t < L) {
-      const float th = ldx(a.phase.ptr, a.phase.dtype,
-                           b * a.phase.stride[0] + t * a.phase.stride[1] + s * a.phase.stride[2]);
+      const float th = decode(ldraw(a.phase.ptr, a.phase.dtype, b * a.phase.stride[0] +
+                                                          t * a.phase.stride[1] + s * a.phase.stride[2]),
+                              a.phase.dtype);
       v = __fmul_rn(kPi, tanhf(th));
     }
     ws[g.ws_ang + static_cast<int64_t>(e)] = v;
   } else {
-    const int idx = (blk - nb_norm - nb_ang) * 4 + (tid >> 6);
+    const int idx = (blk - nb_norm - nb_ang) * 4 + __builtin_amdgcn_readfirstlane(tid >> 6);
     if (idx >= a.batch * a.heads * g.nsub) return;  // whole waves leave together
     const int bh = idx / g.nsub, c = idx - bh * g.nsub;
     const int b = bh / a.heads, h = bh - b * a.heads;
@@ -1199,7 +1215,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       }
       // K^T for the carry, each row scaled by its token's scale * end decay (the carry's
       // K~ e^{cum_last - cum}, ops.py:806-816)
-      const float e0 = SC[SB_::VSF + (2 * rp) / R], e1 = SC[SB_::VSF + (2 * rp + 1) / R];
+      const int r0 = (2 * rp) / R, r1 = (2 * rp + 1) / R;
+      const float cl = SC[SB_::CL];
+      const float e0 = SC[SB_::SCL + r0] * __expf(cl - SC[SB_::CUM + r0]);
+      const float e1 = SC[SB_::SCL + r1] * __expf(cl - SC[SB_::CUM + r1]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int n = n0 + i;
@@ -1458,7 +1477,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     }
     // Outputs, computed transposed (Y^T tiles, rows p, columns the row tile's 16 (token, rank)
     // rows): a lane holds 4 consecutive p of one row, stored as one vector.
-    const float ecum_t = SC[SB_::ECUM + tq];
+    const float ecum_t = __expf(cum_t);
     const int rr = trow - tq * R;  // the lane's rank
 #pragma unroll
     for (int pq = 0; pq < kPT / WPR; ++pq) {
@@ -1606,7 +1625,7 @@ static size_t ws_layout(const m3_scan_args& a, ScanGeom& g) {
   g.tok = rows / rank > 0 ? rows / rank : 1;
   const int64_t len = a.length > 0 ? a.length : 0;
   g.nsub = static_cast<int>((len + g.tok - 1) / g.tok);
-  g.scw = 7 * g.tok + 8;
+  g.scw = 5 * g.tok + 8;  // ScBlk<tok>::SIZE
   g.L4 = static_cast<int>((len + 3) / 4);
   const bool norm = a.q_norm_w.ptr != nullptr;
   const bool angles = a.phase_mode == M3_PHASE_ANGLES;

@@ -312,50 +312,6 @@ __device__ __forceinline__ f4 ld4x(const m3_tensor& t, int64_t i) {
   return ld4<_Float16>(t.ptr, i);
 }
 
-// Runtime-dtype loads split into a load of the raw bits, without control flow, and a decode by
-// selects: a kernel issues all its small loads first and decodes afterwards, so no load waits for
-// another (a load inside a dtype branch, or decoded right away, ends in a full wait). Every
-// address stays inside the element (16-bit tensors re-read their first half / first 8 bytes where
-// FP32 reads the second).
-struct RawX { uint32_t lo, hi; };
-struct Raw4 { uint32_t w[4]; };
-
-__device__ __forceinline__ RawX ldraw(const void* p, int dtype, int64_t i) {
-  const bool w = dtype == M3_F32;
-  const uint16_t* e =
-      reinterpret_cast<const uint16_t*>(static_cast<const char*>(p) + i * (w ? 4 : 2));
-  return RawX{e[0], e[w ? 1 : 0]};
-}
-
-__device__ __forceinline__ float decode_x(uint32_t lo, uint32_t hi, int dtype) {
-  const float f32 = __uint_as_float(lo | (hi << 16));
-  const float bf = __uint_as_float(lo << 16);
-  const float f16 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(lo)));
-  return dtype == M3_F32 ? f32 : (dtype == M3_BF16 ? bf : f16);
-}
-
-__device__ __forceinline__ float decode(RawX r, int dtype) { return decode_x(r.lo, r.hi, dtype); }
-
-// Four consecutive elements (8-byte aligned for 16-bit types, 16-byte for FP32).
-__device__ __forceinline__ Raw4 ldraw4(const m3_tensor& t, int64_t i) {
-  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-  const bool w = t.dtype == M3_F32;
-  const char* base = static_cast<const char*>(t.ptr) + i * (w ? 4 : 2);
-  const u2 x = *reinterpret_cast<const u2*>(base);
-  const u2 y = *reinterpret_cast<const u2*>(base + (w ? 8 : 0));
-  return Raw4{{x[0], x[1], y[0], y[1]}};
-}
-
-__device__ __forceinline__ f4 decode4(const Raw4& r, int dtype) {
-  const uint32_t half[4] = {r.w[0] & 0xffffu, r.w[0] >> 16, r.w[1] & 0xffffu, r.w[1] >> 16};
-  f4 v;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    v[j] = dtype == M3_F32 ? __uint_as_float(r.w[j]) : decode_x(half[j], 0u, dtype);
-  }
-  return v;
-}
-
 __device__ __forceinline__ float ldx_nb(const void* p, int dtype, int64_t i) {
   return decode(ldraw(p, dtype, i), dtype);
 }
