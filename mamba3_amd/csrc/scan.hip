@@ -690,7 +690,8 @@ __device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, fl
 // within-chunk cumsum of adt by a wave scan, and the decay products the scan uses.
 template <int TOK, int TPT>
 __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __restrict__ o,
-                                             int b, int h, int c, int lane) {
+                                             int h, int c, int lane, float dt_in, float a_in,
+                                             float tr_in, float dtn_in, float trn_in) {
   using B = ScBlk<TOK>;
   const int L = a.length;
   const int tb = c * TOK, t = tb + lane;
@@ -698,35 +699,23 @@ __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __res
   const bool tv = lane < wn;
   const bool nv = lane < TOK && t + 1 < L;
   const bool raw_dt = a.raw_dt != 0;
-  // (b, h, c) are wave-uniform: the row bases are scalar; per-token offsets fit 31 bits
-  const void* row_dt = offx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + h * a.dt.stride[2]);
-  const void* row_a = offx(a.a.ptr, a.a.dtype, b * a.a.stride[0] + h * a.a.stride[2]);
-  const void* row_tr = offx(a.trap.ptr, a.trap.dtype, b * a.trap.stride[0] + h * a.trap.stride[2]);
-  const int st_dt = static_cast<int>(a.dt.stride[1]), st_a = static_cast<int>(a.a.stride[1]);
-  const int st_tr = static_cast<int>(a.trap.stride[1]);
-  // raw loads first, all in flight together: this lane's token (clamped to L - 1; masked below)
-  // and the token after the sub-chunk, whose dt (1 - sigmoid(trap)) the last token needs
-  const int tl = min(t, L - 1), tn = min(tb + TOK, L - 1);
-  const RawX dt_r = ldraw(row_dt, a.dt.dtype, tl * st_dt);
-  const RawX a_r = ldraw(row_a, a.a.dtype, tl * st_a);
-  const RawX tr_r = ldraw(row_tr, a.trap.dtype, tl * st_tr);
-  const RawX dtn_r = ldraw(row_dt, a.dt.dtype, tn * st_dt);
-  const RawX trn_r = ldraw(row_tr, a.trap.dtype, tn * st_tr);
-  RawX dtb_r{0u, 0u};
-  if (raw_dt) dtb_r = ldraw(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]);
-  const float dt_bias = raw_dt ? decode(dtb_r, a.dt_bias.dtype) : 0.f;
+  const float dt_bias =
+      raw_dt ? decode(ldraw(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]),
+                      a.dt_bias.dtype)
+             : 0.f;
   float dt = 0.f, adt = 0.f, tr = 0.f;
   if (tv) {
-    dt_adt_fast(raw_dt, decode(dt_r, a.dt.dtype), decode(a_r, a.a.dtype), dt_bias, dt, adt);
-    tr = sigmoid_fast(decode(tr_r, a.trap.dtype));
+    dt_adt_fast(raw_dt, dt_in, a_in, dt_bias, dt, adt);
+    tr = sigmoid_fast(tr_in);
   }
-  // right = dt' (1 - sigmoid(trap')) of the next token: lane + 1's, the last lane's from tn
+  // right = dt' (1 - sigmoid(trap')) of the next token: lane + 1's; the last lane's from the
+  // token after the sub-chunk (dtn_in, trn_in)
   const float own = dt * (1.f - tr);
   float right = __shfl_down(own, 1);
   if (lane == TOK - 1) {
     float dn, an;
-    dt_adt_fast(raw_dt, decode(dtn_r, a.dt.dtype), 0.f, dt_bias, dn, an);
-    right = dn * (1.f - sigmoid_fast(decode(trn_r, a.trap.dtype)));
+    dt_adt_fast(raw_dt, dtn_in, 0.f, dt_bias, dn, an);
+    right = dn * (1.f - sigmoid_fast(trn_in));
   }
   if (!nv) right = 0.f;
   const float gamma = dt * tr;
@@ -763,7 +752,10 @@ __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __res
 //                lane: its RMSNorm factor 1 / sqrt(mean(x^2) + eps) (model.py:190-191);
 //  [.., +nb_ang) one lane per (token, angle), token padded to a multiple of 4: pi * tanh(angle)
 //                (model.py:225-228), 0 in the padding;
-//  [.., +nb_sc)  one wave per (batch, head, sub-chunk): its scalar block.
+//  [.., +nb_sc)  one workgroup per (batch, sub-chunk): the dt / a / trap of its TOK tokens and
+//                the next sub-chunk's first, every head, loaded with consecutive lanes on
+//                consecutive heads (32 heads per pass) into LDS; then one wave per head computes
+//                that head's scalar block.
 template <typename T, int R>
 __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const ScanGeom g,
                                                    float* __restrict__ ws, int nb_norm,
@@ -836,12 +828,52 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
     }
     ws[g.ws_ang + static_cast<int64_t>(e)] = v;
   } else {
-    const int idx = (blk - nb_norm - nb_ang) * 4 + __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (idx >= a.batch * a.heads * g.nsub) return;  // whole waves leave together
-    const int bh = idx / g.nsub, c = idx - bh * g.nsub;
-    const int b = bh / a.heads, h = bh - b * a.heads;
-    scalar_block<TOK, TPT>(a, ws + g.ws_sc + static_cast<int64_t>(idx) * g.scw, b, h, c,
-                           tid & 63);
+    const int bc = blk - nb_norm - nb_ang;
+    if (bc >= a.batch * g.nsub) return;  // whole workgroups leave together
+    const int b = bc / g.nsub, c = bc - b * g.nsub;
+    constexpr int HG = 32, NE = (TOK + 1) * HG, NIT = (NE + 255) / 256;
+    __shared__ float s_in[3][TOK + 1][HG + 1];
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const char* base_dt = static_cast<const char*>(offx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0]));
+    const char* base_a = static_cast<const char*>(offx(a.a.ptr, a.a.dtype, b * a.a.stride[0]));
+    const char* base_tr =
+        static_cast<const char*>(offx(a.trap.ptr, a.trap.dtype, b * a.trap.stride[0]));
+    const int s1_dt = static_cast<int>(a.dt.stride[1]), s2_dt = static_cast<int>(a.dt.stride[2]);
+    const int s1_a = static_cast<int>(a.a.stride[1]), s2_a = static_cast<int>(a.a.stride[2]);
+    const int s1_tr = static_cast<int>(a.trap.stride[1]), s2_tr = static_cast<int>(a.trap.stride[2]);
+    for (int h0 = 0; h0 < a.heads; h0 += HG) {
+      const int hn = min(HG, a.heads - h0);
+      // raw loads of every element first (clamped to valid tokens / heads), then decode and store
+      RawX rd[NIT], ra[NIT], rt[NIT];
+#pragma unroll
+      for (int k = 0; k < NIT; ++k) {
+        const int e = min(tid + 256 * k, NE - 1);
+        const int j = e / HG, hh = e - j * HG;
+        const int t = min(c * TOK + j, L - 1), h = h0 + min(hh, hn - 1);
+        rd[k] = ldraw(base_dt, a.dt.dtype, t * s1_dt + h * s2_dt);
+        ra[k] = ldraw(base_a, a.a.dtype, t * s1_a + h * s2_a);
+        rt[k] = ldraw(base_tr, a.trap.dtype, t * s1_tr + h * s2_tr);
+      }
+#pragma unroll
+      for (int k = 0; k < NIT; ++k) {
+        const int e = tid + 256 * k;
+        if (e < NE) {
+          const int j = e / HG, hh = e - j * HG;
+          s_in[0][j][hh] = decode(rd[k], a.dt.dtype);
+          s_in[1][j][hh] = decode(ra[k], a.a.dtype);
+          s_in[2][j][hh] = decode(rt[k], a.trap.dtype);
+        }
+      }
+      __syncthreads();
+      for (int hh = w; hh < hn; hh += 4) {
+        const int h = h0 + hh, j = min(lane, TOK - 1);
+        scalar_block<TOK, TPT>(
+            a, ws + g.ws_sc + (static_cast<int64_t>(b * a.heads + h) * g.nsub + c) * g.scw, h, c,
+            lane, s_in[0][j][hh], s_in[1][j][hh], s_in[2][j][hh], s_in[0][TOK][hh],
+            s_in[2][TOK][hh]);
+      }
+      __syncthreads();
+    }
   }
 }
 
@@ -1772,11 +1804,11 @@ static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
     const int64_t tokens = static_cast<int64_t>(a.batch) * a.length;
     const int64_t rows = g.ws_norm >= 0 ? tokens * 2 * a.groups * a.rank : 0;
     const int64_t ang = g.ws_ang >= 0 ? static_cast<int64_t>(a.batch) * g.L4 * a.num_angles * 4 : 0;
-    const int64_t blocks = static_cast<int64_t>(a.batch) * a.heads * g.nsub;
+    const int64_t blocks = static_cast<int64_t>(a.batch) * g.nsub;  // scalar-block workgroups
     if (rows >= INT32_MAX || ang >= INT32_MAX || blocks >= INT32_MAX || tokens >= INT32_MAX) {
       return fail(M3_EUNSUPPORTED, "m3_scan_fwd: too many tokens for one launch");
     }
-    const int64_t nb_norm = (rows + 15) / 16, nb_ang = (ang + 255) / 256, nb_sc = (blocks + 3) / 4;
+    const int64_t nb_norm = (rows + 15) / 16, nb_ang = (ang + 255) / 256, nb_sc = blocks;
     if (nb_norm + nb_ang + nb_sc > 0) {
       const dim3 pgrid(static_cast<unsigned>(nb_norm + nb_ang + nb_sc)), pblock(256);
       hipLaunchKernelGGL((prep_kernel<T, R>), pgrid, pblock, 0, stream, a, g,
