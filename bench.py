@@ -149,6 +149,15 @@ def bench_prefill(steps, warmup, log, copy_probe=False):
         proj=proj_size)
 
 
+def step_kernel_name(pairs, rank):
+    """The kernel m3_step dispatches for the model's decode shape (N 128, P 64, 32 angles)."""
+    if rank <= 2:
+        return f"m3::step128_kernel<__bf16, {rank}, {2 if pairs < 1024 else 8}>"
+    if rank == 4 and pairs < 1024:
+        return "m3::step128_kernel<__bf16, 4, 8>"
+    return f"m3::step_kernel<__bf16, {rank}>"
+
+
 def bench_decode(batch, steps, log, rank=1, prefix=2048):
     from mamba3_amd import Mamba3, ops
 
@@ -202,7 +211,7 @@ def bench_decode(batch, steps, log, rank=1, prefix=2048):
                 step_kernel=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS,
                                  unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
                                  us_per_launch=round(t_k * 1e6, 2), bytes_per_launch=nb,
-                                 kernel=f"m3::step_kernel<__bf16, {rank}>"))
+                                 kernel=step_kernel_name(batch * mixer.nheads, rank)))
 
 
 def bench_prefill_config(name, d_model, depth, rank, causal, shape, seed, log, iters=5):
