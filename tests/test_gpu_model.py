@@ -77,6 +77,29 @@ def test_forward_prefill_steps_match_oracle(case, bf16):
             torch.testing.assert_close(a.float().cpu(), b.float(), **tol)
 
 
+@pytest.mark.parametrize("length", [1, 63, 64, 65, 130, 700])
+def test_model_shape_lengths_match_oracle(length):
+    """The model's SISO shape (N 128, P 64, 32 angles: the full-shape kernels) in bf16 autocast
+    over 1 to 11 sub-chunks, ragged and exact: forward output, prefill output and cache."""
+    model, params, dims = _model(128, 128, 1, 1, seed=30)
+    torch.manual_seed(31)
+    x = torch.randn(2, length, 128)
+    with torch.inference_mode(), _oracle_ctx(True):
+        want = op.model_forward(params, x, dims)
+        _, want_cache = op.model_prefill(params, x, dims)
+    with torch.inference_mode(), _gpu_ctx(True):
+        got = model(x.to(DEV))
+        assert ops._HIP_LAST_SCAN_DISPATCH
+        prefix, cache = model.prefill(x.to(DEV))
+    torch.cuda.synchronize()
+    print(f"model shape L={length}: forward {(got.float().cpu() - want.float()).abs().max():.2e}",
+          flush=True)
+    torch.testing.assert_close(got.float().cpu(), want.float(), **BF16)
+    torch.testing.assert_close(prefix.float().cpu(), want.float(), **BF16)
+    for a, b in zip(cache[0], want_cache[0]):
+        torch.testing.assert_close(a.float().cpu(), b.float(), **BF16)
+
+
 @pytest.mark.parametrize("rank", [1, 4])
 def test_cached_steps_match_full_forward(rank):
     """Reference tests/test_model.py:164-184 (step-by-step from an empty cache)."""
