@@ -26,6 +26,7 @@
  *   m3_step         <- mamba3/ops.py:87-190  fused_step (launcher _triton.py:950-1151) and the
  *                      portable mamba3_step ops.py:825-879 with the step prologue of
  *                      _Mamba3Mixer.step model.py:431-469.
+ * m3_linear has no reference hook: it takes the decode step's projection GEMMs (see below).
  */
 #ifndef MAMBA3_HIP_H
 #define MAMBA3_HIP_H
@@ -171,6 +172,33 @@ typedef struct {
 } m3_step_args;
 
 int m3_step(const m3_step_args* args, hipStream_t stream);
+
+/*
+ * A linear layer of the decode path, out[M, N] = x'[M, K] * weight[N, K]^T (+ residual[M, N]),
+ * for few rows (M <= 256, one row per batch element): 16-bit x, weight, residual and out of one
+ * dtype, FP32 accumulation, one rounding. x' is x, or with norm_weight the RMS-normalised
+ * x * rsqrt(mean_k x^2 + norm_eps) * norm_weight (M <= 32 only). It has no counterpart among the
+ * reference's plugin hooks: it replaces the block's RMSNorm, the in_proj / out_proj nn.Linear
+ * calls and the residual add of a decode step (mamba3/model.py:441-458, 514-520), where a
+ * general GEMM leaves most of the GPU idle.
+ * K is a multiple of 32; x and weight rows are 16-byte aligned. The split of K over workgroups
+ * keeps FP32 partial sums in the caller's workspace (m3_linear_workspace_size, 0 when unsplit).
+ */
+typedef struct {
+  int64_t m, n, k;
+  int32_t dtype;        /* M3_BF16 or M3_F16 */
+  float norm_eps;
+  m3_tensor x;          /* [M, K] */
+  m3_tensor weight;     /* [N, K] */
+  m3_tensor norm_weight;/* [K] optional, 16-byte aligned */
+  m3_tensor residual;   /* [M, N] optional */
+  m3_tensor out;        /* [M, N]; may not overlap x or weight, may equal residual */
+  void* workspace;
+  size_t workspace_bytes;
+} m3_linear_args;
+
+int m3_linear_workspace_size(const m3_linear_args* args, size_t* bytes);
+int m3_linear(const m3_linear_args* args, hipStream_t stream);
 
 const char* m3_last_error(void);
 int m3_abi_version(void);

@@ -77,8 +77,17 @@ class StepArgs(ctypes.Structure):
     ]
 
 
+class LinearArgs(ctypes.Structure):
+    _fields_ = [
+        *[(n, ctypes.c_int64) for n in ("m", "n", "k")],
+        ("dtype", ctypes.c_int32), ("norm_eps", ctypes.c_float),
+        *[(n, _T) for n in ("x", "weight", "norm_weight", "residual", "out")],
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 ENTRY_POINTS = ("m3_scan_fwd", "m3_scan_workspace_size", "m3_chunk_state", "m3_step",
-                "m3_last_error", "m3_abi_version")
+                "m3_linear", "m3_linear_workspace_size", "m3_last_error", "m3_abi_version")
 
 _lib: ctypes.CDLL | None = None
 
@@ -92,12 +101,14 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is not built; run `python -m mamba3_amd.build` (hipcc, gfx950)")
     lib = ctypes.CDLL(LIB_PATH)
-    for name in ("m3_scan_fwd", "m3_chunk_state", "m3_step"):
+    for name in ("m3_scan_fwd", "m3_chunk_state", "m3_step", "m3_linear"):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-    lib.m3_scan_workspace_size.restype = ctypes.c_int
-    lib.m3_scan_workspace_size.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_size_t)]
+    for name in ("m3_scan_workspace_size", "m3_linear_workspace_size"):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_size_t)]
     lib.m3_last_error.restype = ctypes.c_char_p
     lib.m3_last_error.argtypes = []
     lib.m3_abi_version.restype = ctypes.c_int
@@ -130,14 +141,16 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise TypeError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16")
 
 
-def scan_workspace(args: ScanArgs, device: torch.device) -> torch.Tensor | None:
-    """Allocate (through torch's caching allocator) the workspace ``m3_scan_fwd`` needs and
-    record it in ``args``; the caller keeps the returned tensor alive across the call."""
+def scan_workspace(args: ctypes.Structure, device: torch.device,
+                   query: str = "m3_scan_workspace_size") -> torch.Tensor | None:
+    """Allocate (through torch's caching allocator) the workspace an entry point needs, as
+    its ``query`` function reports it, and record it in ``args``; the caller keeps the
+    returned tensor alive across the call."""
     lib = load()
     nbytes = ctypes.c_size_t(0)
-    rc = lib.m3_scan_workspace_size(ctypes.byref(args), ctypes.byref(nbytes))
+    rc = getattr(lib, query)(ctypes.byref(args), ctypes.byref(nbytes))
     if rc != 0:
-        raise HipError("m3_scan_workspace_size", rc, lib.m3_last_error().decode(errors="replace"))
+        raise HipError(query, rc, lib.m3_last_error().decode(errors="replace"))
     if nbytes.value == 0:
         return None
     ws = torch.empty(nbytes.value, dtype=torch.uint8, device=device)

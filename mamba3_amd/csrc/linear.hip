@@ -1,0 +1,563 @@
+// m3_linear: out[M, N] = x[M, K] * weight[N, K]^T (+ residual) for the few rows of a decode step.
+//
+// A general GEMM tiles M = 1..256 rows poorly: its large tiles leave most of the 256 CUs idle
+// and each streams the weight at a fraction of HBM bandwidth. Two kernels, both on the bf16 /
+// f16 MFMA 16x16x32 (FP32 accumulation), both keeping several K steps of loads in flight per
+// wave in a register ring:
+//
+// rows kernel (M <= 32): a weight stream. The B operand of a 16x16x32 MFMA is, per lane, 16
+// contiguous bytes of one weight row (lane l16 + 16 lg holds row l16, elements 8 lg .. 8 lg + 7
+// of the 32-element step), and the A operand the same of an x row, so both are loaded straight
+// into registers: no LDS staging, no barrier in the K loop. A workgroup owns 16 * TN columns;
+// its waves split the K range and add their sums through LDS at the end.
+//
+// tile kernel (M > 32): one 256-thread workgroup (4 waves) owns MT rows x NT columns; x and
+// weight tiles are staged through LDS (double buffered, KS elements of K per stage, rows padded
+// by 8 elements so the 16 rows one MFMA operand reads fall in distinct 16-byte bank groups).
+//
+// When the output tiles alone do not fill the GPU, the K axis is also split over workgroups:
+// FP32 partial sums go to the workspace and a reduce kernel adds them (and the residual) and
+// rounds once. Loads go through buffer resources whose extents end at the last byte of the
+// last valid row, so nothing outside the operands is ever read.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "m3_common.hpp"
+#include "m3_host.hpp"
+
+namespace m3 {
+namespace {
+
+constexpr int kStep = 32;           // K elements per MFMA
+constexpr int kOff = 0x7ffffff0;    // buffer offset past every extent: the load returns 0
+
+template <typename T> struct LinMma;
+template <> struct LinMma<__bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f4 mma(v8 a, v8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct LinMma<_Float16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f4 mma(v8 a, v8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+struct LinGeom {
+  const char* x;       // [M, K], row stride x_ld (elements)
+  const char* w;       // [N, K], row stride w_ld
+  const void* res;     // [M, N] or null, row stride r_ld
+  void* out;           // [M, N], row stride o_ld
+  float* part;         // [splits, M, N] FP32 partial sums (splits > 1)
+  const char* nw;      // [K] RMSNorm weight or null (rows kernel, splits == 1)
+  float eps;
+  int m, n, k, k_split, splits;
+  int x_ld, w_ld, r_ld, o_ld;
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t lin_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+// Bytes from the start of row 0 to the end of row rows - 1 (K elements used per row).
+__device__ __forceinline__ int64_t lin_extent(int rows, int ld, int k) {
+  return rows > 0 ? (static_cast<int64_t>(rows - 1) * ld + k) * 2 : 0;
+}
+
+// One output element: to the partial sums of this K split, or (unsplit) plus the residual,
+// rounded once into out.
+template <typename T>
+__device__ __forceinline__ void lin_emit(const LinGeom& g, int split, int m, int n, float y) {
+  if (g.splits > 1) {
+    g.part[(static_cast<int64_t>(split) * g.m + m) * g.n + n] = y;
+    return;
+  }
+  if (g.res != nullptr) {
+    y += static_cast<float>(static_cast<const T*>(g.res)[static_cast<int64_t>(m) * g.r_ld + n]);
+  }
+  static_cast<T*>(g.out)[static_cast<int64_t>(m) * g.o_ld + n] = static_cast<T>(y);
+}
+
+// ----------------------------------------------------------------------------- rows kernel
+
+// M <= 16 TM rows; workgroup (blockIdx.x, blockIdx.z) = 16 TN columns x one K split; its WAVES
+// waves take equal runs of that split's 32-element steps. Rows past M / N are clamped to the last
+// valid row (their sums are never written).
+//
+// NORM (whole K in one workgroup): x is RMS-normalised on the fly. The A operand is x * nw
+// (FP32 product, rounded once to T) and each lane also sums the squares of the x it loads; the
+// per-row sums of squares meet in LDS with the products, and each output is scaled by
+// rsqrt(sum / K + eps): sum_k (x r nw)_k w_k = r sum_k (x nw)_k w_k.
+template <typename T, int TM, int TN, int WAVES, int D, bool NORM>
+__global__ __launch_bounds__(64 * WAVES) void linear_rows_kernel(const LinGeom g) {
+  using M = LinMma<T>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int n0 = blockIdx.x * 16 * TN, split = blockIdx.z;
+  const int k_begin = split * g.k_split;
+  const int all = max(0, min(g.k, k_begin + g.k_split) - k_begin) / kStep;
+  const int per = (all + WAVES - 1) / WAVES;
+  const int s_begin = min(all, w * per);
+  const int nsteps = min(all, s_begin + per) - s_begin;
+  const int kb = k_begin + s_begin * kStep;
+
+  const int vn = min(16 * TN, g.n - n0);
+  const __amdgpu_buffer_rsrc_t rw =
+      lin_rsrc(g.w + static_cast<int64_t>(n0) * g.w_ld * 2, lin_extent(vn, g.w_ld, g.k));
+  const __amdgpu_buffer_rsrc_t rx = lin_rsrc(g.x, lin_extent(g.m, g.x_ld, g.k));
+  const __amdgpu_buffer_rsrc_t rn = lin_rsrc(g.nw, NORM ? int64_t{2} * g.k : 0);
+  int woff[TN], xoff[TM];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) woff[j] = (min(16 * j + l16, vn - 1) * g.w_ld + 8 * lg + kb) * 2;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) xoff[i] = (min(16 * i + l16, g.m - 1) * g.x_ld + 8 * lg + kb) * 2;
+  const int noff = (8 * lg + kb) * 2;
+
+  u32x4 rb[D][TN], ra[D][TM], rnw[D];
+  auto load = [&](int slot, int s) __attribute__((always_inline)) {
+    const bool live = s < nsteps;
+    if constexpr (NORM) {
+      rnw[slot] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rn, live ? noff + 2 * kStep * s : kOff, 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      rb[slot][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rw, live ? woff[j] + 2 * kStep * s : kOff, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      ra[slot][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rx, live ? xoff[i] + 2 * kStep * s : kOff, 0, 0));
+    }
+  };
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+  float ssq[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) ssq[i] = 0.f;
+  auto step = [&](int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      typename M::v8 a = __builtin_bit_cast(typename M::v8, ra[slot][i]);
+      if constexpr (NORM) {
+        const typename M::v8 nv = __builtin_bit_cast(typename M::v8, rnw[slot]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float xf = static_cast<float>(a[e]);
+          ssq[i] = fmaf(xf, xf, ssq[i]);
+          a[e] = static_cast<T>(xf * static_cast<float>(nv[e]));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        acc[i][j] = M::mma(a, __builtin_bit_cast(typename M::v8, rb[slot][j]), acc[i][j]);
+      }
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(d, d);
+  // whole groups of D steps with no exit inside (the wait counts stay exact across the back
+  // edge), then the last nsteps % D steps, which load nothing
+  const int nfull = nsteps - nsteps % D;
+  for (int s0 = 0; s0 < nfull; s0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      step(d);
+      load(d, s0 + d + D);
+      __builtin_amdgcn_sched_barrier(0);  // keep each step's loads right after its MFMAs
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) {
+    if (nfull + d < nsteps) step(d);
+  }
+
+  // lane holds rows 16 i + 4 lg + r, column n0 + 16 j + l16; the waves' sums meet in LDS (and,
+  // with NORM, the sums of squares of rows 16 i + l16, first added over the lane's 4 groups)
+  __shared__ float red[WAVES][TM * TN * 4][64];
+  __shared__ float red_ssq[NORM ? WAVES : 1][TM][16];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[w][(i * TN + j) * 4 + r][lane] = acc[i][j][r];
+    }
+    if constexpr (NORM) {
+      float v = ssq[i] + __shfl_xor(ssq[i], 16);
+      v += __shfl_xor(v, 32);
+      if (lg == 0) red_ssq[w][i][l16] = v;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < TM * TN * 256; e += 64 * WAVES) {
+    const int q = e >> 6, ln = e & 63;
+    float y = 0.f;
+#pragma unroll
+    for (int v = 0; v < WAVES; ++v) y += red[v][q][ln];
+    const int i = q / (4 * TN), j = (q >> 2) % TN, r = q & 3;
+    const int m = 16 * i + 4 * (ln >> 4) + r, n = n0 + 16 * j + (ln & 15);
+    if constexpr (NORM) {
+      float sq = 0.f;
+#pragma unroll
+      for (int v = 0; v < WAVES; ++v) sq += red_ssq[v][i][4 * (ln >> 4) + r];
+      y *= rsqrtf(sq / static_cast<float>(g.k) + g.eps);
+    }
+    if (m < g.m && n < g.n) lin_emit<T>(g, split, m, n, y);
+  }
+}
+
+// ----------------------------------------------------------------------------- tile kernel
+
+// Workgroup tile MT x NT, WM x WN waves, each wave (MT / WM) x (NT / WN) of 16x16 MFMA tiles;
+// KS elements of K per LDS stage. D stages are in flight in registers (a ring indexed statically
+// by unrolling the stage loop D times): at stage s the registers of stage s are free (already in
+// LDS) and take stage s + D.
+template <typename T, int MT, int NT, int WM, int WN, int KS, int D>
+__global__ __launch_bounds__(256) void linear_tile_kernel(const LinGeom g) {
+  using M = LinMma<T>;
+  constexpr int MW = MT / WM, NW = NT / WN, TM = MW / 16, TN = NW / 16;
+  static_assert(WM * WN == 4 && TM >= 1 && TN >= 1, "wave tiling");
+  static_assert(D % 2 == 0, "the LDS buffer of stage s is s & 1 == d & 1");
+  static_assert(KS % kStep == 0 && 512 % KS == 0, "stage width");
+  constexpr int RS = KS + 8;  // LDS row stride (elements)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int wm = w / WN, wn = w - wm * WN;
+  const int n_base = blockIdx.x * NT, m_base = blockIdx.y * MT, split = blockIdx.z;
+  const int k_begin = split * g.k_split;
+  const int nsteps = max(0, min(g.k, k_begin + g.k_split) - k_begin) / KS;
+
+  // A stage's 16-byte chunks are handed out in wave units of 64: RU = 512 / KS tile rows of
+  // KS / 8 chunks. Unit u = 4 j + wave holds x rows RU u.. when u < MT / RU, then weight rows;
+  // units past the tile are dummies. Each unit loads through its own buffer resource, built from
+  // wave-uniform values (rows past M / N and dummy units read zero).
+  constexpr int CPR = KS / 8, RU = 64 / CPR, U = (MT + NT) / RU, NCH = (U + 3) / 4;
+  static_assert(MT % RU == 0 && NT % RU == 0, "unit rows");
+  __shared__ __attribute__((aligned(16))) T sm[2][4 * NCH * RU * RS];
+  __amdgpu_buffer_rsrc_t rs[NCH];
+  int goff[NCH], loff[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int u = 4 * j + w;
+    const bool isx = u < MT / RU;
+    const int row0 = isx ? m_base + RU * u : n_base + RU * (u - MT / RU);
+    const int rows = u < U ? (isx ? g.m : g.n) : 0;
+    const int ld = isx ? g.x_ld : g.w_ld;
+    const int valid = max(0, min(RU, rows - row0));
+    rs[j] = lin_rsrc((isx ? g.x : g.w) + static_cast<int64_t>(row0) * ld * 2,
+                     lin_extent(valid, ld, g.k));
+    goff[j] = ((lane / CPR) * ld + 8 * (lane % CPR) + k_begin) * 2;
+    loff[j] = (RU * u + lane / CPR) * RS + 8 * (lane % CPR);
+  }
+  u32x4 rg[D][NCH];
+  auto load = [&](int slot, int s) __attribute__((always_inline)) {
+    const bool live = s < nsteps;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      rg[slot][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rs[j], live ? goff[j] + 2 * KS * s : kOff, 0, 0));
+    }
+  };
+  auto store = [&](int slot, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) *reinterpret_cast<u32x4*>(&sm[buf][loff[j]]) = rg[slot][j];
+  };
+
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(d, d);
+  store(0, 0);
+  __syncthreads();
+  // stage s from LDS buffer s & 1 (== d & 1, D even); then the registers of stage s + 1 go to
+  // the other buffer (past the last stage: zeros into the idle buffer)
+  auto stage = [&](int d) __attribute__((always_inline)) {
+    const T* buf = sm[d & 1];
+#pragma unroll
+    for (int kk = 0; kk < KS / kStep; ++kk) {
+      typename M::v8 av[TM], bv[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        av[i] = *reinterpret_cast<const typename M::v8*>(
+            &buf[(wm * MW + 16 * i + l16) * RS + kStep * kk + 8 * lg]);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        bv[j] = *reinterpret_cast<const typename M::v8*>(
+            &buf[(MT + wn * NW + 16 * j + l16) * RS + kStep * kk + 8 * lg]);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = M::mma(av[i], bv[j], acc[i][j]);
+      }
+    }
+    store((d + 1) % D, (d & 1) ^ 1);
+    __syncthreads();
+  };
+  // whole groups of D stages with no exit inside, then the last nsteps % D, which load nothing
+  const int nfull = nsteps - nsteps % D;
+  for (int s0 = 0; s0 < nfull; s0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      load(d, s0 + d + D);
+      stage(d);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) {
+    if (nfull + d < nsteps) stage(d);
+  }
+
+  // lane holds rows 16 i + 4 lg + r, column 16 j + l16 of its wave tile
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n_base + wn * NW + 16 * j + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m_base + wm * MW + 16 * i + 4 * lg + r;
+        if (m < g.m && n < g.n) lin_emit<T>(g, split, m, n, acc[i][j][r]);
+      }
+    }
+  }
+}
+
+// out = sum over splits of the partial sums (+ residual), rounded once; one thread per element
+template <typename T>
+__global__ __launch_bounds__(256) void linear_reduce_kernel(const LinGeom g) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= static_cast<int64_t>(g.m) * g.n) return;
+  const int m = static_cast<int>(e / g.n), n = static_cast<int>(e - static_cast<int64_t>(m) * g.n);
+  float y = 0.f;
+  for (int s = 0; s < g.splits; ++s) y += g.part[static_cast<int64_t>(s) * g.m * g.n + e];
+  if (g.res != nullptr) {
+    y += static_cast<float>(static_cast<const T*>(g.res)[static_cast<int64_t>(m) * g.r_ld + n]);
+  }
+  static_cast<T*>(g.out)[static_cast<int64_t>(m) * g.o_ld + n] = static_cast<T>(y);
+}
+
+// ----------------------------------------------------------------------------- host side
+
+// A launch: the kernel and its shape. rows kernel: cfg = TM, TN, WAVES and ring depth d; tile
+// kernel: cfg = MT, NT, KS (wave layout and ring depth follow from them).
+struct LinPlan {
+  bool rows;
+  int a, b, c, d;     // rows: TM, TN, WAVES, D; tile: MT, NT, KS
+  int gx, gy, splits, k_split;
+};
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Splits of K (each a multiple of `unit` elements) so that about `want` workgroups run.
+void split_k(LinPlan& p, int64_t k, int64_t tiles, int64_t want, int64_t unit) {
+  int64_t s = std::max<int64_t>(1, std::min<int64_t>(cdiv(want, tiles), k / unit));
+  int64_t ks = cdiv(cdiv(k, s), unit) * unit;
+  p.splits = static_cast<int>(cdiv(k, ks));
+  p.k_split = static_cast<int>(ks);
+}
+
+LinPlan plan(int64_t m, int64_t n, int64_t k, bool norm) {
+  LinPlan p{};
+  if (m <= 32) {
+    // rows kernel: 16 columns per workgroup, 4 waves splitting K. Measured on the decode shapes
+    // (N 8672 / 2048, K 2048 / 4096, cold weights), one launch that keeps K whole beats a K
+    // split plus the reduce launch from 128 workgroups up, so K is split only below 64
+    // workgroups; the ring holds 8 steps when a wave runs 32 or more, else 4.
+    p.rows = true;
+    p.a = m <= 16 ? 1 : 2;
+    p.b = 1;
+    p.c = 4;
+    p.gx = static_cast<int>(cdiv(n, 16 * p.b));
+    p.gy = 1;
+    split_k(p, k, p.gx, norm ? 1 : 64, 4 * kStep * p.c);
+    p.d = p.k_split / (kStep * p.c) >= 32 ? 8 : 4;
+    return p;
+  }
+  p.rows = false;
+  p.a = m <= 64 ? 64 : 128;
+  p.b = 64;
+  p.c = 64;
+  p.gx = static_cast<int>(cdiv(n, p.b));
+  p.gy = static_cast<int>(cdiv(m, p.a));
+  split_k(p, k, static_cast<int64_t>(p.gx) * p.gy, 256, 8 * p.c);
+  return p;
+}
+
+int validate(const m3_linear_args& a) {
+  if (a.dtype != M3_BF16 && a.dtype != M3_F16) {
+    return fail(M3_EUNSUPPORTED, "m3_linear: dtype %d is not bf16 or f16", a.dtype);
+  }
+  if (a.m <= 0 || a.n <= 0 || a.k <= 0) return fail(M3_EINVAL, "m3_linear: empty dims");
+  if (a.m > 256) return fail(M3_EUNSUPPORTED, "m3_linear: M = %lld > 256", (long long)a.m);
+  if (a.k % kStep != 0) return fail(M3_EUNSUPPORTED, "m3_linear: K %% 32 != 0");
+  int rc;
+  if ((rc = check_tensor(a.x, "x", 2, a.k, true, a.dtype)) != M3_OK) return rc;
+  if ((rc = check_tensor(a.weight, "weight", 2, a.k, true, a.dtype)) != M3_OK) return rc;
+  if ((rc = check_tensor(a.residual, "residual", 2, a.n, false, a.dtype)) != M3_OK) return rc;
+  if ((rc = check_tensor(a.norm_weight, "norm_weight", 1, a.k, false, a.dtype)) != M3_OK) {
+    return rc;
+  }
+  if (a.norm_weight.ptr != nullptr) {
+    if (a.m > 32) return fail(M3_EUNSUPPORTED, "m3_linear: norm_weight needs M <= 32");
+    if (reinterpret_cast<uintptr_t>(a.norm_weight.ptr) % 16 != 0) {
+      return fail(M3_EUNSUPPORTED, "m3_linear: norm_weight must be 16-byte aligned");
+    }
+    if (!(a.norm_eps >= 0.f)) return fail(M3_EINVAL, "m3_linear: norm_eps must be >= 0");
+  }
+  if ((rc = check_tensor(a.out, "out", 2, a.n, true, a.dtype)) != M3_OK) return rc;
+  for (const m3_tensor* t : {&a.x, &a.weight}) {
+    if (reinterpret_cast<uintptr_t>(t->ptr) % 16 != 0 || t->stride[0] % 8 != 0) {
+      return fail(M3_EUNSUPPORTED, "m3_linear: x / weight rows must be 16-byte aligned");
+    }
+  }
+  if ((a.m > 1 && a.x.stride[0] < a.k) || a.weight.stride[0] < a.k) {
+    return fail(M3_EINVAL, "m3_linear: row stride below K");
+  }
+  if ((a.m > 1 && a.out.stride[0] < a.n) ||
+      (a.m > 1 && a.residual.ptr != nullptr && a.residual.stride[0] < a.n)) {
+    return fail(M3_EINVAL, "m3_linear: out / residual row stride below N");
+  }
+  // 32-bit byte offsets: a 32-row run of x or weight, and every out / residual element
+  constexpr int64_t kLdMax = int64_t{1} << 25;
+  if (a.x.stride[0] >= kLdMax || a.weight.stride[0] >= kLdMax || a.k >= kLdMax ||
+      a.n >= INT32_MAX || a.out.stride[0] >= INT32_MAX || a.residual.stride[0] >= INT32_MAX ||
+      a.n * a.weight.stride[0] * 2 >= (int64_t{1} << 31) ||
+      a.m * a.x.stride[0] * 2 >= (int64_t{1} << 31)) {
+    return fail(M3_EUNSUPPORTED, "m3_linear: operand above 2 GiB or row stride too large");
+  }
+  return M3_OK;
+}
+
+size_t workspace_bytes(const m3_linear_args& a, const LinPlan& p) {
+  return p.splits > 1 ? static_cast<size_t>(p.splits) * a.m * a.n * sizeof(float) : 0;
+}
+
+LinGeom geometry(const m3_linear_args& a, const LinPlan& p) {
+  LinGeom g{};
+  g.x = static_cast<const char*>(a.x.ptr);
+  g.w = static_cast<const char*>(a.weight.ptr);
+  g.res = a.residual.ptr;
+  g.out = a.out.ptr;
+  g.part = static_cast<float*>(a.workspace);
+  g.nw = static_cast<const char*>(a.norm_weight.ptr);
+  g.eps = a.norm_eps;
+  g.m = static_cast<int>(a.m);
+  g.n = static_cast<int>(a.n);
+  g.k = static_cast<int>(a.k);
+  g.k_split = p.k_split;
+  g.splits = p.splits;
+  g.x_ld = static_cast<int>(a.x.stride[0]);
+  g.w_ld = static_cast<int>(a.weight.stride[0]);
+  g.r_ld = a.residual.ptr != nullptr ? static_cast<int>(a.residual.stride[0]) : 0;
+  g.o_ld = static_cast<int>(a.out.stride[0]);
+  return g;
+}
+
+template <typename T, int TM, int TN, int WAVES, int D>
+void launch_rows_d(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
+  if (g.nw != nullptr) {
+    hipLaunchKernelGGL((linear_rows_kernel<T, TM, TN, WAVES, D, true>), dim3(p.gx, 1, p.splits),
+                       dim3(64 * WAVES), 0, stream, g);
+  } else {
+    hipLaunchKernelGGL((linear_rows_kernel<T, TM, TN, WAVES, D, false>), dim3(p.gx, 1, p.splits),
+                       dim3(64 * WAVES), 0, stream, g);
+  }
+}
+
+template <typename T, int TM, int TN, int WAVES>
+void launch_rows(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
+  if (p.d == 8) {
+    launch_rows_d<T, TM, TN, WAVES, 8>(g, p, stream);
+  } else {
+    launch_rows_d<T, TM, TN, WAVES, 4>(g, p, stream);
+  }
+}
+
+template <typename T, int MT, int NT, int WM, int WN, int KS, int D>
+void launch_tile(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
+  hipLaunchKernelGGL((linear_tile_kernel<T, MT, NT, WM, WN, KS, D>), dim3(p.gx, p.gy, p.splits),
+                     dim3(256), 0, stream, g);
+}
+
+// The compiled shapes; a plan naming any other is refused.
+template <typename T>
+int launch_plan(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
+  if (p.rows) {
+    if (p.a == 1 && p.b == 1 && p.c == 4) {
+      launch_rows<T, 1, 1, 4>(g, p, stream);
+    } else if (p.a == 2 && p.b == 1 && p.c == 4) {
+      launch_rows<T, 2, 1, 4>(g, p, stream);
+    } else {
+      return fail(M3_EUNSUPPORTED, "m3_linear: no rows kernel %d/%d/%d", p.a, p.b, p.c);
+    }
+  } else if (p.a == 64 && p.b == 64 && p.c == 64) {
+    launch_tile<T, 64, 64, 2, 2, 64, 4>(g, p, stream);
+  } else if (p.a == 128 && p.b == 64 && p.c == 64) {
+    launch_tile<T, 128, 64, 2, 2, 64, 4>(g, p, stream);
+  } else {
+    return fail(M3_EUNSUPPORTED, "m3_linear: no tile kernel %d/%d/%d", p.a, p.b, p.c);
+  }
+  int rc = check_launch("m3_linear");
+  if (rc != M3_OK || p.splits == 1) return rc;
+  const int64_t total = static_cast<int64_t>(g.m) * g.n;
+  hipLaunchKernelGGL((linear_reduce_kernel<T>), dim3(static_cast<unsigned>(cdiv(total, 256))),
+                     dim3(256), 0, stream, g);
+  return check_launch("m3_linear (reduce)");
+}
+
+int run(const m3_linear_args& a, const LinPlan& p, hipStream_t stream) {
+  const size_t need = workspace_bytes(a, p);
+  if (need > 0 && (a.workspace == nullptr || a.workspace_bytes < need ||
+                   reinterpret_cast<uintptr_t>(a.workspace) % 16 != 0)) {
+    return fail(M3_EWORKSPACE, "m3_linear: needs a 16-byte aligned workspace of %zu bytes", need);
+  }
+  const LinGeom g = geometry(a, p);
+  return a.dtype == M3_BF16 ? launch_plan<__bf16>(g, p, stream)
+                            : launch_plan<_Float16>(g, p, stream);
+}
+
+}  // namespace
+}  // namespace m3
+
+extern "C" int m3_linear_workspace_size(const m3_linear_args* args, size_t* bytes) {
+  m3::clear_error();
+  if (args == nullptr || bytes == nullptr) {
+    return m3::fail(M3_EINVAL, "m3_linear_workspace_size: NULL");
+  }
+  const int rc = m3::validate(*args);
+  if (rc != M3_OK) return rc;
+  *bytes = m3::workspace_bytes(
+      *args, m3::plan(args->m, args->n, args->k, args->norm_weight.ptr != nullptr));
+  return M3_OK;
+}
+
+extern "C" int m3_linear(const m3_linear_args* args, hipStream_t stream) {
+  m3::clear_error();
+  if (args == nullptr) return m3::fail(M3_EINVAL, "m3_linear: NULL args");
+  const int rc = m3::validate(*args);
+  if (rc != M3_OK) return rc;
+  return m3::run(*args, m3::plan(args->m, args->n, args->k, args->norm_weight.ptr != nullptr),
+                 stream);
+}

@@ -6,7 +6,9 @@ differs: after the ``in_proj`` GEMM, each mixer hands the raw projection to one 
 kernel (``ops.scan_projection`` / ``ops.step_projection``). That kernel does the B/C
 RMSNorm, dt / A, the bounded phase, bias and rotation, and the chunked SSD or the
 decode step. ``in_proj`` / ``out_proj`` and the residual RMSNorm stay in torch
-(hipBLASLt).
+(hipBLASLt), except in a decode step of a small batch with 16-bit weights: there both
+projections run on ``ops.linear`` (``m3_linear``), the block's RMSNorm fused into
+``in_proj`` and its residual add into ``out_proj``.
 
 Scope: inference (``forward``, ``prefill``, ``step``, ``cuda_graph``) on ROCm devices.
 Autograd through the mixer and CPU execution raise ``RuntimeError``. ``compile`` and
@@ -210,19 +212,41 @@ class _Mamba3Mixer(nn.Module):
             raise ValueError(f"cache tensors must be on {device}")
 
     def step(self, hidden_states: torch.Tensor, cache: _LayerCache | None, *,
-             inplace: bool = False):
+             inplace: bool = False, residual: torch.Tensor | None = None,
+             norm: _RMSNorm | None = None):
+        """One decode token. ``norm`` (the block's RMSNorm) is applied to ``hidden_states``
+        first; with ``residual`` (``[batch, 1, d_model]``) the result is
+        ``residual + out_proj(...)``. For at most ``ops.DECODE_LINEAR_ROWS`` rows and 16-bit
+        weights both projections run on ``ops.linear``, the norm fused into ``in_proj`` and the
+        residual add into ``out_proj``."""
         if hidden_states.ndim != 3 or hidden_states.shape[1:] != (1, self.d_model):
             raise ValueError(
                 f"expected [batch, 1, {self.d_model}], got {tuple(hidden_states.shape)}")
         self._check_inference(hidden_states)
-        proj = self.in_proj(hidden_states)
+        rows = hidden_states[:, 0]
+        small = rows.shape[0] <= ops.DECODE_LINEAR_ROWS
+        if small and ops.linear_supported(rows, self.in_proj.weight):
+            proj = ops.linear(rows, self.in_proj.weight,
+                              norm_weight=norm.weight if norm is not None else None,
+                              norm_eps=norm.eps if norm is not None else ops.NORM_EPS)
+            proj = proj.unsqueeze(1)
+        else:
+            proj = self.in_proj(norm(hidden_states) if norm is not None else hidden_states)
         if cache is None:
             cache = self.allocate_cache(hidden_states.shape[0], device=hidden_states.device,
                                         dtype=proj.dtype)
         else:
             self._validate_cache(cache, hidden_states.shape[0])
         mixed, next_cache = ops.step_projection(proj, self, cache, inplace=inplace)
-        return self.out_proj(mixed.flatten(-2)).unsqueeze(1), next_cache
+        mixed = mixed.flatten(-2)
+        if small and ops.linear_supported(mixed, self.out_proj.weight) and (
+                residual is None or residual.dtype == mixed.dtype):
+            res = residual[:, 0] if residual is not None else None
+            return ops.linear(mixed, self.out_proj.weight, res).unsqueeze(1), next_cache
+        output = self.out_proj(mixed).unsqueeze(1)
+        if residual is not None:
+            output = residual + output
+        return output, next_cache
 
 
 class _Mamba3Block(nn.Module):
@@ -239,8 +263,8 @@ class _Mamba3Block(nn.Module):
         return hidden_states + mixed
 
     def step(self, hidden_states, cache, *, inplace: bool = False):
-        output, next_cache = self.mixer.step(self.norm(hidden_states), cache, inplace=inplace)
-        return hidden_states + output, next_cache
+        return self.mixer.step(hidden_states, cache, inplace=inplace, residual=hidden_states,
+                               norm=self.norm)
 
 
 class Mamba3(nn.Module):

@@ -455,5 +455,90 @@ def step_projection(proj: torch.Tensor, mixer, cache, *, inplace: bool = False):
     return out, nxt
 
 
+# --------------------------------------------------------------------------- decode GEMMs
+
+LINEAR_MAX_ROWS = 256
+LINEAR_NORM_MAX_ROWS = 32
+# Decode steps with at most this many rows run their projections on ``linear``; above it the
+# weights are read few enough times per row that hipBLASLt's GEMMs are as fast.
+DECODE_LINEAR_ROWS = 16
+
+
+def linear_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether ``linear(x, weight)`` takes these operands: 2-D, on one ROCm device, both
+    bfloat16 or both float16, at most ``LINEAR_MAX_ROWS`` rows, K a multiple of 32 with
+    16-byte aligned rows, no autograd, and no autocast that would compute in another dtype."""
+    if x.dim() != 2 or weight.dim() != 2 or x.shape[1] != weight.shape[1]:
+        return False
+    if x.device.type != "cuda" or weight.device != x.device:
+        return False
+    if x.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != x.dtype:
+        return False
+    if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") != x.dtype:
+        return False
+    if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad):
+        return False
+    m, k = x.shape
+    if not 0 < m <= LINEAR_MAX_ROWS or k % 32 != 0 or weight.shape[0] == 0:
+        return False
+    for t in (x, weight):
+        if t.stride(1) != 1 or t.stride(0) % 8 != 0 or t.data_ptr() % 16 != 0:
+            return False
+    return True
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor | None = None, *,
+           out: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None,
+           norm_eps: float = NORM_EPS) -> torch.Tensor:
+    """``x @ weight.T (+ residual)`` for the few rows of a decode step (``m3_linear``).
+
+    ``x`` is ``[M, K]`` (``M <= 256``), ``weight`` the ``[N, K]`` weight of an ``nn.Linear``
+    without bias, both bfloat16 or both float16 (``linear_supported``); ``residual`` and
+    ``out`` are ``[M, N]`` of that dtype. Products accumulate in FP32; the residual is added
+    to the FP32 sum, which is rounded once. With ``norm_weight`` (``[K]``, ``M <= 32``) ``x``
+    is first RMS-normalised, as ``F.rms_norm(x, (K,), norm_weight, norm_eps)``. This replaces
+    the decode step's RMSNorm, ``in_proj`` / ``out_proj`` calls and the block's residual add
+    (reference ``model.py:441-458, 514-520``).
+    """
+    device = _require_device(x, weight, residual, out, norm_weight)
+    _require_inference(x, weight, residual, norm_weight)
+    if not linear_supported(x, weight):
+        raise ValueError(
+            f"linear: unsupported operands x {tuple(x.shape)} {x.dtype} strides {x.stride()}, "
+            f"weight {tuple(weight.shape)} {weight.dtype} strides {weight.stride()}")
+    m, n = x.shape[0], weight.shape[0]
+    for name, t in (("residual", residual), ("out", out)):
+        if t is not None and (tuple(t.shape) != (m, n) or t.dtype != x.dtype):
+            raise ValueError(f"linear: {name} must be [{m}, {n}] {x.dtype}, got "
+                             f"{tuple(t.shape)} {t.dtype}")
+    if norm_weight is not None:
+        if x.shape[0] > LINEAR_NORM_MAX_ROWS:
+            raise ValueError(f"linear: norm_weight needs at most {LINEAR_NORM_MAX_ROWS} rows")
+        norm_weight = norm_weight.detach().to(x.dtype).contiguous()
+        if norm_weight.shape != (x.shape[1],):
+            raise ValueError(f"linear: norm_weight must be [{x.shape[1]}]")
+        if norm_weight.data_ptr() % 16:
+            norm_weight = norm_weight.clone()
+    residual = _inner(residual)
+    if out is None:
+        out = torch.empty(m, n, dtype=x.dtype, device=device)
+    elif out.stride(1) != 1:
+        raise ValueError("linear: out needs a unit inner stride")
+    args = _hip.LinearArgs()
+    args.m, args.n, args.k = m, n, x.shape[1]
+    args.dtype = _hip.dtype_code(x.dtype)
+    args.x = _hip.tensor(x)
+    args.weight = _hip.tensor(weight.detach())
+    args.norm_weight = _hip.tensor(norm_weight)
+    args.norm_eps = float(norm_eps)
+    args.residual = _hip.tensor(residual)
+    args.out = _hip.tensor(out)
+    ws = _hip.scan_workspace(args, device, "m3_linear_workspace_size")
+    _hip.call("m3_linear", args, device)
+    del ws
+    return out
+
+
 __all__ = ["heavy_tail_activation", "mamba3_scan", "mamba3_step", "fused_step", "chunk_state",
-           "ScanCall", "scan_projection", "step_projection", "split_projection"]
+           "ScanCall", "scan_projection", "step_projection", "split_projection", "linear",
+           "linear_supported"]

@@ -45,7 +45,8 @@ def _c_layout() -> dict[str, tuple[int, dict[str, int]]]:
     if shutil.which("gcc") is None:
         pytest.skip("gcc not available")
     structs = {"m3_tensor": _hip.Tensor, "m3_scan_args": _hip.ScanArgs,
-               "m3_step_args": _hip.StepArgs, "m3_chunk_state_args": _hip.ChunkStateArgs}
+               "m3_step_args": _hip.StepArgs, "m3_chunk_state_args": _hip.ChunkStateArgs,
+               "m3_linear_args": _hip.LinearArgs}
     lines = ['#include "mamba3_hip.h"', "#include <stdio.h>", "#include <stddef.h>",
              "int main(void) {"]
     for cname, py in structs.items():
@@ -77,7 +78,8 @@ def test_ctypes_structs_match_the_header_layout():
     layout = _c_layout()
     for cname, py in (("m3_tensor", _hip.Tensor), ("m3_scan_args", _hip.ScanArgs),
                       ("m3_step_args", _hip.StepArgs),
-                      ("m3_chunk_state_args", _hip.ChunkStateArgs)):
+                      ("m3_chunk_state_args", _hip.ChunkStateArgs),
+                      ("m3_linear_args", _hip.LinearArgs)):
         size, fields = layout[cname]
         assert ctypes.sizeof(py) == size, cname
         for field, _ in py._fields_:
@@ -85,7 +87,7 @@ def test_ctypes_structs_match_the_header_layout():
 
 
 def test_null_arguments_are_rejected_without_touching_the_device(lib):
-    for name in ("m3_scan_fwd", "m3_step", "m3_chunk_state"):
+    for name in ("m3_scan_fwd", "m3_step", "m3_chunk_state", "m3_linear"):
         rc = getattr(lib, name)(None, None)
         assert rc == 1, name
         assert b"NULL" in lib.m3_last_error()
@@ -124,3 +126,58 @@ def test_tensor_descriptor_records_pointer_dtype_and_strides():
     assert list(d.stride)[:3] == list(t.stride())
     assert list(d.stride)[3:] == [0, 0]
     assert _hip.tensor(None).ptr is None
+
+
+def _linear_args(m: int, n: int, k: int) -> _hip.LinearArgs:
+    """Argument block with fake, aligned device pointers: only host checks run on it."""
+    args = _hip.LinearArgs(m=m, n=n, k=k, dtype=_hip.BF16)
+    for name, (rows, cols, ptr) in {"x": (m, k, 0x10000), "weight": (n, k, 0x20000),
+                                    "out": (m, n, 0x30000)}.items():
+        t = getattr(args, name)
+        t.ptr, t.dtype = ptr, _hip.BF16
+        t.stride[0], t.stride[1] = cols, 1
+    return args
+
+
+def test_linear_validation_and_workspace_on_the_host(lib):
+    size = ctypes.c_size_t(0)
+    # one row against 512 x 4096: 32 column workgroups, K split in two -> two FP32 partials
+    args = _linear_args(1, 512, 4096)
+    assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 0
+    assert size.value == 2 * 1 * 512 * 4
+    # ... unless the RMSNorm is fused in, which keeps K whole in one workgroup
+    args.norm_weight.ptr, args.norm_weight.dtype, args.norm_eps = 0x40000, _hip.BF16, 1e-5
+    args.norm_weight.stride[0] = 1
+    assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 0
+    assert size.value == 0
+    # the decode shapes run unsplit: 542 / 128 column workgroups, 2 x 136 tiles of 256 rows
+    for m, n, k in ((1, 8672, 2048), (16, 2048, 4096), (256, 8672, 2048)):
+        args = _linear_args(m, n, k)
+        assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 0
+        assert size.value == 0
+    # a split call without its workspace is refused before any launch
+    args = _linear_args(1, 512, 4096)
+    assert lib.m3_linear(ctypes.byref(args), None) == 4
+    assert b"workspace" in lib.m3_last_error()
+    args = _linear_args(33, 64, 2048)
+    args.norm_weight.ptr, args.norm_weight.dtype = 0x40000, _hip.BF16
+    args.norm_weight.stride[0] = 1
+    assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 2
+    assert b"M <= 32" in lib.m3_last_error()
+    for field, value, code, text in (("m", 257, 2, b"M = 257"), ("k", 2040, 2, b"K % 32"),
+                                     ("dtype", _hip.F32, 2, b"dtype")):
+        args = _linear_args(4, 64, 2048)
+        setattr(args, field, value)
+        assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == code
+        assert text in lib.m3_last_error(), field
+    args = _linear_args(4, 64, 2048)
+    args.x.ptr = 0x10008  # 8-byte aligned rows
+    assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 2
+    assert b"16-byte aligned" in lib.m3_last_error()
+    args = _linear_args(4, 64, 2048)
+    args.out.stride[0] = 32  # rows of out overlap
+    assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 1
+    args = _linear_args(4, 64, 2048)
+    args.weight.ptr = None
+    assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 1
+    assert b"weight: required tensor is NULL" in lib.m3_last_error()
