@@ -290,6 +290,31 @@ __device__ __forceinline__ float swap16(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401f));
 }
 
+// x of another lane of the same 16-lane DPP row (ctrl: row_ror:8 = lane ^ 8, row_half_mirror =
+// lane ^ 7 within 8, quad_perm 0xb1 / 0x4e = lane ^ 1 / lane ^ 2).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                               0xf, 0xf, false));
+}
+
+// Reduce-scatter of 8 values over a 32-lane half-wave: lane c returns the sum over all 32 lanes
+// of v[(c >> 2) & 7]. Halving stages trade half the remaining values with lane c ^ 16 (bit 4),
+// c ^ 8 (bit 3) and c ^ 7 (bit 2, same bits 3-4), each lane keeping the half its bit selects;
+// the last two stages add over the quad. 9 exchanges where 8 all-reduces take 40.
+__device__ __forceinline__ float reduce_scatter8(const float (&v)[8], int c) {
+  const bool b4 = (c & 16) != 0, b3 = (c & 8) != 0, b2 = (c & 4) != 0;
+  float h4[4], h3[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) h4[i] = (b4 ? v[4 + i] : v[i]) + swap16(b4 ? v[i] : v[4 + i]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) h3[i] = (b3 ? h4[2 + i] : h4[i]) + dpp<0x128>(b3 ? h4[i] : h4[2 + i]);
+  float h = (b2 ? h3[1] : h3[0]) + dpp<0x141>(b2 ? h3[0] : h3[1]);
+  h += dpp<0xb1>(h);
+  h += dpp<0x4e>(h);
+  return h;
+}
+
 // Four consecutive activation elements (one 8-byte load for 16-bit types, 16 bytes for FP32).
 template <typename T>
 __device__ __forceinline__ f4 ld4(const void* base, int64_t i) {
@@ -343,7 +368,12 @@ __device__ __forceinline__ void st4(void* base, int64_t i, const float (&x)[4]) 
 // use. Per-row rank values and gates go through LDS behind one barrier. The readout sums over a
 // half-wave use DPP; lane c = k finishes row rg + RG k. The small cache outputs are written after a
 // final barrier, when every thread has consumed the cache inputs they may alias.
-template <typename T, int R, int RPT>
+//
+// FULL: the model's step (q / k norm weights and biases, raw dt, angle phases, MIMO rotation for
+// R > 1) with those features fixed at compile time. The prologue is then one basic block: every
+// kernel-argument and input load issues before the first wait, where a branch per optional
+// input would cost a round trip each.
+template <typename T, int R, int RPT, bool FULL>
 __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_args a) {
   constexpr int N = 128, P = 64, S = 32;
   constexpr int RG = P / RPT;  // row groups: thread rows rg + RG k, k < RPT
@@ -352,11 +382,12 @@ __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_ar
   const int b = bh / H, h = bh - b * H;
   const int g = h / (H / a.groups);
   const int tid = threadIdx.x, c = tid & 31, rg = tid >> 5, n0 = 4 * c;
-  const bool norm = a.q_norm_w.ptr != nullptr;
-  const bool bias = a.q_bias.ptr != nullptr;
-  const bool rotate = a.phase_mode != M3_PHASE_NONE;
-  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
-  const bool mimo = a.mimo_rotation != 0;
+  const bool norm = FULL || a.q_norm_w.ptr != nullptr;
+  const bool bias = FULL || a.q_bias.ptr != nullptr;
+  const bool rotate = FULL || a.phase_mode != M3_PHASE_NONE;
+  const bool angles = FULL || a.phase_mode == M3_PHASE_ANGLES;
+  const bool raw_dt = FULL || a.raw_dt != 0;
+  const bool mimo = FULL ? R > 1 : a.mimo_rotation != 0;
 
   __shared__ float s_vr[R][P], s_pvr[R][P], s_zr[R][P], s_mo[R][P];
 
@@ -378,7 +409,7 @@ __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_ar
   const RawX trap_r = ldraw(a.trap.ptr, a.trap.dtype, b * a.trap.stride[0] + h * a.trap.stride[1]);
   const RawX D_r = ldraw(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
   RawX dtb_r{0u, 0u};
-  if (a.raw_dt) dtb_r = ldraw(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]);
+  if (raw_dt) dtb_r = ldraw(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]);
   // phase roles: SISO pairs (2j, 2j+1) -> angles 2c, 2c+1 (c < 16); MIMO pairs (j, j + 2S) ->
   // angles n0 .. n0+3 for the first (c < 8) and third (16 <= c < 24) quarters
   int j0 = -1, nj = 0;
@@ -429,25 +460,36 @@ __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_ar
     px[r] = ld4<T>(a.prev_k.ptr, b * a.prev_k.stride[0] + h * a.prev_k.stride[1] +
                                      r * a.prev_k.stride[2] + n0);
   }
-  // (2) per-row rank values and gates (thread p < P), into LDS, after the loads above are issued
-  if (tid < P) {
-    const int p = tid;
-    const float v = ld_act<T>(a.value, b * a.value.stride[0] + h * a.value.stride[1] + p);
-    const float z = ld_act<T>(a.gate, b * a.gate.stride[0] + h * a.gate.stride[1] + p);
-    const float pv = ld_act<T>(a.prev_value,
-                               b * a.prev_value.stride[0] + h * a.prev_value.stride[1] + p);
+  // (2) per-row rank values and gates of row p = tid % P: every thread loads them with the batch
+  // above (no branch around loads), threads tid < P put them in LDS once decoded
+  const int pl = tid & (P - 1);
+  const float v = ld_act<T>(a.value, b * a.value.stride[0] + h * a.value.stride[1] + pl);
+  const float z = ld_act<T>(a.gate, b * a.gate.stride[0] + h * a.gate.stride[1] + pl);
+  const float pv = ld_act<T>(a.prev_value,
+                             b * a.prev_value.stride[0] + h * a.prev_value.stride[1] + pl);
+  RawX mx_r[R], mz_r[R], mo_r[R];
+  if constexpr (R > 1) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if (R > 1) {
-        const float mx = rnd<T>(ldx_nb(a.mimo_x.ptr, a.mimo_x.dtype,
-                                       h * a.mimo_x.stride[0] + r * a.mimo_x.stride[1] + p));
-        const float mz = rnd<T>(ldx_nb(a.mimo_z.ptr, a.mimo_z.dtype,
-                                       h * a.mimo_z.stride[0] + r * a.mimo_z.stride[1] + p));
+      mx_r[r] = ldraw(a.mimo_x.ptr, a.mimo_x.dtype,
+                      h * a.mimo_x.stride[0] + r * a.mimo_x.stride[1] + pl);
+      mz_r[r] = ldraw(a.mimo_z.ptr, a.mimo_z.dtype,
+                      h * a.mimo_z.stride[0] + r * a.mimo_z.stride[1] + pl);
+      mo_r[r] = ldraw(a.mimo_out.ptr, a.mimo_out.dtype,
+                      h * a.mimo_out.stride[0] + r * a.mimo_out.stride[1] + pl);
+    }
+  }
+  if (tid < P) {
+    const int p = tid;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if constexpr (R > 1) {
+        const float mx = rnd<T>(decode(mx_r[r], a.mimo_x.dtype));
+        const float mz = rnd<T>(decode(mz_r[r], a.mimo_z.dtype));
         s_vr[r][p] = mul_r<T>(v, mx);
         s_pvr[r][p] = mul_r<T>(pv, mx);
         s_zr[r][p] = mul_r<T>(z, mz);
-        s_mo[r][p] = ldx_nb(a.mimo_out.ptr, a.mimo_out.dtype,
-                            h * a.mimo_out.stride[0] + r * a.mimo_out.stride[1] + p);
+        s_mo[r][p] = decode(mo_r[r], a.mimo_out.dtype);
       } else {
         s_vr[r][p] = v;
         s_pvr[r][p] = pv;
@@ -464,7 +506,7 @@ __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_ar
 
   const float dt_in = decode(dt_r, a.dt.dtype), a_in = decode(a_r, a.a.dtype);
   const float trap_in = decode(trap_r, a.trap.dtype), Dh = decode(D_r, a.D.dtype);
-  const float dtb_in = a.raw_dt ? decode(dtb_r, a.dt_bias.dtype) : 0.f;
+  const float dtb_in = raw_dt ? decode(dtb_r, a.dt_bias.dtype) : 0.f;
   float th[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) th[i] = decode(th_r[i], a.angles.dtype);
@@ -479,7 +521,7 @@ __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_ar
 
   // per-(b, h) scalars
   float dt, adt;
-  dt_adt(a.raw_dt, dt_in, a_in, dtb_in, dt, adt);
+  dt_adt(raw_dt, dt_in, a_in, dtb_in, dt, adt);
   const float trap = sigmoidf(trap_in);
   const float alpha = expf(adt);
   const float beta = (1.f - trap) * dt * alpha;
@@ -494,7 +536,7 @@ __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_ar
       if (angles) ph = m3_fmod_2pi(__fadd_rn(old[i], phase_inc(th[i], dt)));
       phn[i] = ph;
       float sv, cv;
-      sincosf(ph, &sv, &cv);
+      __sincosf(ph, &sv, &cv);  // ph in [0, 2 pi): the hardware sine / cosine, as in the scan
       cs[i] = rnd<T>(cv);
       sn[i] = rnd<T>(sv);
     }
@@ -576,8 +618,8 @@ __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_ar
   }
   __syncthreads();  // the per-row LDS vectors
 
-  // (6) state update, readout and epilogue of rows rg + RG k
-  float yrow = 0.f;  // lane c = k keeps row rg + RG k's output
+  // (6) state update of rows rg + RG k, each lane's part of their readouts, then the readout
+  float part[RPT][R];
 #pragma unroll
   for (int k = 0; k < RPT; ++k) {
     const int p = rg + RG * k;
@@ -595,21 +637,52 @@ __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_ar
 #pragma unroll
     for (int j = 0; j < 4; ++j) ns[j] = alpha * st[k][j] + beta * po[j] + gamma * co[j];
     __builtin_nontemporal_store(ns, reinterpret_cast<f4*>(sout + p * sp_out));
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sum += rnd<T>(ns[j]) * qr[r][j];
+      part[k][r] = sum;
+    }
+  }
+  auto epilogue = [&](int p, const float (&tot)[R]) __attribute__((always_inline)) {
     float y = 0.f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      float part = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) part += rnd<T>(ns[j]) * qr[r][j];
-      part = allreduce32(part);
-      const float t = (part + Dh * s_vr[r][p]) * siluf(s_zr[r][p]);
+      const float t = (tot[r] + Dh * s_vr[r][p]) * siluf(s_zr[r][p]);
       y = R > 1 ? y + t * s_mo[r][p] : t;
     }
-    if (c == k) yrow = y;
-  }
-  if (c < RPT) {
-    const int p = rg + RG * c;
-    static_cast<T*>(a.out.ptr)[b * a.out.stride[0] + h * a.out.stride[1] + p] = from_f<T>(yrow);
+    return y;
+  };
+  if constexpr (RPT == 8) {
+    // lane c holds row rg + RG ((c >> 2) & 7); the first lane of each quad stores it
+    float tot[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = part[k][r];
+      tot[r] = reduce_scatter8(v, c);
+    }
+    const int p = rg + RG * ((c >> 2) & 7);
+    const float y = epilogue(p, tot);
+    if ((c & 3) == 0) {
+      static_cast<T*>(a.out.ptr)[b * a.out.stride[0] + h * a.out.stride[1] + p] = from_f<T>(y);
+    }
+  } else {
+    float yrow = 0.f;  // lane c = k keeps row rg + RG k's output
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      float tot[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) tot[r] = allreduce32(part[k][r]);
+      const float y = epilogue(rg + RG * k, tot);
+      if (c == k) yrow = y;
+    }
+    if (c < RPT) {
+      const int p = rg + RG * c;
+      static_cast<T*>(a.out.ptr)[b * a.out.stride[0] + h * a.out.stride[1] + p] = from_f<T>(yrow);
+    }
   }
 
   // (7) the small cache outputs, after every thread has consumed the inputs they may alias
@@ -656,31 +729,41 @@ static bool step128_ok(const m3_step_args& a) {
   return true;
 }
 
+// The model's step: norm weights, biases, raw dt with its bias, angle phases, MIMO rotation iff
+// R > 1 (the FULL form of step128_kernel).
+static bool step_full(const m3_step_args& a) {
+  return a.q_norm_w.ptr != nullptr && a.k_norm_w.ptr != nullptr && a.q_bias.ptr != nullptr &&
+         a.k_bias.ptr != nullptr && a.raw_dt != 0 && a.dt_bias.ptr != nullptr &&
+         a.phase_mode == M3_PHASE_ANGLES && a.angles.ptr != nullptr &&
+         (a.mimo_rotation != 0) == (a.rank > 1);
+}
+
+template <typename T, int R, int RPT>
+static void launch128(const m3_step_args& a, dim3 grid, dim3 block, hipStream_t stream) {
+  if (step_full(a)) {
+    hipLaunchKernelGGL((step128_kernel<T, R, RPT, true>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((step128_kernel<T, R, RPT, false>), grid, block, 0, stream, a);
+  }
+}
+
 template <typename T>
 static int launch_step(const m3_step_args& a, hipStream_t stream) {
   const size_t lds = step_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles);
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kStepThreads);
   // Ranks 1 and 2; rank 4 only below 1024 (batch, head) pairs (with many, its four readout
   // reductions per row make the LDS-staged step_kernel faster; rank 8 always uses that one).
-  // Below 1024 pairs the grid holds at most four waves per SIMD: ranks 1 and 2 take the
-  // 1024-thread form, whose per-row chain is shorter.
+  // The 256-thread form at every batch: at B = 1 its 4 waves start together, where a 1024-
+  // thread form's 16 waves start in four groups about 1400 cycles apart and its barrier waits
+  // for the last (13.1k against 18.1k cycles per workgroup, measured).
   const bool few = static_cast<int64_t>(a.batch) * a.heads < 1024;
   if ((a.rank <= 2 || (a.rank == 4 && few)) && step128_ok(a)) {
-    const dim3 wide(32 * 64 / 2);
     if (a.rank == 1) {
-      if (few) {
-        hipLaunchKernelGGL((step128_kernel<T, 1, 2>), grid, wide, 0, stream, a);
-      } else {
-        hipLaunchKernelGGL((step128_kernel<T, 1, 8>), grid, block, 0, stream, a);
-      }
+      launch128<T, 1, 8>(a, grid, block, stream);
     } else if (a.rank == 2) {
-      if (few) {
-        hipLaunchKernelGGL((step128_kernel<T, 2, 2>), grid, wide, 0, stream, a);
-      } else {
-        hipLaunchKernelGGL((step128_kernel<T, 2, 8>), grid, block, 0, stream, a);
-      }
+      launch128<T, 2, 8>(a, grid, block, stream);
     } else {
-      hipLaunchKernelGGL((step128_kernel<T, 4, 8>), grid, block, 0, stream, a);
+      launch128<T, 4, 8>(a, grid, block, stream);
     }
     return check_launch("m3_step");
   }
