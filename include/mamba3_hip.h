@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define M3_ABI_VERSION 1
+#define M3_ABI_VERSION 2
 
 /* Element types. */
 enum { M3_F32 = 0, M3_BF16 = 1, M3_F16 = 2 };
@@ -90,6 +90,7 @@ typedef struct {
   int32_t mimo_rotation;  /* 0: SISO adjacent pairs (2i, 2i+1); 1: MIMO quarters (i, 2S + i) */
   int32_t raw_dt;         /* 0: dt / a are FP32 dt / adt; 1: raw logits (see above) */
   int32_t phase_mode;     /* M3_PHASE_* */
+  int32_t segments;       /* 0: the library picks; 1: one pass per (b, h); G > 1: G segments */
   float norm_eps;
   m3_tensor q, k;                   /* [B, L, G, R, N] */
   m3_tensor q_norm_w, k_norm_w;     /* [N] optional (C_norm.weight / B_norm.weight) */
@@ -109,6 +110,9 @@ typedef struct {
   m3_tensor final_state;            /* [B, H, P, N] FP32 */
   m3_tensor final_phase;            /* [B, H, S] FP32 optional (ANGLES): phase of token L-1 */
   m3_tensor final_k;                /* [B, H, R, N] optional: biased, rotated k of token L-1 */
+  m3_tensor final_decay;            /* [B, H] FP32 optional: sum of adt over the sequence */
+  m3_tensor block_phase;            /* [B, H, ceil(L / 64), S] FP32 optional (ANGLES): the sum of
+                                       each 64-token block's bounded phase increments */
   void* workspace;                  /* device scratch, m3_scan_workspace_size() bytes */
   size_t workspace_bytes;
 } m3_scan_args;

@@ -14,7 +14,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmamba3_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, BF16, F16 = 0, 1, 2
 PHASE_NONE, PHASE_GIVEN, PHASE_ANGLES = 0, 1, 2
@@ -44,12 +44,13 @@ class ScanArgs(ctypes.Structure):
     _fields_ = [
         *[(n, ctypes.c_int32) for n in ("batch", "length", "heads", "groups", "rank", "d_state",
                                         "head_dim", "num_angles", "chunk", "act_dtype",
-                                        "mimo_rotation", "raw_dt", "phase_mode")],
+                                        "mimo_rotation", "raw_dt", "phase_mode", "segments")],
         ("norm_eps", ctypes.c_float),
         *[(n, _T) for n in ("q", "k", "q_norm_w", "k_norm_w", "q_bias", "k_bias", "value",
                             "gate", "dt", "a", "dt_bias", "trap", "phase", "initial_phase",
                             "D", "mimo_x", "mimo_z", "mimo_out", "initial_state", "initial_k",
-                            "initial_value", "out", "final_state", "final_phase", "final_k")],
+                            "initial_value", "out", "final_state", "final_phase", "final_k",
+                            "final_decay", "block_phase")],
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
     ]

@@ -614,7 +614,8 @@ __device__ __forceinline__ int cs_col(int col, int tt) {
 template <int PG, int TPL, int CST, bool SWZ, bool EXACT>
 __device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, float* poff,
                                             const float* dtv, int t0, int L, int pg, int lane,
-                                            bool angles, const float (&pa)[TPL], float* fph) {
+                                            bool angles, const float (&pa)[TPL], float* fph,
+                                            float* fblk, int64_t blk_stride) {
   float ph[TPL];
   if (angles) {
     float x[TPL];
@@ -651,6 +652,8 @@ __device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, fl
     if (pg == 0) excl = 0.f;
     float base = *pbase, off = *poff;
     if ((t0 & 63) == 0 && t0 > 0) {
+      // the block that just ended: its increment sum, when asked for (block_phase)
+      if (fblk != nullptr && pg == 0) fblk[((t0 >> 6) - 1) * blk_stride] = base;
       off = m3_fmod_2pi_small(__fadd_rn(off, base));
       base = 0.f;
     }
@@ -1075,6 +1078,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
                    ? static_cast<float*>(a.final_phase.ptr) + b * a.final_phase.stride[0] +
                          h * a.final_phase.stride[1] + ps * a.final_phase.stride[2]
                    : nullptr;
+  float* fblk = a.block_phase.ptr != nullptr
+                    ? static_cast<float*>(a.block_phase.ptr) + b * a.block_phase.stride[0] +
+                          h * a.block_phase.stride[1] + ps * a.block_phase.stride[3]
+                    : nullptr;
+  const int64_t blk_stride = a.block_phase.stride[2];
   const __amdgpu_buffer_rsrc_t rs_o =
       make_rsrc(FULL ? static_cast<char*>(a.out.ptr) + b * g.out_b : nullptr, FULL ? L * g.out_t : 0);
   T* out_row = nullptr;
@@ -1155,10 +1163,12 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     float pa[TPL];
     angles_of(pa);
     phase_stage<PG, TPL, CST, SPLIT, !SPLIT>(csb(0), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
-                                     scb(0) + SB_::DTV, 0, L, pg, lane, angles, pa, fph);
+                                     scb(0) + SB_::DTV, 0, L, pg, lane, angles, pa, fph, fblk,
+                                     blk_stride);
   }
   __syncthreads();
 
+  float log_decay = 0.f;  // sum of adt so far: the log of the state's decay over the sequence
   for (int c = 0; c < nsub; ++c) {
     const int t0 = c * TOK;
     const int width = min(TOK, L - t0);
@@ -1355,6 +1365,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     // onto it
     {
       const float ecl = SC[SB_::ECL];
+      log_decay += SC[SB_::CL];
 #pragma unroll
       for (int k = 0; k < kTiles; ++k) {
 #pragma unroll
@@ -1456,7 +1467,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       angles_of(pa);
       phase_stage<PG, TPL, CST, SPLIT, !SPLIT>(csb(c + 1), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
                                        scb(c + 1) + SB_::DTV, t0 + TOK, L, pg, lane, angles, pa,
-                                       fph);
+                                       fph, fblk, blk_stride);
     }
     if constexpr (FULL) loads_side();
     // decayed scores W[t, s] = Sc[t, s] d[t, s] in FP32
@@ -1624,6 +1635,20 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     }
   }
 
+  if (a.final_decay.ptr != nullptr && tid == 0) {
+    static_cast<float*>(a.final_decay.ptr)[b * a.final_decay.stride[0] +
+                                           h * a.final_decay.stride[1]] = log_decay;
+  }
+  // the last block's increment sum (the earlier blocks' were written as each one ended)
+  if (a.block_phase.ptr != nullptr && rotate && angles && L > 0) {
+    for (int i = tid; i < S; i += kThreads) {
+      static_cast<float*>(a.block_phase.ptr)[b * a.block_phase.stride[0] +
+                                             h * a.block_phase.stride[1] +
+                                             ((L - 1) >> 6) * a.block_phase.stride[2] +
+                                             i * a.block_phase.stride[3]] = F[Lay::PBASE + i];
+    }
+  }
+
   // ---- final state
 #pragma unroll
   for (int k = 0; k < kTiles; ++k) {
@@ -1644,6 +1669,292 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   }
 }
 
+
+// ------------------------------------------------------------ segmented scan (composition)
+
+// A sequence split into G equal segments is scanned twice (pass 1: every segment from a zero
+// state and zero phase; pass 2: every segment from its true start), both passes viewing the
+// [B, L] tensors as [B*G, L/G]. Between them, compose_kernel walks each (b, h)'s segments in
+// order. The scan is linear in its initial state and a rotation by phi + psi is the rotation by
+// psi followed by phi, so with pass 1's local end state U_g (built from k rotated by local
+// phases), log-decay l_g = sum adt and last k k_g:
+//   S_{g+1} = e^{l_g} (S_g + c_g sum_r (v_prev mx_r) k_prev_r^T) + U_g Rot(phi_g)^T,
+//   k_prev <- Rot(phi_g) k_g,  v_prev <- v at the segment's last token,
+// where c_g = dt (1 - trap) at the segment's first token (the endpoint continuation the kernel
+// applies to initial_k / initial_value). The phase carry phi is the kernel's own walk over
+// 64-token blocks, off <- fmod(off + block sum) (segments start on block boundaries), redone
+// from pass 1's block sums: bit for bit the carry the unsplit scan reaches there, the fmod
+// representative (sign) included. Pass 2 then starts segment g from (S_g, phi_g, k_prev,
+// v_prev) exactly as a prefill continued from a cache, and its last segment's final state,
+// phase and k are the call's (gather_kernel).
+struct SegGeom {
+  int G, Ls, nbs;         // segments per batch row, tokens and 64-token phase blocks per segment
+  float* seg_state;       // [B*G][H][P][N] pass-1 end states, then pass 2's
+  float* seg_decay;       // [B*G][H]
+  float* seg_blk;         // [B*G][H][nbs][S] pass 1's phase block sums (phase mode ANGLES)
+  float* seg_phase;       // [B*G][H][S] pass 2's final phases
+  void* seg_k;            // [B*G][H][R][N] last k of pass 1, then of pass 2 (activation dtype)
+  float* in_state;        // [B*G][H][P][N] pass-2 initial states
+  float* in_phase;        // [B*G][H][S]
+  void* in_k;             // [B*G][H][R][N]
+  void* in_v;             // [B*G][H][P]
+};
+
+constexpr int kCompThreads = 256;
+constexpr int kCompPer = kNPad * kPPad / kCompThreads;  // state elements per thread
+constexpr int kBlkChunk = 64;                           // phase blocks staged per round trip
+constexpr int kMaxSegments = 256;                       // bounds compose_kernel's LDS
+
+// Dynamic LDS of compose_kernel (floats): the segment start phases [G][S], a chunk of block sums
+// [kBlkChunk][S], one segment's local end state [P * N].
+static size_t compose_lds_bytes(int G, int S, int P, int N) {
+  return sizeof(float) * (static_cast<size_t>(G) * S + kBlkChunk * S + static_cast<size_t>(P) * N);
+}
+
+template <typename T, int R>
+__global__ __launch_bounds__(kCompThreads) void compose_kernel(const m3_scan_args a,
+                                                               const SegGeom sg) {
+  const int H = a.heads, N = a.d_state, P = a.head_dim, S = a.num_angles, G = sg.G;
+  const int b = blockIdx.x / H, h = blockIdx.x - b * H;
+  const int tid = threadIdx.x;
+  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
+  const bool mimo = a.mimo_rotation != 0;
+  const bool raw_dt = a.raw_dt != 0;
+  extern __shared__ float dyn[];
+  float* s_phig = dyn;                       // [G][S] phase carry at each segment's start
+  float* s_blk = dyn + G * S;                // [kBlkChunk][S]
+  float* s_U = s_blk + kBlkChunk * S;        // [P * N]
+  __shared__ float s_cs[kSMax], s_sn[kSMax];
+  __shared__ float s_kp[R * kNPad], s_vp[kPPad], s_vpm[R * kPPad];
+  __shared__ float s_c0, s_dec;
+  T* in_k = static_cast<T*>(sg.in_k);
+  T* in_v = static_cast<T*>(sg.in_v);
+  const T* seg_k = static_cast<const T*>(sg.seg_k);
+  const int PN = P * N;
+  auto row = [&](int g) { return (static_cast<int64_t>(b) * G + g) * H + h; };
+
+  // rotation partner of column n (-1: not rotated) and whether n is the pair's first element
+  auto partner = [&](int n, bool& lo, int& j) {
+    lo = true;
+    j = 0;
+    if (!angles) return -1;
+    if (!mimo) {
+      if (n >= 2 * S) return -1;
+      lo = (n & 1) == 0;
+      j = n >> 1;
+      return n ^ 1;
+    }
+    if (n < S) { j = n; return n + 2 * S; }
+    if (n >= 2 * S && n < 3 * S) { lo = false; j = n - 2 * S; return n - 2 * S; }
+    return -1;
+  };
+  auto rot = [&](float x, float xp, int part, bool lo, int j) {
+    if (part < 0) return x;
+    return lo ? x * s_cs[j] - xp * s_sn[j] : xp * s_sn[j] + x * s_cs[j];
+  };
+
+  // ---- A: the phase carry, walked through every 64-token block in order (the kernel's own
+  // recurrence off <- fmod(off + block sum)), recording each segment's starting carry. All
+  // threads stage the block sums through LDS a chunk at a time; threads s < S walk.
+  if (angles) {
+    float off = 0.f;
+    if (tid < S && a.initial_phase.ptr != nullptr) {
+      off = static_cast<const float*>(a.initial_phase.ptr)
+          [b * a.initial_phase.stride[0] + h * a.initial_phase.stride[1] +
+           tid * a.initial_phase.stride[2]];
+    }
+    for (int g = 0; g < G; ++g) {
+      if (tid < S) s_phig[g * S + tid] = off;
+      if (g == G - 1) break;  // the last segment's blocks carry into nothing pass 2 needs
+      const float* blk = sg.seg_blk + row(g) * sg.nbs * S;
+      for (int k0 = 0; k0 < sg.nbs; k0 += kBlkChunk) {
+        const int nk = min(kBlkChunk, sg.nbs - k0);
+        __syncthreads();  // the walkers are done with the previous chunk
+        for (int i = tid; i < nk * S; i += kCompThreads) s_blk[i] = blk[k0 * S + i];
+        __syncthreads();
+        if (tid < S) {
+          for (int k = 0; k < nk; ++k) off = m3_fmod_2pi_small(__fadd_rn(off, s_blk[k * S + tid]));
+        }
+      }
+    }
+  }
+
+  // ---- B: the state, segment by segment
+  float st[kCompPer];
+#pragma unroll
+  for (int i = 0; i < kCompPer; ++i) {
+    const int e = tid + kCompThreads * i, p = e / N, n = e - p * N;
+    st[i] = (e < PN && a.initial_state.ptr != nullptr)
+                ? static_cast<const float*>(a.initial_state.ptr)
+                      [b * a.initial_state.stride[0] + h * a.initial_state.stride[1] +
+                       p * a.initial_state.stride[2] + n]
+                : 0.f;
+  }
+  for (int i = tid; i < R * N; i += kCompThreads) {
+    const int r = i / N, n = i - r * N;
+    s_kp[i] = a.initial_k.ptr != nullptr
+                  ? to_f(static_cast<const T*>(a.initial_k.ptr)
+                             [b * a.initial_k.stride[0] + h * a.initial_k.stride[1] +
+                              r * a.initial_k.stride[2] + n])
+                  : 0.f;
+  }
+  for (int i = tid; i < P; i += kCompThreads) {
+    s_vp[i] = a.initial_k.ptr != nullptr
+                  ? to_f(static_cast<const T*>(a.initial_value.ptr)
+                             [b * a.initial_value.stride[0] + h * a.initial_value.stride[1] + i])
+                  : 0.f;
+  }
+  // registers of segment g's local end state and endpoint inputs, loaded one segment ahead
+  float un[kCompPer];
+  float dt_raw = 0.f, a_raw = 0.f, tr_raw = 0.f, l_raw = 0.f;
+  auto prefetch = [&](int g) __attribute__((always_inline)) {
+    const float* U = sg.seg_state + row(g) * PN;
+#pragma unroll
+    for (int i = 0; i < kCompPer; ++i) {
+      const int e = tid + kCompThreads * i;
+      un[i] = e < PN ? U[e] : 0.f;
+    }
+    if (tid == 0) {
+      const int t0 = g * sg.Ls;
+      dt_raw = ldx(a.dt.ptr, a.dt.dtype,
+                   b * a.dt.stride[0] + t0 * a.dt.stride[1] + h * a.dt.stride[2]);
+      a_raw = ldx(a.a.ptr, a.a.dtype, b * a.a.stride[0] + t0 * a.a.stride[1] + h * a.a.stride[2]);
+      tr_raw = ldx(a.trap.ptr, a.trap.dtype,
+                   b * a.trap.stride[0] + t0 * a.trap.stride[1] + h * a.trap.stride[2]);
+      l_raw = sg.seg_decay[row(g)];
+    }
+  };
+  const float dtb = raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]) : 0.f;
+  float decay_sum = 0.f;
+  prefetch(0);
+  __syncthreads();
+
+  for (int g = 0; g < G; ++g) {
+    const int64_t sh = row(g);
+    // (1) segment g's start for pass 2; cos / sin of its carry; its local state to LDS; the
+    // endpoint coefficient and the rank values of v_prev
+#pragma unroll
+    for (int i = 0; i < kCompPer; ++i) {
+      const int e = tid + kCompThreads * i;
+      if (e < PN) {
+        sg.in_state[sh * PN + e] = st[i];
+        s_U[e] = un[i];
+      }
+    }
+    for (int i = tid; i < S; i += kCompThreads) {
+      const float phi = angles ? s_phig[g * S + i] : 0.f;
+      if (angles) sg.in_phase[sh * S + i] = phi;
+      float sv, cv;
+      __sincosf(phi, &sv, &cv);
+      s_cs[i] = cv;
+      s_sn[i] = sv;
+    }
+    for (int i = tid; i < R * N; i += kCompThreads) in_k[sh * R * N + i] = from_f<T>(s_kp[i]);
+    for (int i = tid; i < P; i += kCompThreads) {
+      in_v[sh * P + i] = from_f<T>(s_vp[i]);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        s_vpm[r * kPPad + i] =
+            R > 1 ? mul_r<T>(s_vp[i], rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
+                                                 h * a.mimo_x.stride[0] +
+                                                     r * a.mimo_x.stride[1] + i)))
+                  : s_vp[i];
+      }
+    }
+    if (tid == 0) {
+      float dt0, adt0;
+      dt_adt(raw_dt, dt_raw, a_raw, dtb, dt0, adt0);
+      s_c0 = dt0 * (1.f - sigmoidf(tr_raw));
+      s_dec = expf(l_raw);
+      decay_sum += l_raw;
+    }
+    __syncthreads();
+    if (g + 1 < G) prefetch(g + 1);
+
+    // (2) the state at the segment's end: e^l (S + c0 sum_r (v_prev mx_r) k_prev_r^T) + Rot U
+    const float c0 = s_c0, dec = s_dec;
+#pragma unroll
+    for (int i = 0; i < kCompPer; ++i) {
+      const int e = tid + kCompThreads * i;
+      if (e >= PN) continue;
+      const int p = e / N, n = e - p * N;
+      float endpoint = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) endpoint += s_vpm[r * kPPad + p] * s_kp[r * N + n];
+      bool lo;
+      int j;
+      const int part = partner(n, lo, j);
+      const float u = rot(s_U[e], part >= 0 ? s_U[p * N + part] : 0.f, part, lo, j);
+      st[i] = dec * (st[i] + c0 * endpoint) + u;
+    }
+    // (3) the next segment's endpoint: this segment's last k, rotated by its carry, and value
+    float nk[(R * kNPad + kCompThreads - 1) / kCompThreads];
+#pragma unroll
+    for (int q = 0; q < (R * kNPad + kCompThreads - 1) / kCompThreads; ++q) {
+      const int i = tid + kCompThreads * q;
+      nk[q] = 0.f;
+      if (i < R * N) {
+        const int r = i / N, n = i - r * N;
+        bool lo;
+        int j;
+        const int part = partner(n, lo, j);
+        const float x = to_f(seg_k[sh * R * N + i]);
+        const float xp = part >= 0 ? to_f(seg_k[sh * R * N + r * N + part]) : 0.f;
+        nk[q] = rnd<T>(rot(x, xp, part, lo, j));
+      }
+    }
+    const int tl = g * sg.Ls + sg.Ls - 1;
+    const float nv = tid < P ? to_f(static_cast<const T*>(a.value.ptr)
+                                        [b * a.value.stride[0] + tl * a.value.stride[1] +
+                                         h * a.value.stride[2] + tid])
+                             : 0.f;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < (R * kNPad + kCompThreads - 1) / kCompThreads; ++q) {
+      const int i = tid + kCompThreads * q;
+      if (i < R * N) s_kp[i] = nk[q];
+    }
+    if (tid < P) s_vp[tid] = nv;
+    __syncthreads();
+  }
+
+  // the call's decay (its final state, phase and k come from pass 2: gather_kernel)
+  if (a.final_decay.ptr != nullptr && tid == 0) {
+    static_cast<float*>(a.final_decay.ptr)[b * a.final_decay.stride[0] +
+                                           h * a.final_decay.stride[1]] = decay_sum;
+  }
+}
+
+// The call's final state, phase and k: pass 2's of each batch row's last segment.
+template <typename T, int R>
+__global__ __launch_bounds__(kCompThreads) void gather_kernel(const m3_scan_args a,
+                                                              const SegGeom sg) {
+  const int H = a.heads, N = a.d_state, P = a.head_dim, S = a.num_angles;
+  const int b = blockIdx.x / H, h = blockIdx.x - b * H;
+  const int64_t sh = (static_cast<int64_t>(b) * sg.G + sg.G - 1) * H + h;
+  for (int e = threadIdx.x; e < P * N; e += kCompThreads) {
+    const int p = e / N, n = e - p * N;
+    static_cast<float*>(a.final_state.ptr)[b * a.final_state.stride[0] +
+                                           h * a.final_state.stride[1] +
+                                           p * a.final_state.stride[2] + n] =
+        sg.seg_state[sh * P * N + e];
+  }
+  if (a.final_phase.ptr != nullptr) {
+    for (int i = threadIdx.x; i < S; i += kCompThreads) {
+      static_cast<float*>(a.final_phase.ptr)[b * a.final_phase.stride[0] +
+                                             h * a.final_phase.stride[1] +
+                                             i * a.final_phase.stride[2]] = sg.seg_phase[sh * S + i];
+    }
+  }
+  if (a.final_k.ptr != nullptr) {
+    for (int i = threadIdx.x; i < R * N; i += kCompThreads) {
+      const int r = i / N, n = i - r * N;
+      static_cast<T*>(a.final_k.ptr)[b * a.final_k.stride[0] + h * a.final_k.stride[1] +
+                                     r * a.final_k.stride[2] + n] =
+          static_cast<const T*>(sg.seg_k)[sh * R * N + i];
+    }
+  }
+}
 
 // ------------------------------------------------------------------ host side
 
@@ -1789,8 +2100,10 @@ static int launch_kernel(const m3_scan_args& a, const ScanGeom& g, const float* 
   return check_launch("m3_scan_fwd");
 }
 
+// One pass: the prep kernel (unless `run_prep` is false: its workspace already holds this
+// geometry's results) and the scan kernel.
 template <typename T, int R>
-static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
+static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep) {
   ScanGeom g = make_geom<T>(a);
   static_assert(Layout<T>::BYTES <= 160 * 1024, "LDS layout exceeds 160 KiB");
   const float* prep = nullptr;
@@ -1809,7 +2122,7 @@ static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
       return fail(M3_EUNSUPPORTED, "m3_scan_fwd: too many tokens for one launch");
     }
     const int64_t nb_norm = (rows + 15) / 16, nb_ang = (ang + 255) / 256, nb_sc = blocks;
-    if (nb_norm + nb_ang + nb_sc > 0) {
+    if (run_prep && nb_norm + nb_ang + nb_sc > 0) {
       const dim3 pgrid(static_cast<unsigned>(nb_norm + nb_ang + nb_sc)), pblock(256);
       hipLaunchKernelGGL((prep_kernel<T, R>), pgrid, pblock, 0, stream, a, g,
                          static_cast<float*>(a.workspace), static_cast<int>(nb_norm),
@@ -1823,6 +2136,200 @@ static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
     return launch_kernel<T, R, true>(a, g, prep, grid, block, stream);
   }
   return launch_kernel<T, R, false>(a, g, prep, grid, block, stream);
+}
+
+// Sub-chunk length of a call's geometry.
+static int sub_chunk_tokens(const m3_scan_args& a) {
+  ScanGeom g{};
+  ws_layout(a, g);
+  return g.tok;
+}
+
+// Whether the [B, L] tensors can be viewed as [B*G, L/G]: each batch row of every per-token
+// tensor is its L tokens at the token stride.
+static bool segmentable(const m3_scan_args& a) {
+  const m3_tensor* ts[] = {&a.q, &a.k, &a.value, &a.gate, &a.dt, &a.a, &a.trap, &a.out};
+  for (const m3_tensor* t : ts) {
+    if (t->stride[0] != static_cast<int64_t>(a.length) * t->stride[1]) return false;
+  }
+  if (a.phase_mode != M3_PHASE_NONE &&
+      a.phase.stride[0] != static_cast<int64_t>(a.length) * a.phase.stride[1]) {
+    return false;
+  }
+  return a.head_dim <= kPPad && a.d_state <= kNPad;
+}
+
+// Segments a call's sequence is split into: 1 for none, -1 for an explicit request that cannot
+// be met. Automatic (segments == 0) when the one-workgroup-per-(b, h) grid would fill at most
+// half of the 256 CUs: the largest power of 2 G with B*H*G <= 256 that cuts L into equal
+// segments of at least 8 sub-chunks (whole 64-token phase blocks with angle phases), taken from
+// G = 4 up (the split scans the sequence twice).
+static int segments_for(const m3_scan_args& a) {
+  if (a.segments == 1 || a.length <= 0 || a.batch <= 0) return 1;
+  if (a.segments < 0) return -1;
+  if (!segmentable(a)) return a.segments > 1 ? -1 : 1;
+  const int64_t bh = static_cast<int64_t>(a.batch) * a.heads;
+  // segments start on the 64-token phase blocks (counted from the call's start)
+  const int align = a.phase_mode == M3_PHASE_ANGLES ? 64 : 1;
+  if (a.segments > 1) {
+    const bool ok = a.segments <= kMaxSegments &&
+                    a.length % (static_cast<int64_t>(a.segments) * align) == 0 &&
+                    bh * a.segments <= INT32_MAX;
+    return ok ? a.segments : -1;
+  }
+  const int tok = sub_chunk_tokens(a);
+  int G = 1;
+  while (bh * G * 2 <= 256 && a.length % (2 * G * align) == 0 &&
+         a.length / (2 * G) >= 8 * tok) {
+    G *= 2;
+  }
+  return G >= 4 ? G : 1;
+}
+
+static m3_tensor contiguous(void* p, int dtype, std::initializer_list<int64_t> dims) {
+  m3_tensor t{};
+  t.ptr = p;
+  t.dtype = dtype;
+  int64_t st = 1;
+  const int nd = static_cast<int>(dims.size());
+  for (int i = nd - 1; i >= 0; --i) {
+    t.stride[i] = st;
+    st *= dims.begin()[i];
+  }
+  return t;
+}
+
+// Pass-1 argument block (pointers into the workspace filled in at launch) and the byte offsets
+// of the segment buffers, after the prep region.
+struct SegPlan {
+  m3_scan_args a1;
+  size_t prep_bytes, total_bytes;
+  size_t o_state, o_decay, o_blk, o_phase, o_k, o_in_state, o_in_phase, o_in_k, o_in_v;
+};
+
+static SegPlan plan_segments(const m3_scan_args& a, int G) {
+  SegPlan sp{};
+  m3_scan_args& a1 = sp.a1;
+  a1 = a;
+  const int Ls = a.length / G;
+  a1.batch = a.batch * G;
+  a1.length = Ls;
+  a1.segments = 1;
+  for (m3_tensor* t : {&a1.q, &a1.k, &a1.value, &a1.gate, &a1.dt, &a1.a, &a1.trap, &a1.out}) {
+    t->stride[0] = t->stride[1] * Ls;
+  }
+  if (a.phase_mode != M3_PHASE_NONE) a1.phase.stride[0] = a1.phase.stride[1] * Ls;
+  a1.initial_state = m3_tensor{};
+  a1.initial_phase = m3_tensor{};
+  a1.initial_k = m3_tensor{};
+  a1.initial_value = m3_tensor{};
+  ScanGeom g1{};
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  sp.prep_bytes = up(ws_layout(a1, g1));
+  const size_t es = a.act_dtype == M3_F32 ? 4 : 2;
+  const size_t rows = static_cast<size_t>(a1.batch) * a.heads;
+  size_t off = sp.prep_bytes;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += up(bytes);
+    return o;
+  };
+  const size_t PN = static_cast<size_t>(a.head_dim) * a.d_state;
+  sp.o_state = take(rows * PN * 4);
+  sp.o_decay = take(rows * 4);
+  sp.o_blk = take(rows * ((a1.length + 63) / 64) * a.num_angles * 4);
+  sp.o_phase = take(rows * a.num_angles * 4);
+  sp.o_k = take(rows * a.rank * a.d_state * es);
+  sp.o_in_state = take(rows * PN * 4);
+  sp.o_in_phase = take(rows * a.num_angles * 4);
+  sp.o_in_k = take(rows * a.rank * a.d_state * es);
+  sp.o_in_v = take(rows * a.head_dim * es);
+  sp.total_bytes = off;
+  return sp;
+}
+
+// The segmented scan: pass 1 (prep + scan of every segment from zero), the composition, pass 2
+// (scan of every segment from its true start; prep's results are the same and are reused).
+template <typename T, int R>
+static int launch_segmented(const m3_scan_args& a, int G, hipStream_t stream) {
+  SegPlan sp = plan_segments(a, G);
+  if (a.workspace == nullptr || a.workspace_bytes < sp.total_bytes || !aligned16(a.workspace)) {
+    return fail(M3_EWORKSPACE, "m3_scan_fwd: needs a 16-byte aligned workspace of %zu bytes",
+                sp.total_bytes);
+  }
+  char* ws = static_cast<char*>(a.workspace);
+  const int64_t BG = sp.a1.batch, H = a.heads, P = a.head_dim, N = a.d_state, S = a.num_angles;
+  const bool angles = a.phase_mode == M3_PHASE_ANGLES;
+  SegGeom sg{};
+  sg.G = G;
+  sg.Ls = sp.a1.length;
+  sg.nbs = (sg.Ls + 63) / 64;
+  sg.seg_state = reinterpret_cast<float*>(ws + sp.o_state);
+  sg.seg_decay = reinterpret_cast<float*>(ws + sp.o_decay);
+  sg.seg_blk = reinterpret_cast<float*>(ws + sp.o_blk);
+  sg.seg_phase = reinterpret_cast<float*>(ws + sp.o_phase);
+  sg.seg_k = ws + sp.o_k;
+  sg.in_state = reinterpret_cast<float*>(ws + sp.o_in_state);
+  sg.in_phase = reinterpret_cast<float*>(ws + sp.o_in_phase);
+  sg.in_k = ws + sp.o_in_k;
+  sg.in_v = ws + sp.o_in_v;
+
+  m3_scan_args a1 = sp.a1;
+  a1.workspace = ws;
+  a1.workspace_bytes = sp.prep_bytes;
+  a1.final_state = contiguous(sg.seg_state, M3_F32, {BG, H, P, N});
+  a1.final_decay = contiguous(sg.seg_decay, M3_F32, {BG, H});
+  a1.final_phase = m3_tensor{};
+  a1.block_phase = angles ? contiguous(sg.seg_blk, M3_F32, {BG, H, sg.nbs, S}) : m3_tensor{};
+  a1.final_k = contiguous(sg.seg_k, a.act_dtype, {BG, H, R, N});
+  int rc = launch_pass<T, R>(a1, stream, true);
+  if (rc != M3_OK) return rc;
+
+  const size_t clds = compose_lds_bytes(G, S, P, N);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&compose_kernel<T, R>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(compose_lds_bytes(kMaxSegments, kSMax,
+                                                                          kPPad, kNPad)));
+    if (e != hipSuccess) {
+      return fail(M3_ELAUNCH, "m3_scan_fwd: hipFuncSetAttribute: %s", hipGetErrorString(e));
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((compose_kernel<T, R>), dim3(static_cast<unsigned>(a.batch) * a.heads),
+                     dim3(kCompThreads), clds, stream, a, sg);
+  rc = check_launch("m3_scan_fwd (compose)");
+  if (rc != M3_OK) return rc;
+
+  m3_scan_args a2 = a1;
+  a2.initial_state = contiguous(sg.in_state, M3_F32, {BG, H, P, N});
+  a2.initial_phase = angles ? contiguous(sg.in_phase, M3_F32, {BG, H, S}) : m3_tensor{};
+  a2.initial_k = contiguous(sg.in_k, a.act_dtype, {BG, H, R, N});
+  a2.initial_value = contiguous(sg.in_v, a.act_dtype, {BG, H, P});
+  a2.final_state = a1.final_state;
+  a2.final_phase = angles ? contiguous(sg.seg_phase, M3_F32, {BG, H, S}) : m3_tensor{};
+  a2.final_k = a1.final_k;
+  a2.final_decay = m3_tensor{};
+  a2.block_phase = m3_tensor{};
+  rc = launch_pass<T, R>(a2, stream, false);
+  if (rc != M3_OK) return rc;
+  hipLaunchKernelGGL((gather_kernel<T, R>), dim3(static_cast<unsigned>(a.batch) * a.heads),
+                     dim3(kCompThreads), 0, stream, a, sg);
+  return check_launch("m3_scan_fwd (gather)");
+}
+
+template <typename T, int R>
+static int launch_scan_r(const m3_scan_args& a, hipStream_t stream) {
+  const int G = segments_for(a);
+  if (G < 0) {
+    return fail(M3_EUNSUPPORTED,
+                "m3_scan_fwd: %d segments need 1 < segments <= 256 dividing L into whole "
+                "64-token blocks (angle phases), and token-major batch rows",
+                a.segments);
+  }
+  if (G > 1) return launch_segmented<T, R>(a, G, stream);
+  return launch_pass<T, R>(a, stream, true);
 }
 
 template <typename T>
@@ -1891,6 +2398,8 @@ static int validate_scan(const m3_scan_args& a) {
       (rc = check_tensor(a.out, "out", 4, P, true, act)) ||
       (rc = check_tensor(a.final_state, "final_state", 4, N, true, M3_F32)) ||
       (rc = check_tensor(a.final_phase, "final_phase", 3, 1, false, M3_F32)) ||
+      (rc = check_tensor(a.final_decay, "final_decay", 2, 1, false, M3_F32)) ||
+      (rc = check_tensor(a.block_phase, "block_phase", 4, 1, false, M3_F32)) ||
       (rc = check_tensor(a.final_k, "final_k", 4, N, false, act))) {
     return rc;
   }
@@ -1911,8 +2420,8 @@ static int validate_scan(const m3_scan_args& a) {
       static_cast<int64_t>(a.length) * a.phase.stride[1] >= lim) {
     return fail(M3_EUNSUPPORTED, "m3_scan_fwd: a batch row of phase exceeds 2^31 elements");
   }
-  if (a.final_phase.ptr != nullptr && !angles) {
-    return fail(M3_EINVAL, "m3_scan_fwd: final_phase needs phase_mode ANGLES");
+  if ((a.final_phase.ptr != nullptr || a.block_phase.ptr != nullptr) && !angles) {
+    return fail(M3_EINVAL, "m3_scan_fwd: final_phase / block_phase need phase_mode ANGLES");
   }
   return M3_OK;
 }
@@ -1925,7 +2434,8 @@ extern "C" int m3_scan_workspace_size(const m3_scan_args* args, size_t* bytes) {
     return m3::fail(M3_EINVAL, "m3_scan_workspace_size: NULL argument");
   }
   m3::ScanGeom g{};
-  *bytes = m3::ws_layout(*args, g);
+  const int G = m3::segments_for(*args);
+  *bytes = G > 1 ? m3::plan_segments(*args, G).total_bytes : m3::ws_layout(*args, g);
   return M3_OK;
 }
 

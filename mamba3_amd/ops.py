@@ -22,6 +22,10 @@ from . import _hip
 _HIP_LAST_DISPATCH = False
 _HIP_LAST_SCAN_DISPATCH = False
 NORM_EPS = 1e-5
+# Sequence segments of a scan call: 0 lets the library split long sequences of few (batch,
+# head) pairs over more workgroups (two passes and a composition of the segment states); 1 never
+# splits; G > 1 asks for G equal segments.
+SCAN_SEGMENTS = 0
 
 
 def heavy_tail_activation(x: torch.Tensor) -> torch.Tensor:
@@ -172,7 +176,8 @@ def mamba3_scan(q, k, value, gate, adt, dt, trap_logits, D, *, mimo_x=None, mimo
         batch=batch, length=length, heads=heads, groups=groups, rank=rank, d_state=d_state,
         head_dim=head_dim, num_angles=num_angles, chunk=chunk_size,
         act_dtype=_hip.dtype_code(q.dtype), mimo_rotation=int(bool(mimo_rotation)), raw_dt=0,
-        phase_mode=_hip.PHASE_NONE if phase is None else _hip.PHASE_GIVEN, norm_eps=NORM_EPS)
+        phase_mode=_hip.PHASE_NONE if phase is None else _hip.PHASE_GIVEN, norm_eps=NORM_EPS,
+        segments=SCAN_SEGMENTS)
     keep = [_inner(q), _inner(k), _inner(value), _inner(gate), adt.float(), dt.float(),
             trap_logits, None if phase is None else phase.float(), _param(D), _param(mimo_x),
             _param(mimo_z), _param(mimo_out), _param(q_bias), _param(k_bias), state_in,
@@ -391,7 +396,7 @@ class ScanCall:
             batch=batch, length=length, heads=h, groups=1, rank=r, d_state=n, head_dim=p,
             num_angles=s, chunk=chunk_size, act_dtype=_hip.dtype_code(act),
             mimo_rotation=int(r > 1), raw_dt=1, phase_mode=_hip.PHASE_ANGLES,
-            norm_eps=NORM_EPS)
+            norm_eps=NORM_EPS, segments=SCAN_SEGMENTS)
         params = [_param(t) for t in (mixer.C_norm.weight, mixer.B_norm.weight, mixer.C_bias,
                                       mixer.B_bias, mixer.dt_bias, mixer.D, mixer.mimo_x,
                                       mixer.mimo_z, mixer.mimo_out)]

@@ -1,0 +1,147 @@
+"""The segmented scan: a long sequence of few (batch, head) pairs split into G segments.
+
+``m3_scan_fwd`` scans every segment from a zero state and phase, composes the segment states in
+order (decay, endpoint term, rotation by the segment's phase offset), then rescans every segment
+from its true start. Checked against the oracle and against the unsplit scan on the same inputs:
+FP32 within 1e-4 (abs and rel); 16-bit outputs within 2e-2 of the output scale. The split forms
+FP32 sums in another order, so split and unsplit agree to FP32 rounding, not bitwise.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from mamba3_amd import Mamba3, ops
+from oracle import portable as op
+from test_gpu_scan import _inputs
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+F32 = dict(rtol=1e-4, atol=1e-4)
+
+
+@pytest.fixture
+def segments(monkeypatch):
+    def set_segments(g: int) -> None:
+        monkeypatch.setattr(ops, "SCAN_SEGMENTS", g)
+    return set_segments
+
+
+def _scan(inp, chunk):
+    dev = {n: (t.to(DEV) if isinstance(t, torch.Tensor) else t) for n, t in inp.items()}
+    with torch.inference_mode():
+        y, s = ops.mamba3_scan(**dev, chunk_size=chunk)
+    assert ops._HIP_LAST_SCAN_DISPATCH
+    return y.cpu(), s.cpu()
+
+
+def _scale_close(got, want, tol=2e-2):
+    scale = want.abs().max().item()
+    err = (got.float() - want.float()).abs().max().item()
+    assert err <= tol * scale, f"max |d| {err:.3e} > {tol} x scale {scale:.3e}"
+
+
+@pytest.mark.parametrize("rank", [1, 4])
+@pytest.mark.parametrize("phase,initial", [(True, True), (False, False), (True, False)])
+@pytest.mark.parametrize("segs", [2, 4, 8])
+def test_fp32_split_matches_unsplit_and_oracle(rank, phase, initial, segs, segments):
+    inp = _inputs(rank, torch.float32, batch=2, length=1024, heads=2, seed=40 + segs,
+                  phase=phase, initial=initial)
+    chunk = 32 // rank
+    segments(1)
+    y1, s1 = _scan(inp, chunk)
+    segments(segs)
+    y2, s2 = _scan(inp, chunk)
+    torch.testing.assert_close(y2, y1, **F32)
+    torch.testing.assert_close(s2, s1, **F32)
+    y_ref, s_ref = op.ssd_scan(**inp, chunk_size=chunk)
+    torch.testing.assert_close(y2, y_ref, **F32)
+    torch.testing.assert_close(s2, s_ref, **F32)
+
+
+@pytest.mark.parametrize("rank", [1, 4])
+def test_bf16_split_matches_unsplit(rank, segments):
+    inp = _inputs(rank, torch.bfloat16, batch=1, length=2048, heads=3, seed=50 + rank)
+    chunk = 64 // rank
+    segments(1)
+    y1, s1 = _scan(inp, chunk)
+    segments(8)
+    y2, s2 = _scan(inp, chunk)
+    _scale_close(y2, y1)
+    _scale_close(s2, s1)
+    y_ref, s_ref = op.ssd_scan(**inp, chunk_size=chunk)
+    _scale_close(y2, y_ref)
+
+
+def test_explicit_segments_must_divide_the_length(segments):
+    inp = _inputs(1, torch.float32, batch=1, length=1000, heads=2, seed=3)
+    segments(3)
+    with pytest.raises(ops._hip.HipError, match="segments"):
+        _scan(inp, 32)
+
+
+def _model(rank, seed):
+    torch.manual_seed(seed)
+    model = Mamba3(128, d_state=128, depth=1, mimo_rank=rank).eval()
+    params = {k: v.detach().clone() for k, v in model.state_dict().items()}
+    return model.to(DEV), params, op.Dims(128, 128, rank)
+
+
+def _workspace_bytes(model, x):
+    mixer = model.layers[0].mixer
+    with torch.inference_mode():
+        proj = mixer.in_proj(model.layers[0].norm(x))
+        call = ops.ScanCall(proj, mixer)
+    ws = call._keep[-1]
+    return 0 if ws is None else ws.numel()
+
+
+@pytest.mark.parametrize("rank", [1, 4])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_model_auto_split_matches_oracle(rank, bf16, segments):
+    """B = 1 with 4 heads leaves most CUs idle: the library splits the 4096 tokens on its own
+    (the workspace grows by the segment buffers), and forward and prefill still match."""
+    model, params, dims = _model(rank, seed=60 + rank)
+    torch.manual_seed(61)
+    x = torch.randn(1, 4096, 128)
+    xd = x.to(DEV)
+    segments(1)
+    unsplit = _workspace_bytes(model, xd)
+    segments(0)
+    assert _workspace_bytes(model, xd) > unsplit
+    ctx_cpu = torch.autocast("cpu", dtype=torch.bfloat16, enabled=bf16)
+    ctx_gpu = torch.autocast("cuda", dtype=torch.bfloat16, enabled=bf16)
+    with torch.inference_mode(), ctx_cpu:
+        want = op.model_forward(params, x, dims)
+        _, want_cache = op.model_prefill(params, x, dims)
+    with torch.inference_mode(), ctx_gpu:
+        got = model(xd)
+        _, cache = model.prefill(xd)
+    if bf16:
+        _scale_close(got.cpu(), want)
+        for g, w in zip(cache[0], want_cache[0]):
+            _scale_close(g.cpu(), w)
+    else:
+        torch.testing.assert_close(got.cpu(), want, **F32)
+        for g, w in zip(cache[0], want_cache[0]):
+            torch.testing.assert_close(g.cpu().float(), w.float(), **F32)
+
+
+def test_split_scan_continues_from_a_cache(segments):
+    """A split mixer scan continued from the cache of a split scan of the first half equals one
+    unsplit scan of the whole sequence (outputs and every cache tensor)."""
+    model, _, _ = _model(1, seed=70)
+    torch.manual_seed(71)
+    x = torch.randn(1, 4096, 128, device=DEV)
+    with torch.inference_mode():
+        mixer = model.layers[0].mixer
+        h = model.layers[0].norm(x)
+        segments(1)
+        full, full_cache = mixer(h, return_cache=True)
+        segments(0)
+        first, cache = mixer(h[:, :2048], return_cache=True)
+        second, cache2 = mixer(h[:, 2048:], cache=cache, return_cache=True)
+    torch.testing.assert_close(torch.cat((first, second), 1), full, **F32)
+    for a, b in zip(cache2, full_cache):
+        torch.testing.assert_close(a, b, **F32)
