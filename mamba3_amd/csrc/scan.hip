@@ -1701,56 +1701,66 @@ struct SegGeom {
 };
 
 constexpr int kCompThreads = 256;
-constexpr int kCompPer = kNPad * kPPad / kCompThreads;  // state elements per thread
-constexpr int kBlkChunk = 64;                           // phase blocks staged per round trip
+constexpr int kCompRows = 8;                              // state rows per workgroup
+constexpr int kCompPer = kCompRows * kNPad / kCompThreads;  // state elements per thread
+constexpr int kBlkChunk = 256;                          // phase blocks staged per round trip
 constexpr int kMaxSegments = 256;                       // bounds compose_kernel's LDS
 
-// Dynamic LDS of compose_kernel (floats): the segment start phases [G][S], a chunk of block sums
-// [kBlkChunk][S], one segment's local end state [P * N].
-static size_t compose_lds_bytes(int G, int S, int P, int N) {
-  return sizeof(float) * (static_cast<size_t>(G) * S + kBlkChunk * S + static_cast<size_t>(P) * N);
+// Dynamic LDS of compose_kernel (floats): per segment the carry, its cos and sin [3][G][S], the
+// endpoint coefficient and decay [2][G], a chunk of block sums [kBlkChunk][S], the workgroup's
+// rows of one segment's local end state [kCompRows * N].
+static size_t compose_lds_bytes(int G, int S, int N) {
+  return sizeof(float) * (static_cast<size_t>(3) * G * S + 2 * G + kBlkChunk * S +
+                          static_cast<size_t>(kCompRows) * N);
 }
 
+// One workgroup per (batch, head, group of kCompRows state rows): the rows are independent in the
+// composition (rotations pair columns within a row, the endpoint term is an outer product).
 template <typename T, int R>
 __global__ __launch_bounds__(kCompThreads) void compose_kernel(const m3_scan_args a,
                                                                const SegGeom sg) {
   const int H = a.heads, N = a.d_state, P = a.head_dim, S = a.num_angles, G = sg.G;
-  const int b = blockIdx.x / H, h = blockIdx.x - b * H;
+  const int nrg = (P + kCompRows - 1) / kCompRows;  // row groups per (b, h)
+  const int bh = blockIdx.x / nrg, rg = blockIdx.x - bh * nrg;
+  const int b = bh / H, h = bh - b * H;
+  const int p0 = rg * kCompRows, np = min(kCompRows, P - p0);
   const int tid = threadIdx.x;
   const bool angles = a.phase_mode == M3_PHASE_ANGLES;
   const bool mimo = a.mimo_rotation != 0;
   const bool raw_dt = a.raw_dt != 0;
+  const bool lead = rg == 0;  // writes the per-(b, h) outputs: phases, k, decay
   extern __shared__ float dyn[];
   float* s_phig = dyn;                       // [G][S] phase carry at each segment's start
-  float* s_blk = dyn + G * S;                // [kBlkChunk][S]
-  float* s_U = s_blk + kBlkChunk * S;        // [P * N]
-  __shared__ float s_cs[kSMax], s_sn[kSMax];
-  __shared__ float s_kp[R * kNPad], s_vp[kPPad], s_vpm[R * kPPad];
-  __shared__ float s_c0, s_dec;
+  float* s_csg = s_phig + G * S;             // [G][S] its cos
+  float* s_sng = s_csg + G * S;              // [G][S] its sin
+  float* s_c0g = s_sng + G * S;              // [G] endpoint coefficient dt (1 - trap)
+  float* s_decg = s_c0g + G;                 // [G] e^{sum adt}
+  float* s_blk = s_decg + G;                 // [kBlkChunk][S]
+  float* s_U = s_blk + kBlkChunk * S;        // [kCompRows * N]
+  __shared__ float s_kp[R * kNPad], s_vpm[R * kCompRows], s_vp[kCompRows];
   T* in_k = static_cast<T*>(sg.in_k);
   T* in_v = static_cast<T*>(sg.in_v);
   const T* seg_k = static_cast<const T*>(sg.seg_k);
-  const int PN = P * N;
+  const int lgN = 31 - __builtin_clz(N);  // d_state is a power of 2: element e = (p << lgN) | n
+  const int RN = np << lgN;               // this workgroup's state elements
   auto row = [&](int g) { return (static_cast<int64_t>(b) * G + g) * H + h; };
 
-  // rotation partner of column n (-1: not rotated) and whether n is the pair's first element
-  auto partner = [&](int n, bool& lo, int& j) {
-    lo = true;
-    j = 0;
-    if (!angles) return -1;
+  // rotation partner of column n (-1: not rotated), whether n is the pair's first element, and
+  // the pair's angle: SISO pairs (2j, 2j+1), j < S; MIMO pairs (j, j + 2S), j < S
+  const int S2 = 2 * S;
+  auto partner = [&](int n, bool& lo, int& j) __attribute__((always_inline)) {
     if (!mimo) {
-      if (n >= 2 * S) return -1;
       lo = (n & 1) == 0;
       j = n >> 1;
-      return n ^ 1;
+      return (angles && n < S2) ? (n ^ 1) : -1;
     }
-    if (n < S) { j = n; return n + 2 * S; }
-    if (n >= 2 * S && n < 3 * S) { lo = false; j = n - 2 * S; return n - 2 * S; }
-    return -1;
+    lo = n < S2;
+    j = lo ? n : n - S2;
+    return (angles && j < S) ? (lo ? n + S2 : j) : -1;
   };
-  auto rot = [&](float x, float xp, int part, bool lo, int j) {
+  auto rot = [&](float x, float xp, int part, bool lo, float c, float sn) {
     if (part < 0) return x;
-    return lo ? x * s_cs[j] - xp * s_sn[j] : xp * s_sn[j] + x * s_cs[j];
+    return lo ? x * c - xp * sn : xp * sn + x * c;
   };
 
   // ---- A: the phase carry, walked through every 64-token block in order (the kernel's own
@@ -1770,156 +1780,196 @@ __global__ __launch_bounds__(kCompThreads) void compose_kernel(const m3_scan_arg
       for (int k0 = 0; k0 < sg.nbs; k0 += kBlkChunk) {
         const int nk = min(kBlkChunk, sg.nbs - k0);
         __syncthreads();  // the walkers are done with the previous chunk
-        for (int i = tid; i < nk * S; i += kCompThreads) s_blk[i] = blk[k0 * S + i];
+        if ((S & 3) == 0) {  // whole float4s (16-byte aligned: the buffer rows are S floats)
+          for (int i = 4 * tid; i < nk * S; i += 4 * kCompThreads) {
+            *reinterpret_cast<float4*>(s_blk + i) =
+                *reinterpret_cast<const float4*>(blk + k0 * S + i);
+          }
+        } else {
+          for (int i = tid; i < nk * S; i += kCompThreads) s_blk[i] = blk[k0 * S + i];
+        }
         __syncthreads();
         if (tid < S) {
-          for (int k = 0; k < nk; ++k) off = m3_fmod_2pi_small(__fadd_rn(off, s_blk[k * S + tid]));
+          // the block sums do not depend on the carry: read 8 ahead of the fmod chain
+          int k = 0;
+          for (; k + 8 <= nk; k += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = s_blk[(k + u) * S + tid];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) off = m3_fmod_2pi_small(__fadd_rn(off, v[u]));
+          }
+          for (; k < nk; ++k) off = m3_fmod_2pi_small(__fadd_rn(off, s_blk[k * S + tid]));
         }
       }
     }
   }
+  __syncthreads();
+  // per segment, in parallel: cos / sin of the carry, the endpoint coefficient, the decay
+  for (int i = tid; i < G * S; i += kCompThreads) {
+    float sv, cv;
+    __sincosf(angles ? s_phig[i] : 0.f, &sv, &cv);
+    s_csg[i] = cv;
+    s_sng[i] = sv;
+  }
+  float decay_sum = 0.f;
+  {
+    const float dtb = raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]) : 0.f;
+    for (int g = tid; g < G; g += kCompThreads) {
+      const int t0 = g * sg.Ls;
+      float dt0, adt0;
+      dt_adt(raw_dt, ldx(a.dt.ptr, a.dt.dtype,
+                         b * a.dt.stride[0] + t0 * a.dt.stride[1] + h * a.dt.stride[2]),
+             ldx(a.a.ptr, a.a.dtype, b * a.a.stride[0] + t0 * a.a.stride[1] + h * a.a.stride[2]),
+             dtb, dt0, adt0);
+      s_c0g[g] = dt0 * (1.f - sigmoidf(ldx(a.trap.ptr, a.trap.dtype,
+                                           b * a.trap.stride[0] + t0 * a.trap.stride[1] +
+                                               h * a.trap.stride[2])));
+      s_decg[g] = expf(sg.seg_decay[row(g)]);
+    }
+    if (lead && tid == 0) {
+      for (int g = 0; g < G; ++g) decay_sum += sg.seg_decay[row(g)];
+    }
+  }
 
-  // ---- B: the state, segment by segment
+  // ---- B: this workgroup's state rows, segment by segment
   float st[kCompPer];
 #pragma unroll
   for (int i = 0; i < kCompPer; ++i) {
-    const int e = tid + kCompThreads * i, p = e / N, n = e - p * N;
-    st[i] = (e < PN && a.initial_state.ptr != nullptr)
+    const int e = tid + kCompThreads * i, p = p0 + (e >> lgN), n = e & (N - 1);
+    st[i] = (e < RN && a.initial_state.ptr != nullptr)
                 ? static_cast<const float*>(a.initial_state.ptr)
                       [b * a.initial_state.stride[0] + h * a.initial_state.stride[1] +
                        p * a.initial_state.stride[2] + n]
                 : 0.f;
   }
   for (int i = tid; i < R * N; i += kCompThreads) {
-    const int r = i / N, n = i - r * N;
+    const int r = i >> lgN, n = i & (N - 1);
     s_kp[i] = a.initial_k.ptr != nullptr
                   ? to_f(static_cast<const T*>(a.initial_k.ptr)
                              [b * a.initial_k.stride[0] + h * a.initial_k.stride[1] +
                               r * a.initial_k.stride[2] + n])
                   : 0.f;
   }
-  for (int i = tid; i < P; i += kCompThreads) {
-    s_vp[i] = a.initial_k.ptr != nullptr
-                  ? to_f(static_cast<const T*>(a.initial_value.ptr)
-                             [b * a.initial_value.stride[0] + h * a.initial_value.stride[1] + i])
-                  : 0.f;
+  if (tid < np) {
+    s_vp[tid] = a.initial_k.ptr != nullptr
+                    ? to_f(static_cast<const T*>(a.initial_value.ptr)
+                               [b * a.initial_value.stride[0] + h * a.initial_value.stride[1] +
+                                p0 + tid])
+                    : 0.f;
   }
-  // registers of segment g's local end state and endpoint inputs, loaded one segment ahead
-  float un[kCompPer];
-  float dt_raw = 0.f, a_raw = 0.f, tr_raw = 0.f, l_raw = 0.f;
+  // registers of segment g's local end state (this workgroup's rows), last k and the value of
+  // its last token, loaded one segment ahead
+  constexpr int KQ = (R * kNPad + kCompThreads - 1) / kCompThreads;
+  float un[kCompPer], kx[KQ], kxp[KQ], vlast = 0.f;
   auto prefetch = [&](int g) __attribute__((always_inline)) {
-    const float* U = sg.seg_state + row(g) * PN;
+    const int64_t sh = row(g);
+    const float* U = sg.seg_state + (sh * P + p0) * N;
 #pragma unroll
     for (int i = 0; i < kCompPer; ++i) {
       const int e = tid + kCompThreads * i;
-      un[i] = e < PN ? U[e] : 0.f;
+      un[i] = e < RN ? U[e] : 0.f;
     }
-    if (tid == 0) {
-      const int t0 = g * sg.Ls;
-      dt_raw = ldx(a.dt.ptr, a.dt.dtype,
-                   b * a.dt.stride[0] + t0 * a.dt.stride[1] + h * a.dt.stride[2]);
-      a_raw = ldx(a.a.ptr, a.a.dtype, b * a.a.stride[0] + t0 * a.a.stride[1] + h * a.a.stride[2]);
-      tr_raw = ldx(a.trap.ptr, a.trap.dtype,
-                   b * a.trap.stride[0] + t0 * a.trap.stride[1] + h * a.trap.stride[2]);
-      l_raw = sg.seg_decay[row(g)];
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) {
+      const int i = min(tid + kCompThreads * q, R * N - 1);
+      const int r = i >> lgN, n = i & (N - 1);
+      bool lo;
+      int j;
+      const int part = partner(n, lo, j);
+      kx[q] = to_f(seg_k[sh * R * N + i]);
+      kxp[q] = to_f(seg_k[sh * R * N + r * N + (part >= 0 ? part : n)]);
     }
+    const int tl = g * sg.Ls + sg.Ls - 1;
+    vlast = to_f(static_cast<const T*>(a.value.ptr)[b * a.value.stride[0] +
+                                                    tl * a.value.stride[1] +
+                                                    h * a.value.stride[2] + p0 +
+                                                    min(tid, np - 1)]);
   };
-  const float dtb = raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]) : 0.f;
-  float decay_sum = 0.f;
   prefetch(0);
   __syncthreads();
 
   for (int g = 0; g < G; ++g) {
     const int64_t sh = row(g);
-    // (1) segment g's start for pass 2; cos / sin of its carry; its local state to LDS; the
-    // endpoint coefficient and the rank values of v_prev
+    const float* csg = s_csg + g * S;
+    const float* sng = s_sng + g * S;
+    // (1) segment g's start for pass 2; its local state rows to LDS; the rank values of v_prev
 #pragma unroll
     for (int i = 0; i < kCompPer; ++i) {
       const int e = tid + kCompThreads * i;
-      if (e < PN) {
-        sg.in_state[sh * PN + e] = st[i];
+      if (e < RN) {
+        sg.in_state[(sh * P + p0) * N + e] = st[i];
         s_U[e] = un[i];
       }
     }
-    for (int i = tid; i < S; i += kCompThreads) {
-      const float phi = angles ? s_phig[g * S + i] : 0.f;
-      if (angles) sg.in_phase[sh * S + i] = phi;
-      float sv, cv;
-      __sincosf(phi, &sv, &cv);
-      s_cs[i] = cv;
-      s_sn[i] = sv;
+    if (lead) {
+      if (angles) {
+        for (int i = tid; i < S; i += kCompThreads) sg.in_phase[sh * S + i] = s_phig[g * S + i];
+      }
+      for (int i = tid; i < R * N; i += kCompThreads) in_k[sh * R * N + i] = from_f<T>(s_kp[i]);
     }
-    for (int i = tid; i < R * N; i += kCompThreads) in_k[sh * R * N + i] = from_f<T>(s_kp[i]);
-    for (int i = tid; i < P; i += kCompThreads) {
-      in_v[sh * P + i] = from_f<T>(s_vp[i]);
+    if (tid < np) {
+      in_v[sh * P + p0 + tid] = from_f<T>(s_vp[tid]);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        s_vpm[r * kPPad + i] =
-            R > 1 ? mul_r<T>(s_vp[i], rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
-                                                 h * a.mimo_x.stride[0] +
-                                                     r * a.mimo_x.stride[1] + i)))
-                  : s_vp[i];
+        s_vpm[r * kCompRows + tid] =
+            R > 1 ? mul_r<T>(s_vp[tid], rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
+                                                   h * a.mimo_x.stride[0] +
+                                                       r * a.mimo_x.stride[1] + p0 + tid)))
+                  : s_vp[tid];
       }
     }
-    if (tid == 0) {
-      float dt0, adt0;
-      dt_adt(raw_dt, dt_raw, a_raw, dtb, dt0, adt0);
-      s_c0 = dt0 * (1.f - sigmoidf(tr_raw));
-      s_dec = expf(l_raw);
-      decay_sum += l_raw;
+    float kx_c[KQ], kxp_c[KQ];
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) {
+      kx_c[q] = kx[q];
+      kxp_c[q] = kxp[q];
     }
+    const float nv = vlast;
     __syncthreads();
     if (g + 1 < G) prefetch(g + 1);
 
     // (2) the state at the segment's end: e^l (S + c0 sum_r (v_prev mx_r) k_prev_r^T) + Rot U
-    const float c0 = s_c0, dec = s_dec;
+    const float c0 = s_c0g[g], dec = s_decg[g];
 #pragma unroll
     for (int i = 0; i < kCompPer; ++i) {
       const int e = tid + kCompThreads * i;
-      if (e >= PN) continue;
-      const int p = e / N, n = e - p * N;
+      if (e >= RN) continue;
+      const int pl = e >> lgN, n = e & (N - 1);
       float endpoint = 0.f;
 #pragma unroll
-      for (int r = 0; r < R; ++r) endpoint += s_vpm[r * kPPad + p] * s_kp[r * N + n];
+      for (int r = 0; r < R; ++r) endpoint += s_vpm[r * kCompRows + pl] * s_kp[(r << lgN) + n];
       bool lo;
       int j;
       const int part = partner(n, lo, j);
-      const float u = rot(s_U[e], part >= 0 ? s_U[p * N + part] : 0.f, part, lo, j);
+      const float u = part >= 0 ? rot(s_U[e], s_U[(pl << lgN) + part], part, lo, csg[j], sng[j])
+                                : s_U[e];
       st[i] = dec * (st[i] + c0 * endpoint) + u;
     }
     // (3) the next segment's endpoint: this segment's last k, rotated by its carry, and value
-    float nk[(R * kNPad + kCompThreads - 1) / kCompThreads];
+    float nk[KQ];
 #pragma unroll
-    for (int q = 0; q < (R * kNPad + kCompThreads - 1) / kCompThreads; ++q) {
+    for (int q = 0; q < KQ; ++q) {
       const int i = tid + kCompThreads * q;
-      nk[q] = 0.f;
-      if (i < R * N) {
-        const int r = i / N, n = i - r * N;
-        bool lo;
-        int j;
-        const int part = partner(n, lo, j);
-        const float x = to_f(seg_k[sh * R * N + i]);
-        const float xp = part >= 0 ? to_f(seg_k[sh * R * N + r * N + part]) : 0.f;
-        nk[q] = rnd<T>(rot(x, xp, part, lo, j));
-      }
+      const int n = i & (N - 1);
+      bool lo;
+      int j;
+      const int part = i < R * N ? partner(n, lo, j) : -1;
+      nk[q] = part >= 0 ? rnd<T>(rot(kx_c[q], kxp_c[q], part, lo, csg[j], sng[j]))
+                        : rnd<T>(kx_c[q]);
     }
-    const int tl = g * sg.Ls + sg.Ls - 1;
-    const float nv = tid < P ? to_f(static_cast<const T*>(a.value.ptr)
-                                        [b * a.value.stride[0] + tl * a.value.stride[1] +
-                                         h * a.value.stride[2] + tid])
-                             : 0.f;
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < (R * kNPad + kCompThreads - 1) / kCompThreads; ++q) {
+    for (int q = 0; q < KQ; ++q) {
       const int i = tid + kCompThreads * q;
       if (i < R * N) s_kp[i] = nk[q];
     }
-    if (tid < P) s_vp[tid] = nv;
+    if (tid < np) s_vp[tid] = nv;
     __syncthreads();
   }
 
   // the call's decay (its final state, phase and k come from pass 2: gather_kernel)
-  if (a.final_decay.ptr != nullptr && tid == 0) {
+  if (lead && a.final_decay.ptr != nullptr && tid == 0) {
     static_cast<float*>(a.final_decay.ptr)[b * a.final_decay.stride[0] +
                                            h * a.final_decay.stride[1]] = decay_sum;
   }
@@ -2285,19 +2335,21 @@ static int launch_segmented(const m3_scan_args& a, int G, hipStream_t stream) {
   int rc = launch_pass<T, R>(a1, stream, true);
   if (rc != M3_OK) return rc;
 
-  const size_t clds = compose_lds_bytes(G, S, P, N);
+  const size_t clds = compose_lds_bytes(G, S, N);
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&compose_kernel<T, R>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(compose_lds_bytes(kMaxSegments, kSMax,
-                                                                          kPPad, kNPad)));
+                                                                          kNPad)));
     if (e != hipSuccess) {
       return fail(M3_ELAUNCH, "m3_scan_fwd: hipFuncSetAttribute: %s", hipGetErrorString(e));
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((compose_kernel<T, R>), dim3(static_cast<unsigned>(a.batch) * a.heads),
+  const unsigned row_groups = static_cast<unsigned>((P + kCompRows - 1) / kCompRows);
+  hipLaunchKernelGGL((compose_kernel<T, R>),
+                     dim3(static_cast<unsigned>(a.batch) * a.heads * row_groups),
                      dim3(kCompThreads), clds, stream, a, sg);
   rc = check_launch("m3_scan_fwd (compose)");
   if (rc != M3_OK) return rc;
