@@ -147,6 +147,10 @@ struct ScanGeom {
   const char* proj;
   int64_t proj_b, out_b;
   int tok_b, o_q, o_k, o_v, o_z, o_dt, o_a, o_tr, qk_g, qk_r, vz_h, sc_h, out_t, out_h;
+  // the output's physical start and the offset of logical token 0 from it (non-zero when the
+  // call runs backwards: token strides < 0, logical token t at physical token L - 1 - t)
+  const char* out_base;
+  int out_o0;
 };
 
 __device__ __forceinline__ f4 zero4() {
@@ -431,7 +435,7 @@ struct Feed {
     const int nrow = (q2 - scw) >> 1;  // norm word: row of the sub-chunk (token nrow / R)
     if constexpr (FULL) {
       tok_b = g.tok_b;
-      rs_p = make_rsrc(g.proj + b * g.proj_b, L * tok_b);
+      rs_p = make_rsrc(g.proj + b * g.proj_b, L * (tok_b < 0 ? -tok_b : tok_b));
       rs_w = make_rsrc(prep, g.ws_bytes);
       o_qk = g.o_q + grp * g.qk_g + r0 * g.qk_r + tt0 * tok_b + n0 * ES;
       o_vz = g.o_v + h * g.vz_h + 2 * vp * tok_b + p0 * ES;
@@ -1084,12 +1088,13 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
                     : nullptr;
   const int64_t blk_stride = a.block_phase.stride[2];
   const __amdgpu_buffer_rsrc_t rs_o =
-      make_rsrc(FULL ? static_cast<char*>(a.out.ptr) + b * g.out_b : nullptr, FULL ? L * g.out_t : 0);
+      make_rsrc(FULL ? const_cast<char*>(g.out_base) + b * g.out_b : nullptr,
+                FULL ? L * (g.out_t < 0 ? -g.out_t : g.out_t) : 0);
   T* out_row = nullptr;
   int out_t = 0, o_out = 0;
   if constexpr (FULL) {
     out_t = g.out_t;
-    o_out = h * g.out_h;
+    o_out = h * g.out_h + g.out_o0;
   } else {
     out_row = static_cast<T*>(a.out.ptr) + b * a.out.stride[0] + h * a.out.stride[2];
     out_t = static_cast<int>(a.out.stride[1]);
@@ -2079,7 +2084,8 @@ static bool projection_form(const m3_scan_args& a, ScanGeom& g, int es) {
   }
   if (a.a.stride[2] != a.dt.stride[2] || a.trap.stride[2] != a.dt.stride[2]) return false;
   const int64_t lim = INT32_MAX;
-  const int64_t tok = a.q.stride[1] * es;
+  const bool rev = a.q.stride[1] < 0;  // every per-token tensor runs the same way (validated)
+  const int64_t tok = (rev ? -a.q.stride[1] : a.q.stride[1]) * es;
   const int64_t ext_q = ((a.groups - 1) * a.q.stride[2] + (a.rank - 1) * a.q.stride[3] +
                          a.d_state) * es;
   const int64_t ext_v = ((a.heads - 1) * a.value.stride[2] + a.head_dim) * es;
@@ -2092,7 +2098,7 @@ static bool projection_form(const m3_scan_args& a, ScanGeom& g, int es) {
     off[i] = static_cast<const char*>(ts[i]->ptr) - base;
     if (off[i] + ext[i] > tok) return false;
   }
-  const int64_t out_tok = a.out.stride[1] * es;
+  const int64_t out_tok = (rev ? -a.out.stride[1] : a.out.stride[1]) * es;
   if (((a.heads - 1) * a.out.stride[2] + a.head_dim) * es > out_tok) return false;
   const int64_t len = a.length;
   if (len * tok >= lim || len * out_tok >= lim || len * a.groups * a.rank * 8 >= lim ||
@@ -2100,23 +2106,28 @@ static bool projection_form(const m3_scan_args& a, ScanGeom& g, int es) {
       static_cast<int64_t>(g.nsub) * g.scw * 4 >= lim) {
     return false;
   }
-  g.proj = base;
+  // backwards: the slices' pointers address logical token 0, the physical row L - 1; the buffer
+  // starts at physical row 0 and logical token t sits (L - 1 - t) rows above it
+  const int64_t shift = rev ? (len - 1) * tok : 0;
+  g.proj = base - shift;
   g.proj_b = a.q.stride[0] * es;
-  g.tok_b = static_cast<int>(tok);
-  g.o_q = static_cast<int>(off[0]);
-  g.o_k = static_cast<int>(off[1]);
-  g.o_v = static_cast<int>(off[2]);
-  g.o_z = static_cast<int>(off[3]);
-  g.o_dt = static_cast<int>(off[4]);
-  g.o_a = static_cast<int>(off[5]);
-  g.o_tr = static_cast<int>(off[6]);
+  g.tok_b = static_cast<int>(rev ? -tok : tok);
+  g.o_q = static_cast<int>(off[0] + shift);
+  g.o_k = static_cast<int>(off[1] + shift);
+  g.o_v = static_cast<int>(off[2] + shift);
+  g.o_z = static_cast<int>(off[3] + shift);
+  g.o_dt = static_cast<int>(off[4] + shift);
+  g.o_a = static_cast<int>(off[5] + shift);
+  g.o_tr = static_cast<int>(off[6] + shift);
   g.qk_g = static_cast<int>(a.q.stride[2] * es);
   g.qk_r = static_cast<int>(a.q.stride[3] * es);
   g.vz_h = static_cast<int>(a.value.stride[2] * es);
   g.sc_h = static_cast<int>(a.dt.stride[2] * es);
   g.out_b = a.out.stride[0] * es;
-  g.out_t = static_cast<int>(out_tok);
+  g.out_t = static_cast<int>(rev ? -out_tok : out_tok);
   g.out_h = static_cast<int>(a.out.stride[2] * es);
+  g.out_o0 = static_cast<int>(rev ? (len - 1) * out_tok : 0);
+  g.out_base = static_cast<const char*>(a.out.ptr) - g.out_o0;
   return true;
 }
 
@@ -2198,11 +2209,13 @@ static int sub_chunk_tokens(const m3_scan_args& a) {
 // Whether the [B, L] tensors can be viewed as [B*G, L/G]: each batch row of every per-token
 // tensor is its L tokens at the token stride.
 static bool segmentable(const m3_scan_args& a) {
+  // one batch row: its stride never matters (also for a call running backwards)
+  const bool one = a.batch == 1;
   const m3_tensor* ts[] = {&a.q, &a.k, &a.value, &a.gate, &a.dt, &a.a, &a.trap, &a.out};
   for (const m3_tensor* t : ts) {
-    if (t->stride[0] != static_cast<int64_t>(a.length) * t->stride[1]) return false;
+    if (!one && t->stride[0] != static_cast<int64_t>(a.length) * t->stride[1]) return false;
   }
-  if (a.phase_mode != M3_PHASE_NONE &&
+  if (!one && a.phase_mode != M3_PHASE_NONE &&
       a.phase.stride[0] != static_cast<int64_t>(a.length) * a.phase.stride[1]) {
     return false;
   }
@@ -2396,6 +2409,16 @@ static int launch_scan(const m3_scan_args& a, hipStream_t stream) {
 
 static bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
+// A per-token tensor may run backwards (stride[1] < 0: token t at ptr + t * stride[1]; the
+// reverse direction of a bidirectional layer reads the forward projection this way); the
+// other checks see the forward stride.
+static int check_token_tensor(const m3_tensor& t, const char* name, int dims, int64_t inner,
+                              bool required, int dtype) {
+  m3_tensor f = t;
+  if (f.stride[1] < 0) f.stride[1] = -f.stride[1];
+  return check_tensor(f, name, dims, inner, required, dtype);
+}
+
 static int validate_scan(const m3_scan_args& a) {
   if (a.batch < 0 || a.length < 0 || a.heads <= 0 || a.groups <= 0 || a.rank <= 0 ||
       a.d_state <= 0 || a.head_dim <= 0 || a.num_angles < 0) {
@@ -2424,20 +2447,21 @@ static int validate_scan(const m3_scan_args& a) {
   const int act = a.act_dtype, N = a.d_state, P = a.head_dim;
   const bool angles = a.phase_mode == M3_PHASE_ANGLES;
   int rc;
-  if ((rc = check_tensor(a.q, "q", 5, N, true, act)) ||
-      (rc = check_tensor(a.k, "k", 5, N, true, act)) ||
+  if ((rc = check_token_tensor(a.q, "q", 5, N, true, act)) ||
+      (rc = check_token_tensor(a.k, "k", 5, N, true, act)) ||
       (rc = check_tensor(a.q_norm_w, "q_norm_w", 1, N, false, -1)) ||
       (rc = check_tensor(a.k_norm_w, "k_norm_w", 1, N, a.q_norm_w.ptr != nullptr, -1)) ||
       (rc = check_tensor(a.q_bias, "q_bias", 3, N, false, -1)) ||
       (rc = check_tensor(a.k_bias, "k_bias", 3, N, a.q_bias.ptr != nullptr, -1)) ||
-      (rc = check_tensor(a.value, "value", 4, P, true, act)) ||
-      (rc = check_tensor(a.gate, "gate", 4, P, true, act)) ||
-      (rc = check_tensor(a.dt, "dt", 3, 1, true, -1)) ||
-      (rc = check_tensor(a.a, "a", 3, 1, true, -1)) ||
+      (rc = check_token_tensor(a.value, "value", 4, P, true, act)) ||
+      (rc = check_token_tensor(a.gate, "gate", 4, P, true, act)) ||
+      (rc = check_token_tensor(a.dt, "dt", 3, 1, true, -1)) ||
+      (rc = check_token_tensor(a.a, "a", 3, 1, true, -1)) ||
       (rc = check_tensor(a.dt_bias, "dt_bias", 1, 1, a.raw_dt != 0, -1)) ||
-      (rc = check_tensor(a.trap, "trap", 3, 1, true, -1)) ||
-      (rc = check_tensor(a.phase, "phase", angles ? 3 : 4, 1, a.phase_mode != M3_PHASE_NONE,
-                         a.phase_mode == M3_PHASE_GIVEN ? M3_F32 : -1)) ||
+      (rc = check_token_tensor(a.trap, "trap", 3, 1, true, -1)) ||
+      (rc = check_token_tensor(a.phase, "phase", angles ? 3 : 4, 1,
+                               a.phase_mode != M3_PHASE_NONE,
+                               a.phase_mode == M3_PHASE_GIVEN ? M3_F32 : -1)) ||
       (rc = check_tensor(a.initial_phase, "initial_phase", 3, 1, false, M3_F32)) ||
       (rc = check_tensor(a.D, "D", 1, 1, true, -1)) ||
       (rc = check_tensor(a.mimo_x, "mimo_x", 3, P, a.rank > 1, -1)) ||
@@ -2447,7 +2471,7 @@ static int validate_scan(const m3_scan_args& a) {
       (rc = check_tensor(a.initial_k, "initial_k", 4, N, false, act)) ||
       (rc = check_tensor(a.initial_value, "initial_value", 3, P, a.initial_k.ptr != nullptr,
                          act)) ||
-      (rc = check_tensor(a.out, "out", 4, P, true, act)) ||
+      (rc = check_token_tensor(a.out, "out", 4, P, true, act)) ||
       (rc = check_tensor(a.final_state, "final_state", 4, N, true, M3_F32)) ||
       (rc = check_tensor(a.final_phase, "final_phase", 3, 1, false, M3_F32)) ||
       (rc = check_tensor(a.final_decay, "final_decay", 2, 1, false, M3_F32)) ||
@@ -2469,8 +2493,19 @@ static int validate_scan(const m3_scan_args& a) {
     }
   }
   if (a.phase_mode != M3_PHASE_NONE &&
-      static_cast<int64_t>(a.length) * a.phase.stride[1] >= lim) {
+      static_cast<int64_t>(a.length) * (a.phase.stride[1] < 0 ? -a.phase.stride[1]
+                                                               : a.phase.stride[1]) >= lim) {
     return fail(M3_EUNSUPPORTED, "m3_scan_fwd: a batch row of phase exceeds 2^31 elements");
+  }
+  if (a.length > 1) {
+    const bool back = a.q.stride[1] < 0;
+    const m3_tensor* ts[] = {&a.k, &a.value, &a.gate, &a.dt, &a.a, &a.trap, &a.out};
+    bool same = true;
+    for (const m3_tensor* t : ts) same = same && ((t->stride[1] < 0) == back);
+    if (a.phase_mode != M3_PHASE_NONE) same = same && ((a.phase.stride[1] < 0) == back);
+    if (!same) {
+      return fail(M3_EINVAL, "m3_scan_fwd: per-token tensors must all run the same way");
+    }
   }
   if ((a.final_phase.ptr != nullptr || a.block_phase.ptr != nullptr) && !angles) {
     return fail(M3_EINVAL, "m3_scan_fwd: final_phase / block_phase need phase_mode ANGLES");

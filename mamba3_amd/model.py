@@ -172,10 +172,13 @@ class _Mamba3Mixer(nn.Module):
             last_value = proj[:, -1, self.d_inner:2 * self.d_inner].unflatten(
                 -1, (self.nheads, self.headdim)).clone()
             return output, (final_phase, state, final_k, last_value)
-        # Bidirectional (model.py:330-362): the reversed sequence with the same weights.
-        proj_r = self.in_proj(torch.flip(hidden_states, dims=(1,)))
-        mixed_r, _, _, _ = ops.scan_projection(proj_r, self, chunk_size=self._chunk())
-        backward = self.out_proj(torch.flip(mixed_r, dims=(1,)).flatten(-2))
+        # Bidirectional (model.py:330-362): the reversed sequence with the same weights. The
+        # projection is per token, so in_proj(flip(x)) = flip(in_proj(x)): the reverse scan reads
+        # this projection backwards and writes its output back in forward order (no flip, no
+        # second projection).
+        mixed_r, _, _, _ = ops.scan_projection(proj, self, chunk_size=self._chunk(),
+                                               reverse=True)
+        backward = self.out_proj(mixed_r.flatten(-2))
         blend = torch.sigmoid(self.direction_logit).to(dtype=output.dtype)
         return output * blend + backward * (1.0 - blend)
 

@@ -363,6 +363,15 @@ def split_projection(proj: torch.Tensor, mixer) -> dict[str, torch.Tensor]:
         dt=ddt, a=da, trap=trap, angles=ang, lead=lead)
 
 
+def _backwards(desc: _hip.Tensor, length: int) -> None:
+    """Make a per-token descriptor run backwards: token t at the old token L - 1 - t."""
+    if desc.ptr is None or length <= 1:
+        return
+    size = 4 if desc.dtype == _hip.F32 else 2
+    desc.ptr += (length - 1) * desc.stride[1] * size
+    desc.stride[1] = -desc.stride[1]
+
+
 class ScanCall:
     """One ``m3_scan_fwd`` launch over the raw ``in_proj`` output ``[B, L, proj]``, prepared once.
 
@@ -370,10 +379,16 @@ class ScanCall:
     block points at; ``launch()`` enqueues the call on the device's current stream and may be
     repeated (each launch rewrites the outputs). Fuses ``_project`` (B/C RMSNorm, dt, adt),
     ``_phase``, bias, rotation and the chunked SSD (reference ``model.py:282-309``).
+
+    ``reverse=True`` scans the sequence from its last token to its first, reading ``proj`` and
+    writing ``out`` through backwards token strides: ``out`` then holds, in forward order,
+    what scanning ``flip(proj)`` and flipping the result back gives (the reverse direction of
+    a bidirectional layer, reference ``model.py:330-362``, without either flip or a second
+    projection).
     """
 
     def __init__(self, proj: torch.Tensor, mixer, *, cache=None, want_cache: bool = False,
-                 chunk_size: int = 256):
+                 chunk_size: int = 256, reverse: bool = False):
         self.device = _require_device(proj)
         v = split_projection(proj, mixer)
         batch, length = proj.shape[0], proj.shape[1]
@@ -411,6 +426,12 @@ class ScanCall:
         args.final_state = _hip.tensor(self.final_state)
         args.final_phase = _hip.tensor(self.final_phase)
         args.final_k = _hip.tensor(self.final_k)
+        if reverse:
+            if cache is not None or want_cache:
+                raise ValueError("a reverse scan has no cache")
+            for desc in (args.q, args.k, args.value, args.gate, args.dt, args.a, args.trap,
+                         args.phase, args.out):
+                _backwards(desc, length)
         with torch.cuda.device(dev):
             keep.append(_hip.scan_workspace(args, dev))
         self.args = args
@@ -425,14 +446,15 @@ class ScanCall:
 
 
 def scan_projection(proj: torch.Tensor, mixer, *, cache=None, want_cache: bool = False,
-                    chunk_size: int = 256):
+                    chunk_size: int = 256, reverse: bool = False):
     """The whole mixer scan from the raw ``in_proj`` output ``[B, L, proj]``.
 
     Fuses ``_project`` (B/C RMSNorm, dt, adt), ``_phase``, bias, rotation and the chunked
     SSD (reference ``model.py:282-309``). Returns ``(mixed [B,L,H,P], state, final_phase,
-    final_k)``; the last two are ``None`` unless ``want_cache``.
+    final_k)``; the last two are ``None`` unless ``want_cache``. ``reverse``: see ``ScanCall``.
     """
-    call = ScanCall(proj, mixer, cache=cache, want_cache=want_cache, chunk_size=chunk_size)
+    call = ScanCall(proj, mixer, cache=cache, want_cache=want_cache, chunk_size=chunk_size,
+                    reverse=reverse)
     call.launch()
     return call.out, call.final_state, call.final_phase, call.final_k
 
