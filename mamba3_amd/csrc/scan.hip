@@ -884,7 +884,11 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
   }
 }
 
-template <typename T, int R, bool FULL>
+// SO (state only, with FULL): the segmented scan's first pass, which needs the end state, log
+// decay, last k and phase block sums but no outputs. The stores of Qs, VR, ZR, Sb and the output
+// are left out, and with them (dead code) the q math, the scores, the decay weights, the intra
+// and inter products and the epilogue; k, the carry tiles and products and the phase remain.
+template <typename T, int R, bool FULL, bool SO = false>
 __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, const ScanGeom g,
                                                         const float* __restrict__ prep) {
   using M = Mma<T>;
@@ -1255,7 +1259,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
             k[i] = fmaf(kp[i], ss, k[i] * cc);
           }
         }
-        st_row8<T>(Qs + row * LQ + n0, q);
+        if constexpr (!SO) st_row8<T>(Qs + row * LQ + n0, q);
         st_row8<T>(Ks + row * LQ + n0, k);
 #pragma unroll
         for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
@@ -1307,6 +1311,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
+          if constexpr (SO) break;
           *reinterpret_cast<u32x2*>(VR + (2 * vp + j) * LP + p0) = (u32x2){rv[j][0], rv[j][1]};
           *reinterpret_cast<u32x2*>(ZR + (2 * vp + j) * LP + p0) = (u32x2){rz[j][0], rz[j][1]};
         }
@@ -1318,6 +1323,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
+          if constexpr (SO) break;
           f4 vq, zq;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -1339,8 +1345,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
               vq[i] = mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p0 + i]);
               zq[i] = mul_r<T>(z[j][i], F[Lay::MZ + r * kPPad + p0 + i]);
             }
-            st_quad<T>(VR + row * LP + p0, vq);
-            st_quad<T>(ZR + row * LP + p0, zq);
+            if constexpr (!SO) {
+              st_quad<T>(VR + row * LP + p0, vq);
+              st_quad<T>(ZR + row * LP + p0, zq);
+            }
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -1361,7 +1369,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) {
       const int u = w + kWaves * k;
-      if (all_tiles || u < n_tiles) {
+      if (!SO && (all_tiles || u < n_tiles)) {
         const int ni = u / kPT, pj = u - ni * kPT;
         st_quad<T>(Sb + (16 * pj + l16) * LQ + 16 * ni + 4 * lg, st[k]);
       }
@@ -1413,7 +1421,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     const int tq = trow / R;
     // 16-bit: the query rows of this tile, B operand of the scores and A operand of inter
     typename M::v8 qv[F32 ? 1 : NP / 32];
-    if constexpr (!F32) {
+    if constexpr (!F32 && !SO) {
 #pragma unroll
       for (int kk = 0; kk < NP / 32; ++kk) {
         qv[kk] = *reinterpret_cast<const typename M::v8*>(Qs + trow * LQ + 32 * kk + 8 * lg);
@@ -1424,7 +1432,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
     for (int sj = 0; sj < RT; ++sj) {
       acc[sj] = zero4();
-      if (sj > it) continue;
+      if (SO || sj > it) continue;
       if constexpr (!F32) {
 #pragma unroll
         for (int kk = 0; kk < NP / 32; ++kk) {
@@ -1475,6 +1483,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
                                        fph, fblk, blk_stride);
     }
     if constexpr (FULL) loads_side();
+    if constexpr (SO) {
+      __syncthreads();
+      continue;
+    }
     // decayed scores W[t, s] = Sc[t, s] d[t, s] in FP32
     const float cum_t = SC[SB_::CUM + tq];
     const float gam_t = SC[SB_::GAM + tq];
@@ -2143,12 +2155,12 @@ static bool full_shape(const m3_scan_args& a, ScanGeom& g, int R) {
          g.vec_vz && projection_form(a, g, a.act_dtype == M3_F32 ? 4 : 2);
 }
 
-template <typename T, int R, bool FULL>
+template <typename T, int R, bool FULL, bool SO = false>
 static int launch_kernel(const m3_scan_args& a, const ScanGeom& g, const float* prep, dim3 grid,
                          dim3 block, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel<T, R, FULL>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel<T, R, FULL, SO>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        Layout<T>::BYTES);
     if (e != hipSuccess) {
@@ -2156,15 +2168,18 @@ static int launch_kernel(const m3_scan_args& a, const ScanGeom& g, const float* 
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((scan_kernel<T, R, FULL>), grid, block, Layout<T>::BYTES, stream, a, g,
+  hipLaunchKernelGGL((scan_kernel<T, R, FULL, SO>), grid, block, Layout<T>::BYTES, stream, a, g,
                      prep);
   return check_launch("m3_scan_fwd");
 }
 
 // One pass: the prep kernel (unless `run_prep` is false: its workspace already holds this
 // geometry's results) and the scan kernel.
+// `state_only`: the caller needs only the end state, decay, last k and phase block sums (the
+// outputs are not written where the state-only kernel form applies: the model's shape, 16-bit).
 template <typename T, int R>
-static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep) {
+static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep,
+                       bool state_only = false) {
   ScanGeom g = make_geom<T>(a);
   static_assert(Layout<T>::BYTES <= 160 * 1024, "LDS layout exceeds 160 KiB");
   const float* prep = nullptr;
@@ -2194,6 +2209,9 @@ static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep)
   }
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kThreads);
   if (full_shape(a, g, R) && prep != nullptr) {
+    if constexpr (sizeof(T) == 2) {
+      if (state_only) return launch_kernel<T, R, true, true>(a, g, prep, grid, block, stream);
+    }
     return launch_kernel<T, R, true>(a, g, prep, grid, block, stream);
   }
   return launch_kernel<T, R, false>(a, g, prep, grid, block, stream);
@@ -2345,7 +2363,7 @@ static int launch_segmented(const m3_scan_args& a, int G, hipStream_t stream) {
   a1.final_phase = m3_tensor{};
   a1.block_phase = angles ? contiguous(sg.seg_blk, M3_F32, {BG, H, sg.nbs, S}) : m3_tensor{};
   a1.final_k = contiguous(sg.seg_k, a.act_dtype, {BG, H, R, N});
-  int rc = launch_pass<T, R>(a1, stream, true);
+  int rc = launch_pass<T, R>(a1, stream, true, /*state_only=*/true);
   if (rc != M3_OK) return rc;
 
   const size_t clds = compose_lds_bytes(G, S, N);
