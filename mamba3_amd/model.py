@@ -219,9 +219,9 @@ class _Mamba3Mixer(nn.Module):
              norm: _RMSNorm | None = None):
         """One decode token. ``norm`` (the block's RMSNorm) is applied to ``hidden_states``
         first; with ``residual`` (``[batch, 1, d_model]``) the result is
-        ``residual + out_proj(...)``. For at most ``ops.DECODE_LINEAR_ROWS`` rows and 16-bit
-        weights both projections run on ``ops.linear``, the norm fused into ``in_proj`` and the
-        residual add into ``out_proj``."""
+        ``residual + out_proj(...)``. With 16-bit weights, ``in_proj`` runs on ``ops.linear``
+        with the norm fused up to ``ops.DECODE_LINEAR_ROWS`` rows, and ``out_proj`` with the
+        residual add fused up to ``ops.DECODE_LINEAR_OUT_ROWS``."""
         if hidden_states.ndim != 3 or hidden_states.shape[1:] != (1, self.d_model):
             raise ValueError(
                 f"expected [batch, 1, {self.d_model}], got {tuple(hidden_states.shape)}")
@@ -242,8 +242,8 @@ class _Mamba3Mixer(nn.Module):
             self._validate_cache(cache, hidden_states.shape[0])
         mixed, next_cache = ops.step_projection(proj, self, cache, inplace=inplace)
         mixed = mixed.flatten(-2)
-        if small and ops.linear_supported(mixed, self.out_proj.weight) and (
-                residual is None or residual.dtype == mixed.dtype):
+        if rows.shape[0] <= ops.DECODE_LINEAR_OUT_ROWS and ops.linear_supported(
+                mixed, self.out_proj.weight) and (residual is None or residual.dtype == mixed.dtype):
             res = residual[:, 0] if residual is not None else None
             return ops.linear(mixed, self.out_proj.weight, res).unsqueeze(1), next_cache
         output = self.out_proj(mixed).unsqueeze(1)

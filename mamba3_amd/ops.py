@@ -486,9 +486,12 @@ def step_projection(proj: torch.Tensor, mixer, cache, *, inplace: bool = False):
 
 LINEAR_MAX_ROWS = 256
 LINEAR_NORM_MAX_ROWS = 32
-# Decode steps with at most this many rows run their projections on ``linear``; above it the
-# weights are read few enough times per row that hipBLASLt's GEMMs are as fast.
+# Decode steps run in_proj (with the block's RMSNorm fused) on ``linear`` up to
+# DECODE_LINEAR_ROWS rows, and out_proj (with the residual add fused) up to
+# DECODE_LINEAR_OUT_ROWS. Measured on the decode shapes with cold weights: above these, hipBLASLt
+# (plus the separate norm or add) is as fast.
 DECODE_LINEAR_ROWS = 16
+DECODE_LINEAR_OUT_ROWS = 64
 
 
 def linear_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:

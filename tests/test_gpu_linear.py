@@ -125,15 +125,16 @@ def test_linear_rejects_what_it_does_not_take():
 
 
 @pytest.mark.parametrize("rank", [1, 4])
-def test_bf16_weight_decode_matches_oracle(rank, monkeypatch):
-    """A bf16-weight model's decode steps (3 rows) run both projections on ops.linear
-    (counted; RMSNorm fused into in_proj, residual into out_proj) and match the oracle model
-    fed the same bf16-rounded weights and inputs in FP32."""
+@pytest.mark.parametrize("batch,per_layer", [(3, 2), (40, 1)])
+def test_bf16_weight_decode_matches_oracle(rank, batch, per_layer, monkeypatch):
+    """A bf16-weight model's decode steps run their projections on ops.linear (counted: both
+    at 3 rows, RMSNorm fused into in_proj and the residual into out_proj; out_proj only at 40
+    rows) and match the oracle model fed the same bf16-rounded weights and inputs in FP32."""
     torch.manual_seed(21 + rank)
     model = Mamba3(128, d_state=128, depth=2, mimo_rank=rank).eval().to(torch.bfloat16)
     model = model.to(DEV)
     dims = op.Dims(128, 128, rank)
-    x = torch.randn(3, 12, 128).to(torch.bfloat16)
+    x = torch.randn(batch, 12, 128).to(torch.bfloat16)
     calls = []
     real = ops.linear
 
@@ -160,5 +161,9 @@ def test_bf16_weight_decode_matches_oracle(rank, monkeypatch):
             o, cache = model.step(x[:, t:t + 1].to(DEV), cache)
             got.append(o)
         got = torch.cat(got, 1)
-    assert len(calls) == 8 * 2 * 2  # 8 tokens x 2 layers x (in_proj, out_proj)
-    torch.testing.assert_close(got.float().cpu(), want, rtol=2e-2, atol=2e-2)
+    assert len(calls) == 8 * 2 * per_layer  # 8 tokens x 2 layers x projections on linear
+    # every intermediate of the bf16 model is rounded to bf16, the oracle's stay FP32: the 16-bit
+    # bar of the scan tests, 2e-2 of the output scale elementwise and 1e-2 in norm
+    d = got.float().cpu() - want
+    assert d.abs().max().item() <= 2e-2 * want.abs().max().item()
+    assert d.norm().item() <= 1e-2 * want.norm().item()
