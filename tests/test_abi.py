@@ -181,3 +181,55 @@ def test_linear_validation_and_workspace_on_the_host(lib):
     args.weight.ptr = None
     assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 1
     assert b"weight: required tensor is NULL" in lib.m3_last_error()
+
+
+def _hook_scan_args(batch: int, length: int, heads: int, segments: int) -> _hip.ScanArgs:
+    """A hook-form scan (no phase) over contiguous tensors at fake, aligned device pointers:
+    host-side checks and the workspace query only."""
+    n, p = 64, 64
+    args = _hip.ScanArgs(batch=batch, length=length, heads=heads, groups=1, rank=1, d_state=n,
+                         head_dim=p, num_angles=0, chunk=64, act_dtype=_hip.BF16,
+                         phase_mode=_hip.PHASE_NONE, segments=segments)
+    shapes = {"q": (length, 1, 1, n), "k": (length, 1, 1, n), "value": (length, heads, p),
+              "gate": (length, heads, p), "dt": (length, heads), "a": (length, heads),
+              "trap": (length, heads), "out": (length, heads, p), "final_state": (heads, p, n),
+              "D": ()}
+    ptr = 0x100000
+    for name, dims in shapes.items():
+        t = getattr(args, name)
+        t.ptr, t.dtype = ptr, (_hip.F32 if name in ("final_state", "D") else _hip.BF16)
+        ptr += 1 << 28
+        full = (batch, *dims) if name != "D" else (heads,)
+        stride = 1
+        for i in range(len(full) - 1, -1, -1):
+            t.stride[i] = stride
+            stride *= full[i]
+    return args
+
+
+def test_scan_split_decision_on_the_host(lib):
+    size = ctypes.c_size_t(0)
+
+    def ws(batch, length, heads, segments):
+        args = _hook_scan_args(batch, length, heads, segments)
+        assert lib.m3_scan_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 0
+        return size.value
+
+    # 4 (batch, head) pairs over 4096 tokens: split (the workspace gains the segment buffers)
+    assert ws(1, 4096, 4, 0) > ws(1, 4096, 4, 1)
+    assert ws(1, 4096, 4, 8) > ws(1, 4096, 4, 1)
+    # 256 pairs fill the GPU; 512 tokens are too short to split: one pass each
+    assert ws(8, 4096, 32, 0) == ws(8, 4096, 32, 1)
+    assert ws(1, 512, 4, 0) == ws(1, 512, 4, 1)
+    # an explicit split that does not divide the sequence is refused before any launch
+    args = _hook_scan_args(1, 4096, 4, 3)
+    assert lib.m3_scan_fwd(ctypes.byref(args), None) == 2
+    assert b"segments" in lib.m3_last_error()
+
+
+def test_scan_backwards_token_strides_on_the_host(lib):
+    """Per-token tensors may run backwards (the reverse scan), but all of them together."""
+    args = _hook_scan_args(1, 128, 2, 1)
+    args.value.stride[1] = -args.value.stride[1]
+    assert lib.m3_scan_fwd(ctypes.byref(args), None) == 1
+    assert b"run the same way" in lib.m3_last_error()
