@@ -150,11 +150,11 @@ def bench_prefill(steps, warmup, log, copy_probe=False):
 
 
 def step_kernel_name(pairs, rank):
-    """The kernel m3_step dispatches for the model's decode shape (N 128, P 64, 32 angles)."""
-    if rank <= 2:
-        return f"m3::step128_kernel<__bf16, {rank}, {2 if pairs < 1024 else 8}>"
-    if rank == 4 and pairs < 1024:
-        return "m3::step128_kernel<__bf16, 4, 8>"
+    """The kernel m3_step dispatches for the model's bf16 decode step (N 128, P 64, 32 angles)."""
+    if rank == 1:
+        return "m3::step128_kernel<__bf16, 1, 8, true>"
+    if rank in (2, 4):
+        return f"m3::step_mma_kernel<__bf16, {rank}, true>"
     return f"m3::step_kernel<__bf16, {rank}>"
 
 

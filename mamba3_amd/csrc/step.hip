@@ -3,6 +3,8 @@
 // the rotation of q/k, the trapezoid state update, the readout, the D skip, the SiLU gate and the
 // MIMO rank sum. Replaces ops.fused_step (ops.py:87-190) and its Triton kernel
 // (_triton.py:564-947), and the portable ops.mamba3_step (ops.py:825-879).
+#include <type_traits>
+
 #include "m3_common.hpp"
 #include "m3_host.hpp"
 #include "m3_math.h"
@@ -708,6 +710,331 @@ __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_ar
   }
 }
 
+// The model's decode shape with 16-bit activations and rank R > 1, the readout on MFMA. One
+// 256-thread workgroup per (batch, head); wave w owns state rows p in [16 w, 16 w + 16): half-wave
+// hw = 0, 1 of the wave holds rows 16 w + 2 k + hw (k < 8), columns 4c .. 4c+3, so one load
+// instruction of the wave covers two whole 512-byte rows (16 rows x 64 bytes, the MFMA output
+// layout, streams 15% slower).
+//   - The update S' = alpha S + beta sum_r pvr_r pk_r + gamma sum_r vr_r k_r runs on the VALU in
+//     the order of step128_kernel; k and pk of the lane's columns come from LDS once.
+//   - The readout Y[r][p] = q_r . rnd(S'[p]) is a 16x16x32 MFMA per wave over four K steps: the
+//     wave's 16 rounded rows go through LDS (each wave reads only the rows it wrote), q is A and
+//     the rows are B, so lanes 0-15 end with every rank of row 16 w + lane.
+// Prologue: half-wave j computes q / k / previous k of rank j % R for columns 4c .. 4c+3 (RMSNorm
+// sums over the half-wave, MIMO partner columns n +- 64 in lane c ^ 16) while the state loads are
+// in flight; half-waves j >= R compute duplicates and store nothing.
+template <typename T, int R, bool FULL>
+__global__ __launch_bounds__(256) void step_mma_kernel(const m3_step_args a) {
+  static_assert(sizeof(T) == 2 && (R == 2 || R == 4), "16-bit activations, rank 2 or 4");
+  constexpr int N = 128, P = 64, S = 32, RPT = 8;
+  constexpr int SBW = N + 8;  // rounded-state rows padded: 16 rows at one column hit 16 bank groups
+  typedef T t4 __attribute__((ext_vector_type(4)));
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  const int H = a.heads;
+  const int bh = blockIdx.x;
+  const int b = bh / H, h = bh - b * H;
+  const int g = h / (H / a.groups);
+  const int tid = threadIdx.x, c = tid & 31, hw = tid >> 5, n0 = 4 * c;
+  const int rk = hw & (R - 1);        // the rank this half-wave computes
+  const bool owner = hw < R;          // ... and stores
+  const int l = tid & 63, w = tid >> 6, lm = l & 15, lg = l >> 4;
+  const bool norm = FULL || a.q_norm_w.ptr != nullptr;
+  const bool bias = FULL || a.q_bias.ptr != nullptr;
+  const bool rotate = FULL || a.phase_mode != M3_PHASE_NONE;
+  const bool angles = FULL || a.phase_mode == M3_PHASE_ANGLES;
+  const bool raw_dt = FULL || a.raw_dt != 0;
+  const bool mimo = FULL ? true : a.mimo_rotation != 0;
+
+  __shared__ float s_vr[R][P], s_zr[R][P], s_mo[R][P];
+  __shared__ __align__(16) float s_vrt[P][R];   // rank values by row: one vector read per row
+  __shared__ __align__(16) float s_pvrt[P][R];
+  __shared__ __align__(16) float s_k[R][N];
+  __shared__ __align__(16) float s_pk[R][N];
+  __shared__ __align__(16) T s_q[R][N];
+  __shared__ __align__(16) T s_sb[P][SBW];
+
+  // (1) this thread's state rows
+  auto prow = [&](int k) { return 16 * w + 2 * k + (hw & 1); };
+  const float* sin_ = static_cast<const float*>(a.state_in.ptr) + b * a.state_in.stride[0] +
+                      h * a.state_in.stride[1] + n0;
+  float* sout = static_cast<float*>(a.state_out.ptr) + b * a.state_out.stride[0] +
+                h * a.state_out.stride[1] + n0;
+  const int64_t sp_in = a.state_in.stride[2], sp_out = a.state_out.stride[2];
+  f4 st[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    st[k] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(sin_ + prow(k) * sp_in));
+  }
+
+  // (2) every small input of the (b, h): raw loads issued together, decoded after
+  const RawX dt_r = ldraw(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + h * a.dt.stride[1]);
+  const RawX a_r = ldraw(a.a.ptr, a.a.dtype, b * a.a.stride[0] + h * a.a.stride[1]);
+  const RawX trap_r = ldraw(a.trap.ptr, a.trap.dtype, b * a.trap.stride[0] + h * a.trap.stride[1]);
+  const RawX D_r = ldraw(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
+  RawX dtb_r{0u, 0u};
+  if (raw_dt) dtb_r = ldraw(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]);
+  // phase roles as in step128_kernel: SISO pairs (2j, 2j+1) -> angles 2c, 2c+1 (c < 16); MIMO
+  // pairs (j, j + 2S) -> angles n0 .. n0+3 for the first (c < 8) and third (16 <= c < 24) quarters
+  int j0 = -1, nj = 0;
+  if (rotate) {
+    if (!mimo) {
+      if (c < S / 2) { j0 = 2 * c; nj = 2; }
+    } else if (c < S / 4) {
+      j0 = n0; nj = 4;
+    } else if (c >= S / 2 && c < 3 * S / 4) {
+      j0 = n0 - 2 * S; nj = 4;
+    }
+  }
+  const float* ph_in = static_cast<const float*>(a.phase_in.ptr) + b * a.phase_in.stride[0] +
+                       h * a.phase_in.stride[1];
+  float old[4] = {0.f, 0.f, 0.f, 0.f};
+  RawX th_r[4] = {};
+  if (rotate) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = nj > 0 ? j0 + min(i, nj - 1) : 0;  // lanes without angles read angle 0
+      old[i] = ph_in[j * a.phase_in.stride[2]];
+    }
+  }
+  if (rotate && angles) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = nj > 0 ? j0 + min(i, nj - 1) : 0;
+      th_r[i] = ldraw(a.angles.ptr, a.angles.dtype, b * a.angles.stride[0] + j * a.angles.stride[1]);
+    }
+  }
+  Raw4 wq_r{}, wk_r{}, bq_r{}, bk_r{};
+  if (norm) {
+    wq_r = ldraw4(a.q_norm_w, n0);  // weights may be FP32 or the activation type
+    wk_r = ldraw4(a.k_norm_w, n0);
+  }
+  if (bias) {
+    bq_r = ldraw4(a.q_bias, h * a.q_bias.stride[0] + rk * a.q_bias.stride[1] + n0);
+    bk_r = ldraw4(a.k_bias, h * a.k_bias.stride[0] + rk * a.k_bias.stride[1] + n0);
+  }
+  const f4 qx = ld4<T>(a.q.ptr, b * a.q.stride[0] + g * a.q.stride[1] + rk * a.q.stride[2] + n0);
+  const f4 kx = ld4<T>(a.k.ptr, b * a.k.stride[0] + g * a.k.stride[1] + rk * a.k.stride[2] + n0);
+  const f4 px = ld4<T>(a.prev_k.ptr, b * a.prev_k.stride[0] + h * a.prev_k.stride[1] +
+                                         rk * a.prev_k.stride[2] + n0);
+  // rank values and gates of rank w % R, row p = tid % P: every thread loads them with the batch
+  // above (no branch around loads), waves w < R put them in LDS once decoded
+  const int pl = tid & (P - 1), rw = w & (R - 1);
+  const float v = ld_act<T>(a.value, b * a.value.stride[0] + h * a.value.stride[1] + pl);
+  const float z = ld_act<T>(a.gate, b * a.gate.stride[0] + h * a.gate.stride[1] + pl);
+  const float pv = ld_act<T>(a.prev_value,
+                             b * a.prev_value.stride[0] + h * a.prev_value.stride[1] + pl);
+  const RawX mx_r = ldraw(a.mimo_x.ptr, a.mimo_x.dtype,
+                          h * a.mimo_x.stride[0] + rw * a.mimo_x.stride[1] + pl);
+  const RawX mz_r = ldraw(a.mimo_z.ptr, a.mimo_z.dtype,
+                          h * a.mimo_z.stride[0] + rw * a.mimo_z.stride[1] + pl);
+  const RawX mo_r = ldraw(a.mimo_out.ptr, a.mimo_out.dtype,
+                          h * a.mimo_out.stride[0] + rw * a.mimo_out.stride[1] + pl);
+  if (w < R) {
+    const float mx = rnd<T>(decode(mx_r, a.mimo_x.dtype));
+    const float mz = rnd<T>(decode(mz_r, a.mimo_z.dtype));
+    const float vr = mul_r<T>(v, mx);
+    s_vr[rw][pl] = vr;
+    s_vrt[pl][rw] = vr;
+    s_pvrt[pl][rw] = mul_r<T>(pv, mx);
+    s_zr[rw][pl] = mul_r<T>(z, mz);
+    s_mo[rw][pl] = decode(mo_r, a.mimo_out.dtype);
+  }
+
+  const float dt_in = decode(dt_r, a.dt.dtype), a_in = decode(a_r, a.a.dtype);
+  const float trap_in = decode(trap_r, a.trap.dtype), Dh = decode(D_r, a.D.dtype);
+  const float dtb_in = raw_dt ? decode(dtb_r, a.dt_bias.dtype) : 0.f;
+  float th[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) th[i] = decode(th_r[i], a.angles.dtype);
+  const f4 wq = decode4(wq_r, a.q_norm_w.dtype), wk = decode4(wk_r, a.k_norm_w.dtype);
+  const f4 bq = decode4(bq_r, a.q_bias.dtype), bk = decode4(bk_r, a.k_bias.dtype);
+
+  // per-(b, h) scalars
+  float dt, adt;
+  dt_adt(raw_dt, dt_in, a_in, dtb_in, dt, adt);
+  const float trap = sigmoidf(trap_in);
+  const float alpha = expf(adt);
+  const float beta = (1.f - trap) * dt * alpha;
+  const float gamma = trap * dt;
+
+  // (3) phases of the angles this thread's columns use
+  float phn[4] = {0.f, 0.f, 0.f, 0.f}, cs[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i < nj) {
+      float ph = old[i];
+      if (angles) ph = m3_fmod_2pi(__fadd_rn(old[i], phase_inc(th[i], dt)));
+      phn[i] = ph;
+      float sv, cv;
+      __sincosf(ph, &sv, &cv);  // ph in [0, 2 pi): the hardware sine / cosine, as in the scan
+      cs[i] = rnd<T>(cv);
+      sn[i] = rnd<T>(sv);
+    }
+  }
+
+  // (4) q / k of rank rk, columns n0 .. n0+3: RMSNorm, weight, bias, rotation (the rounding steps
+  // of step128_kernel)
+  float q[4], k[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    q[j] = qx[j];
+    k[j] = kx[j];
+  }
+  if (norm) {
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sq += q[j] * q[j];
+      sk += k[j] * k[j];
+    }
+    sq = allreduce32(sq);
+    sk = allreduce32(sk);
+    const float rq = 1.f / sqrtf(sq / static_cast<float>(N) + a.norm_eps);
+    const float rk_ = 1.f / sqrtf(sk / static_cast<float>(N) + a.norm_eps);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      q[j] = rnd<T>(q[j] * rq * rnd<T>(wq[j]));
+      k[j] = rnd<T>(k[j] * rk_ * rnd<T>(wk[j]));
+    }
+  }
+  if (bias) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      q[j] = add_r<T>(q[j], rnd<T>(bq[j]));
+      k[j] = add_r<T>(k[j], rnd<T>(bk[j]));
+    }
+  }
+  if (rotate && !mimo) {
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      const float lq = q[2 * pp], hq = q[2 * pp + 1], lk = k[2 * pp], hk = k[2 * pp + 1];
+      if (nj > 0) {
+        q[2 * pp] = sub_r<T>(mul_r<T>(lq, cs[pp]), mul_r<T>(hq, sn[pp]));
+        q[2 * pp + 1] = add_r<T>(mul_r<T>(lq, sn[pp]), mul_r<T>(hq, cs[pp]));
+        k[2 * pp] = sub_r<T>(mul_r<T>(lk, cs[pp]), mul_r<T>(hk, sn[pp]));
+        k[2 * pp + 1] = add_r<T>(mul_r<T>(lk, sn[pp]), mul_r<T>(hk, cs[pp]));
+      }
+    }
+  } else if (rotate) {
+    // partner columns n +- 2S = +-64 live in lane c xor 16
+    float oq[4], ok[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      oq[j] = swap16(q[j]);
+      ok[j] = swap16(k[j]);
+    }
+    if (nj > 0) {
+      const bool first = c < S / 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (first) {
+          q[j] = sub_r<T>(mul_r<T>(q[j], cs[j]), mul_r<T>(oq[j], sn[j]));
+          k[j] = sub_r<T>(mul_r<T>(k[j], cs[j]), mul_r<T>(ok[j], sn[j]));
+        } else {
+          q[j] = add_r<T>(mul_r<T>(oq[j], sn[j]), mul_r<T>(q[j], cs[j]));
+          k[j] = add_r<T>(mul_r<T>(ok[j], sn[j]), mul_r<T>(k[j], cs[j]));
+        }
+      }
+    }
+  }
+  if (owner) {
+    *reinterpret_cast<t4*>(&s_q[rk][n0]) = t4{from_f<T>(q[0]), from_f<T>(q[1]), from_f<T>(q[2]),
+                                              from_f<T>(q[3])};
+    *reinterpret_cast<f4*>(&s_k[rk][n0]) = f4{k[0], k[1], k[2], k[3]};
+    *reinterpret_cast<f4*>(&s_pk[rk][n0]) = px;
+    // k_out may alias prev_k: this thread alone read these elements of it (px, above)
+    st4<T>(a.k_out.ptr, b * a.k_out.stride[0] + h * a.k_out.stride[1] + rk * a.k_out.stride[2] +
+                            n0, k);
+  }
+  __syncthreads();  // the per-row and per-column LDS vectors
+  // value_out may alias prev_value, which every wave read before the barrier
+  if (tid < P && a.value_out.ptr != nullptr) {
+    static_cast<T*>(a.value_out.ptr)[b * a.value_out.stride[0] + h * a.value_out.stride[1] +
+                                     tid] = from_f<T>(v);
+  }
+
+  // (5) state update of this thread's rows (the sums of step128_kernel), the rounded rows to LDS
+  float kk[R][4], pk[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const f4 kv = *reinterpret_cast<const f4*>(&s_k[r][n0]);
+    const f4 pv4 = *reinterpret_cast<const f4*>(&s_pk[r][n0]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      kk[r][j] = kv[j];
+      pk[r][j] = pv4[j];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int p = prow(k);
+    typedef float fr __attribute__((ext_vector_type(R)));
+    const fr pvr = *reinterpret_cast<const fr*>(&s_pvrt[p][0]);
+    const fr vr = *reinterpret_cast<const fr*>(&s_vrt[p][0]);
+    float po[4] = {0.f, 0.f, 0.f, 0.f}, co[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        po[j] += pvr[r] * pk[r][j];
+        co[j] += vr[r] * kk[r][j];
+      }
+    }
+    f4 ns;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ns[j] = alpha * st[k][j] + beta * po[j] + gamma * co[j];
+    __builtin_nontemporal_store(ns, reinterpret_cast<f4*>(sout + p * sp_out));
+    *reinterpret_cast<t4*>(&s_sb[p][n0]) =
+        t4{from_f<T>(ns[0]), from_f<T>(ns[1]), from_f<T>(ns[2]), from_f<T>(ns[3])};
+  }
+
+  // (6) readout of the wave's rows: A = q (row m holds rank m % R), B = the rounded rows; LDS
+  // operations of one wave complete in order, so a wave-level fence orders its writes before its
+  // reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int prow_l = 16 * w + lm;
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < N / 32; ++s) {
+    const t8 av = *reinterpret_cast<const t8*>(&s_q[lm & (R - 1)][32 * s + 8 * lg]);
+    const t8 bv = *reinterpret_cast<const t8*>(&s_sb[prow_l][32 * s + 8 * lg]);
+    if constexpr (std::is_same<T, __bf16>::value) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+    } else {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+    }
+  }
+  // lanes l < 16 hold Y[r][16 w + l] in acc[r]; D skip, gate and the rank sum in rank order
+  if (lg == 0) {
+    const int p = prow_l;
+    float y = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float t = (acc[r] + Dh * s_vr[r][p]) * siluf(s_zr[r][p]);
+      y = y + t * s_mo[r][p];
+    }
+    static_cast<T*>(a.out.ptr)[b * a.out.stride[0] + h * a.out.stride[1] + p] = from_f<T>(y);
+  }
+
+  // (7) phase_out may alias phase_in, which every half-wave read before the barrier above
+  if (hw == 0) {
+    float* ph_out = static_cast<float*>(a.phase_out.ptr) + b * a.phase_out.stride[0] +
+                    h * a.phase_out.stride[1];
+    if (rotate) {
+      // each angle has one writer: SISO c < 16, MIMO the first quarter (c < 8)
+      const bool writer = !mimo || c < S / 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (writer && i < nj) ph_out[(j0 + i) * a.phase_out.stride[2]] = phn[i];
+      }
+    } else if (c < S) {
+      ph_out[c * a.phase_out.stride[2]] = ph_in[c * a.phase_in.stride[2]];
+    }
+  }
+}
+
 static size_t step_lds_bytes(int R, int N, int P, int S) {
   return sizeof(float) * (static_cast<size_t>(5) * R * N + 5 * R * P + P + 3 * S + 2 * R);
 }
@@ -747,10 +1074,30 @@ static void launch128(const m3_step_args& a, dim3 grid, dim3 block, hipStream_t 
   }
 }
 
+template <typename T, int R>
+static void launch_mma(const m3_step_args& a, dim3 grid, hipStream_t stream) {
+  if (step_full(a)) {
+    hipLaunchKernelGGL((step_mma_kernel<T, R, true>), grid, dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((step_mma_kernel<T, R, false>), grid, dim3(256), 0, stream, a);
+  }
+}
+
 template <typename T>
 static int launch_step(const m3_step_args& a, hipStream_t stream) {
   const size_t lds = step_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles);
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kStepThreads);
+  if constexpr (sizeof(T) == 2) {
+    // 16-bit activations, ranks 2 and 4: the update and the readout on MFMA
+    if ((a.rank == 2 || a.rank == 4) && step128_ok(a)) {
+      if (a.rank == 2) {
+        launch_mma<T, 2>(a, grid, stream);
+      } else {
+        launch_mma<T, 4>(a, grid, stream);
+      }
+      return check_launch("m3_step");
+    }
+  }
   // Ranks 1 and 2; rank 4 only below 1024 (batch, head) pairs (with many, its four readout
   // reductions per row make the LDS-staged step_kernel faster; rank 8 always uses that one).
   // The 256-thread form at every batch: at B = 1 its 4 waves start together, where a 1024-

@@ -99,8 +99,9 @@ def test_fused_step_matches_oracle(dtype, rank, dims):
 @pytest.mark.parametrize("rank", [1, 2, 4])
 def test_fused_step_many_heads_matches_oracle(dtype, rank):
     """1088 (batch, head) pairs: the launch shape of large decode batches (256 threads per
-    pair, 8 state rows per thread for ranks 1 and 2; the LDS-staged kernel for rank 4), at the
-    model's head shape, both out of place and with the outputs aliasing the cache."""
+    pair: 8 state rows per thread for rank 1 and FP32 rank 2; for 16-bit ranks 2 and 4 the
+    update and readout on MFMA; the LDS-staged kernel for FP32 rank 4), at the model's head
+    shape, both out of place and with the outputs aliasing the cache."""
     inp = _inputs(rank, dtype, batch=17, heads=64, seed=20 + rank)
     y_ref, (ph_ref, s_ref, k_ref, _) = _oracle_fused(inp)
     d = _dev(inp)
