@@ -303,12 +303,16 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--decode-batch", type=int, default=256)
     ap.add_argument("--decode-steps", type=int, default=512)
+    ap.add_argument("--decode-rank", type=int, default=1, choices=(1, 2, 4),
+                    help="MIMO rank of the decode line's model (config 4 runs 1 and 4)")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--extra", action="store_true",
                     help="also measure BASELINE configs 3, 5 and config 4 at B=1/64 and R=4")
+    ap.add_argument("--extra-only", choices=("config3", "config5", "config5_long", "decode"),
+                    help="with --extra: measure only this one of the extra configurations")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates PMC byte counters)")
     args = ap.parse_args()
@@ -325,19 +329,22 @@ def main() -> None:
     pre = bench_prefill(args.steps, args.warmup, log, copy_probe=args.copy_probe)
     decode = None
     if not args.no_decode:
-        decode = bench_decode(args.decode_batch, args.decode_steps, log)
+        decode = bench_decode(args.decode_batch, args.decode_steps, log, rank=args.decode_rank)
     extra = None
     if args.extra:
-        extra = {
-            "config3_mimo_prefill": bench_prefill_config(
-                "config 3", 1024, 4, 4, True, (8, 4096, 1024), 2, log),
-            "config5_bidir_16x2048": bench_prefill_config(
-                "config 5", 768, 12, 1, False, (16, 2048, 768), 4, log),
-            "config5_bidir_1x65536": bench_prefill_config(
-                "config 5 long", 768, 12, 1, False, (1, 65536, 768), 4, log, iters=2),
-            "config4_decode": [bench_decode(b, args.decode_steps, log, rank=r)
-                               for b, r in ((1, 1), (64, 1), (256, 4), (64, 4), (1, 4))],
+        runs = {
+            "config3_mimo_prefill": ("config3", lambda: bench_prefill_config(
+                "config 3", 1024, 4, 4, True, (8, 4096, 1024), 2, log)),
+            "config5_bidir_16x2048": ("config5", lambda: bench_prefill_config(
+                "config 5", 768, 12, 1, False, (16, 2048, 768), 4, log)),
+            "config5_bidir_1x65536": ("config5_long", lambda: bench_prefill_config(
+                "config 5 long", 768, 12, 1, False, (1, 65536, 768), 4, log, iters=2)),
+            "config4_decode": ("decode", lambda: [
+                bench_decode(b, args.decode_steps, log, rank=r)
+                for b, r in ((1, 1), (64, 1), (256, 4), (64, 4), (1, 4))]),
         }
+        extra = {name: run() for name, (key, run) in runs.items()
+                 if args.extra_only in (None, key)}
     cpu = None if args.no_cpu else bench_cpu(log, args.cpu_batch, args.cpu_tokens)
     value = pre["tokens"] / pre["per_launch"]
     line = {

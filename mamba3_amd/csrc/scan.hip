@@ -403,6 +403,7 @@ template <typename T, int R, bool FULL>
 struct Feed {
   static constexpr int ES = sizeof(T), W8 = Words<T>::W8, W4 = Words<T>::W4;
   static constexpr int ROWS = Mma<T>::ROWS, TOK = ROWS / R;
+  static constexpr int VJ = R == 1 ? 2 : 1;  // value / gate tokens per lane
   // FULL
   __amdgpu_buffer_rsrc_t rs_p, rs_w;
   int o_qk, o_vz, d_q1, d_k, d_z, tok_b;  // per-lane byte offsets at token 0, uniform deltas
@@ -438,7 +439,7 @@ struct Feed {
       rs_p = make_rsrc(g.proj + b * g.proj_b, L * (tok_b < 0 ? -tok_b : tok_b));
       rs_w = make_rsrc(prep, g.ws_bytes);
       o_qk = g.o_q + grp * g.qk_g + r0 * g.qk_r + tt0 * tok_b + n0 * ES;
-      o_vz = g.o_v + h * g.vz_h + 2 * vp * tok_b + p0 * ES;
+      o_vz = g.o_v + h * g.vz_h + (R == 1 ? 2 * vp : (2 * vp) / R) * tok_b + p0 * ES;
       d_q1 = R == 1 ? tok_b : g.qk_r;  // row 2rp + 1: the next token (R = 1) or the next rank
       d_k = g.o_k - g.o_q;
       d_z = g.o_z - g.o_v;
@@ -500,8 +501,8 @@ struct Feed {
     }
   }
 
-  // q / k rows 2rp, 2rp+1 and value / gate tokens 2vp, 2vp+1 of the sub-chunk at token t0
-  // (nw valid tokens)
+  // q / k rows 2rp, 2rp+1 and the value / gate of rows 2vp, 2vp+1 of the sub-chunk at token t0
+  // (nw valid tokens): tokens 2vp, 2vp+1 for R = 1, else token 2vp / R (both rows' ranks)
   __device__ __forceinline__ void words(int t0, int nw, bool qk_on, bool vz_on,
                                         uint32_t (&rq)[2][W8], uint32_t (&rk)[2][W8],
                                         uint32_t (&rv)[2][W4], uint32_t (&rz)[2][W4]) const {
@@ -539,15 +540,15 @@ struct Feed {
     if constexpr (FULL) {
       const int tb = t0 * tok_b;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < VJ; ++j) {
         bload_words<W4>(rv[j], rs_p, o_vz + tb + j * tok_b);
         bload_words<W4>(rz[j], rs_p, o_vz + tb + j * tok_b + d_z);
       }
     } else {
       if (vz_on) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int tt = 2 * vp + j;
+        for (int j = 0; j < VJ; ++j) {
+          const int tt = R == 1 ? 2 * vp + j : (2 * vp) / R;
           const bool ok = tt < nw;
           const int tg = t0 + tt;
           load_words<T, 4>(rv[j], v_row + tg * v_t, ok ? vz_n : 0, vec_vz);
@@ -956,10 +957,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // 64 columns)
   const bool qk_on = SPLIT || (rp < ROWS / 2 && n0 < N);
   const int qk_n = min(8, N - n0);
-  // v / z: token pair vp (tokens 2vp, 2vp+1), columns p0 .. p0+3
+  // v / z: row pair vp (rows 2vp, 2vp+1; tokens 2vp, 2vp+1 for R = 1), columns p0 .. p0+3
   constexpr int P4 = kPPad / 4;
   const int vp = tid / P4, p0 = 4 * (tid % P4);
-  const bool vz_on = SPLIT || (2 * vp < TOK && p0 < P);
+  const bool vz_on = SPLIT || (2 * vp < TOK * R && p0 < P);
   const int vz_n = min(4, P - p0);
   // phase: angle ps, token group pg (tokens TPL pg .. TPL pg + TPL-1)
   const int pg = tid % PG, ps = tid / PG;
@@ -1171,7 +1172,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   if (ph_on && nsub > 0) {
     float pa[TPL];
     angles_of(pa);
-    phase_stage<PG, TPL, CST, SPLIT, !SPLIT>(csb(0), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
+    phase_stage<PG, TPL, CST, SPLIT, F32>(csb(0), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
                                      scb(0) + SB_::DTV, 0, L, pg, lane, angles, pa, fph, fblk,
                                      blk_stride);
   }
@@ -1241,7 +1242,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
               kp[i] = k[i ^ 1];
             } else {
               const int half = N >> 1;
-              if (half >= 8) {
+              if (FULL) {
+                // N = 128: the partner lane is lane ^ 8, a rotation by 8 in the 16-lane row
+                qp[i] = dpp_shr<0x128>(q[i]);
+                kp[i] = dpp_shr<0x128>(k[i]);
+              } else if (half >= 8) {
                 qp[i] = __shfl_xor(q[i], half >> 3, 16);
                 kp[i] = __shfl_xor(k[i], half >> 3, 16);
               } else {
@@ -1290,9 +1295,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     // value / gate of tokens 2vp, 2vp+1, columns p0 .. p0+3: rank values v mx_r -> VT
     // (transposed, swizzled) and VR (row-major), rank gates z mz_r -> ZR (row-major)
     if (vz_on) {
-      float v[2][4], z[2][4];
+      constexpr int VJ = Feed<T, R, FULL>::VJ;
+      float v[VJ][4], z[VJ][4];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < VJ; ++j) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           v[j][i] = raw_get<T>(rv[j], i);
@@ -1334,33 +1340,29 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           st_quad<T>(ZR + (2 * vp + j) * LP + p0, zq);
         }
       } else {
+        // rows 2vp, 2vp+1: ranks r0, r0 + 1 of token 2vp / R (every lane of the workgroup has a
+        // row pair, as for R = 1)
+        const int r0 = (2 * vp) % R;
+        f4 vq[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            const int row = (2 * vp + j) * R + r;
-            f4 vq, zq;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              vq[i] = mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p0 + i]);
-              zq[i] = mul_r<T>(z[j][i], F[Lay::MZ + r * kPPad + p0 + i]);
-            }
-            if constexpr (!SO) {
-              st_quad<T>(VR + row * LP + p0, vq);
-              st_quad<T>(ZR + row * LP + p0, zq);
-            }
-          }
+        for (int jr = 0; jr < 2; ++jr) {
+          const int r = r0 + jr, row = 2 * vp + jr;
+          f4 zq;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int p = p0 + i;
-            if (!FULL && p >= P) continue;
+            vq[jr][i] = mul_r<T>(v[0][i], F[Lay::MX + r * kPPad + p0 + i]);
+            zq[i] = mul_r<T>(z[0][i], F[Lay::MZ + r * kPPad + p0 + i]);
+          }
+          if constexpr (!SO) {
+            st_quad<T>(VR + row * LP + p0, vq[jr]);
+            st_quad<T>(ZR + row * LP + p0, zq);
+          }
+        }
 #pragma unroll
-            for (int r = 0; r < R; r += 2) {
-              const int row = (2 * vp + j) * R + r;
-              st_pair<T>(VT + p * LR + swz<ROWS>(row, p >> VSH),
-                         mul_r<T>(v[j][i], F[Lay::MX + r * kPPad + p]),
-                         mul_r<T>(v[j][i], F[Lay::MX + (r + 1) * kPPad + p]));
-            }
+        for (int i = 0; i < 4; ++i) {
+          const int p = p0 + i;
+          if (FULL || p < P) {
+            st_pair<T>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH), vq[0][i], vq[1][i]);
           }
         }
       }
@@ -1478,7 +1480,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     if (ph_on && c + 1 < nsub) {
       float pa[TPL];
       angles_of(pa);
-      phase_stage<PG, TPL, CST, SPLIT, !SPLIT>(csb(c + 1), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
+      phase_stage<PG, TPL, CST, SPLIT, F32>(csb(c + 1), ps, F + Lay::PBASE + ps, F + Lay::POFF + ps,
                                        scb(c + 1) + SB_::DTV, t0 + TOK, L, pg, lane, angles, pa,
                                        fph, fblk, blk_stride);
     }
