@@ -296,6 +296,60 @@ def bench_cpu(log, batch=8, length=8192):
                         f"1 warmup"))
 
 
+def bench_cpu_decode(log, batch=256, steps=3):
+    """The CPU oracle on the decode step's hot path: one config-4 layer (d_model 2048, R = 1) at
+    ``batch`` rows, FP32, from the raw ``in_proj`` output (the GEMMs are not timed, as on the
+    GPU's step-kernel line): split, B/C RMSNorm, dt/A, head biases, phase advance, rotation and
+    the exact update and readout."""
+    from oracle import portable as op
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    torch.manual_seed(3)
+    dims = op.Dims(2048, 128, 1)
+    params = op.init_params(2048, d_state=128, depth=1, mimo_rank=1)
+    pre = "layers.0.mixer."
+    hh, pp, nn_ = dims.nheads, dims.headdim, dims.d_state
+    cache = list(op.zero_cache(dims, batch, torch.float32))
+    cache[1] = torch.randn(batch, hh, pp, nn_) * 0.1
+    with torch.inference_mode():
+        projs = [torch.nn.functional.linear(
+            op.rms_norm(torch.randn(batch, 2048), params["layers.0.norm.weight"]),
+            params[pre + "in_proj.weight"]) for _ in range(steps + 1)]
+
+        def hot_path(proj, cache):
+            z, xv, b, c, ddt, da, trap, ang = torch.split(proj, dims.split_sizes, dim=-1)
+            k = op.rms_norm(b.reshape(batch, 1, 1, nn_), params[pre + "B_norm.weight"])
+            q = op.rms_norm(c.reshape(batch, 1, 1, nn_), params[pre + "C_norm.weight"])
+            q = q.expand(batch, hh, 1, nn_) + params[pre + "C_bias"]
+            k = k.expand(batch, hh, 1, nn_) + params[pre + "B_bias"]
+            dt = torch.nn.functional.softplus(ddt + params[pre + "dt_bias"])
+            adt = (-op.heavy_tail(da)).clamp(max=-op.A_FLOOR) * dt
+            phase = torch.fmod(cache[0] + op.phase_increment(ang, dt), op.TWO_PI)
+            q, k = op.rotate(q[:, None], k[:, None], phase[:, None], mimo=False)
+            return op.step_update(q[:, 0], k[:, 0], xv.reshape(batch, hh, pp),
+                                  z.reshape(batch, hh, pp), adt, dt, trap, params[pre + "D"],
+                                  (phase, cache[1], cache[2], cache[3]))
+
+        _, cache = hot_path(projs[0], cache)
+        times = []
+        for i in range(steps):
+            t0 = time.perf_counter()
+            _, cache = hot_path(projs[i + 1], cache)
+            times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    tok_s = batch / (24 * t)
+    log(f"cpu oracle decode: {t * 1e3:.1f} ms per layer step at B={batch} on {cores} threads -> "
+        f"{tok_s:.1f} tok/s over 24 layers (step hot path only)")
+    return dict(value=round(tok_s, 1), unit="tok/s", cores=cores, kind="port",
+                ms_per_layer_step=round(t * 1e3, 2),
+                sample=(f"the decode step's hot path (split, B/C RMSNorm, dt/A, biases, phase, "
+                        f"rotation, update and readout; no projection GEMMs) of one config-4 layer "
+                        f"(d_model 2048, R 1) at B={batch} in FP32, median of {steps} steps after "
+                        f"1 warmup; value = B / (24 x per-layer time), to set beside "
+                        f"decode.step_kernel"))
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -346,6 +400,7 @@ def main() -> None:
         extra = {name: run() for name, (key, run) in runs.items()
                  if args.extra_only in (None, key)}
     cpu = None if args.no_cpu else bench_cpu(log, args.cpu_batch, args.cpu_tokens)
+    cpu_decode = None if args.no_cpu or args.no_decode else bench_cpu_decode(log)
     value = pre["tokens"] / pre["per_launch"]
     line = {
         "metric": METRIC,
@@ -369,6 +424,7 @@ def main() -> None:
         "forward": pre["forward"],
         "decode": decode,
         "cpu_baseline": cpu,
+        "cpu_baseline_decode": cpu_decode,
     }
     if extra is not None:
         line["extra_configs"] = extra
