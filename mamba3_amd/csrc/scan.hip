@@ -756,85 +756,134 @@ __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __res
 }
 
 // Head-independent and per-(head, sub-chunk) work ahead of the scan, three block ranges:
-//  [0, nb_norm)  one 16-lane group per raw q / k row (token, group, rank, q|k), 8 elements per
-//                lane: its RMSNorm factor 1 / sqrt(mean(x^2) + eps) (model.py:190-191);
-//  [.., +nb_ang) one lane per (token, angle), token padded to a multiple of 4: pi * tanh(angle)
-//                (model.py:225-228), 0 in the padding;
+//  [0, nb_norm)  one 16-lane group per kNormRows raw q / k rows (token, group, rank, q|k), 8
+//                elements per lane: each row's RMSNorm factor 1 / sqrt(mean(x^2) + eps)
+//                (model.py:190-191);
+//  [.., +nb_ang) one lane per kAngQuads (4-token group, angle) pairs, tokens padded to a multiple
+//                of 4: pi * tanh(angle) (model.py:225-228), 0 in the padding;
+// The first two give each workgroup several rows' loads in flight: with one round trip per
+// workgroup they were bound by workgroup turnover (the scalar blocks' LDS allows 6 workgroups per
+// CU). The scalar blocks, the longest workgroups, are dispatched first.
 //  [.., +nb_sc)  one workgroup per (batch, sub-chunk): the dt / a / trap of its TOK tokens and
 //                the next sub-chunk's first, every head, loaded with consecutive lanes on
 //                consecutive heads (32 heads per pass) into LDS; then one wave per head computes
 //                that head's scalar block.
+constexpr int kNormRows = 8;  // q / k rows per 16-lane group of prep_kernel
+constexpr int kAngQuads = 4;  // (4-token group, angle) pairs per lane of prep_kernel
+
 template <typename T, int R>
 __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const ScanGeom g,
                                                    float* __restrict__ ws, int nb_norm,
                                                    int nb_ang) {
   // every index below fits 31 bits (checked by the host)
   constexpr int TOK = Mma<T>::ROWS / R, TPT = 16 / R;
-  const int tid = threadIdx.x, blk = blockIdx.x;
+  // the longest-running range (scalar blocks) is dispatched first: block ids [0, nb_sc) map to
+  // it, the rest to the norm and angle ranges in order
+  const int nb_sc = a.batch * g.nsub;
+  const int tid = threadIdx.x;
+  const int blk = static_cast<int>(blockIdx.x) < nb_sc ? static_cast<int>(blockIdx.x) + nb_norm + nb_ang
+                                                       : static_cast<int>(blockIdx.x) - nb_sc;
   const int L = a.length, tokens = a.batch * L;
   if (blk < nb_norm) {
+    // rows blk * 16 kNormRows + (tid >> 4) + 16 k, k < kNormRows: every row's loads first
     const int gr_n = a.groups * a.rank;
-    const int row = blk * 16 + (tid >> 4);  // (token, group-rank, q|k)
-    if (row >= tokens * gr_n * 2) return;   // whole 16-lane groups leave together
-    const int l16 = tid & 15;
-    const int tok = row / (2 * gr_n);
-    const int rem = row - tok * 2 * gr_n;
-    const int gr = rem >> 1, which = rem & 1;
-    const int gi = gr / a.rank, r = gr - gi * a.rank;
-    const int b = tok / L, t = tok - b * L;
-    const m3_tensor& x = which ? a.k : a.q;
-    const T* p = static_cast<const T*>(x.ptr) + b * x.stride[0] + t * x.stride[1] +
-                 gi * x.stride[2] + r * x.stride[3] + 8 * l16;
+    const int nrows = tokens * gr_n * 2;
+    const int l16 = tid & 15, row0 = blk * 16 * kNormRows + (tid >> 4);
     const int N = a.d_state;
-    float ss = 0.f;
+    const bool in = 8 * l16 < N;  // lanes past column N load column 0 and count zeros
+    auto row_ptr = [&](int row) {
+      const int tok = row / (2 * gr_n);
+      const int rem = row - tok * 2 * gr_n;
+      const int gr = rem >> 1, which = rem & 1;
+      const int gi = gr / a.rank, r = gr - gi * a.rank;
+      const int b = tok / L, t = tok - b * L;
+      const m3_tensor& x = which ? a.k : a.q;
+      return static_cast<const T*>(x.ptr) + b * x.stride[0] + t * x.stride[1] +
+             gi * x.stride[2] + r * x.stride[3] + (in ? 8 * l16 : 0);
+    };
+    float ss[kNormRows];
     if (g.vec_qk) {
-      if (8 * l16 < N) {
-        uint32_t w8[Words<T>::W8];
+      uint32_t w8[kNormRows][Words<T>::W8];
+#pragma unroll
+      for (int k = 0; k < kNormRows; ++k) {
+        // rows past the end re-read the last row; their sums are not stored
+        const T* p = row_ptr(min(row0 + 16 * k, nrows - 1));
 #pragma unroll
         for (int j = 0; j < Words<T>::W8; j += 4) {
           const uint4 q = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(p) + j);
-          w8[j] = q.x;
-          w8[j + 1] = q.y;
-          w8[j + 2] = q.z;
-          w8[j + 3] = q.w;
+          w8[k][j] = in ? q.x : 0u;
+          w8[k][j + 1] = in ? q.y : 0u;
+          w8[k][j + 2] = in ? q.z : 0u;
+          w8[k][j + 3] = in ? q.w : 0u;
         }
+      }
+#pragma unroll
+      for (int k = 0; k < kNormRows; ++k) {
+        ss[k] = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float v = raw_get<T>(w8, i);
-          ss = fmaf(v, v, ss);
+          const float v = raw_get<T>(w8[k], i);
+          ss[k] = fmaf(v, v, ss[k]);
         }
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (8 * l16 + i < N) {
-          const float v = to_f(p[i]);
-          ss = fmaf(v, v, ss);
+      for (int k = 0; k < kNormRows; ++k) {
+        const T* p = row_ptr(min(row0 + 16 * k, nrows - 1));
+        ss[k] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (in && 8 * l16 + i < N) {
+            const float v = to_f(p[i]);
+            ss[k] = fmaf(v, v, ss[k]);
+          }
         }
       }
     }
 #pragma unroll
-    for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
-    if (l16 == 0) {
-      ws[g.ws_norm + static_cast<int64_t>(row)] =
-          1.f / sqrtf(ss / static_cast<float>(N) + a.norm_eps);
+    for (int k = 0; k < kNormRows; ++k) {
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) ss[k] += __shfl_xor(ss[k], o, 16);
+      const int row = row0 + 16 * k;
+      if (l16 == 0 && row < nrows) {
+        ws[g.ws_norm + static_cast<int64_t>(row)] =
+            1.f / sqrtf(ss[k] / static_cast<float>(N) + a.norm_eps);
+      }
     }
   } else if (blk < nb_norm + nb_ang) {
-    // element (b, t4, s, i) of the angle region, token t = 4 t4 + i
+    // (b, t4, s) quads blk * 256 kAngQuads + tid + 256 k: the angle s of tokens 4 t4 .. 4 t4 + 3,
+    // written as the angle region's 4 consecutive elements (b, t4, s, i); 0 past token L - 1
     const int S = a.num_angles;
-    const int e = (blk - nb_norm) * 256 + tid;
-    if (e >= a.batch * g.L4 * S * 4) return;
-    const int i = e & 3, rest = e >> 2;
-    const int s = rest % S, bt4 = rest / S;
-    const int b = bt4 / g.L4, t = 4 * (bt4 - b * g.L4) + i;
-    float v = 0.f;
-    if (t < L) {
-      const float th = decode(ldraw(a.phase.ptr, a.phase.dtype, b * a.phase.stride[0] +
-                                                          t * a.phase.stride[1] + s * a.phase.stride[2]),
-                              a.phase.dtype);
-      v = __fmul_rn(kPi, tanhf(th));
+    const int nq = a.batch * g.L4 * S;
+    const int q0 = (blk - nb_norm) * 256 * kAngQuads + tid;
+    RawX raw[kAngQuads][4];
+#pragma unroll
+    for (int k = 0; k < kAngQuads; ++k) {
+      const int quad = min(q0 + 256 * k, nq - 1);
+      const int sa = quad % S, bt4 = quad / S;
+      const int b = bt4 / g.L4, t4 = bt4 - b * g.L4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = min(4 * t4 + i, L - 1);
+        raw[k][i] = ldraw(a.phase.ptr, a.phase.dtype,
+                          b * a.phase.stride[0] + t * a.phase.stride[1] + sa * a.phase.stride[2]);
+      }
     }
-    ws[g.ws_ang + static_cast<int64_t>(e)] = v;
+#pragma unroll
+    for (int k = 0; k < kAngQuads; ++k) {
+      const int quad = q0 + 256 * k;
+      if (quad >= nq) continue;
+      const int bt4 = quad / S;
+      const int t4 = bt4 - (bt4 / g.L4) * g.L4;
+      float4 v;
+      float* vv = reinterpret_cast<float*>(&v);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float th = decode(raw[k][i], a.phase.dtype);
+        vv[i] = 4 * t4 + i < L ? __fmul_rn(kPi, tanhf(th)) : 0.f;
+      }
+      *reinterpret_cast<float4*>(ws + g.ws_ang + 4 * static_cast<int64_t>(quad)) = v;
+    }
   } else {
     const int bc = blk - nb_norm - nb_ang;
     if (bc >= a.batch * g.nsub) return;  // whole workgroups leave together
@@ -2199,7 +2248,8 @@ static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep,
     if (rows >= INT32_MAX || ang >= INT32_MAX || blocks >= INT32_MAX || tokens >= INT32_MAX) {
       return fail(M3_EUNSUPPORTED, "m3_scan_fwd: too many tokens for one launch");
     }
-    const int64_t nb_norm = (rows + 15) / 16, nb_ang = (ang + 255) / 256, nb_sc = blocks;
+    const int64_t nb_norm = (rows + 16 * kNormRows - 1) / (16 * kNormRows);
+    const int64_t nb_ang = (ang / 4 + 256 * kAngQuads - 1) / (256 * kAngQuads), nb_sc = blocks;
     if (run_prep && nb_norm + nb_ang + nb_sc > 0) {
       const dim3 pgrid(static_cast<unsigned>(nb_norm + nb_ang + nb_sc)), pblock(256);
       hipLaunchKernelGGL((prep_kernel<T, R>), pgrid, pblock, 0, stream, a, g,
