@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define M3_ABI_VERSION 2
+#define M3_ABI_VERSION 3
 
 /* Element types. */
 enum { M3_F32 = 0, M3_BF16 = 1, M3_F16 = 2 };
@@ -203,6 +203,30 @@ typedef struct {
 
 int m3_linear_workspace_size(const m3_linear_args* args, size_t* bytes);
 int m3_linear(const m3_linear_args* args, hipStream_t stream);
+
+/*
+ * The residual stream between mixers, one pass: s = x (+ add, summed in FP32 and rounded to x's
+ * dtype), optionally sum_out = s, and out = (s * rsqrt(mean(s^2) + eps)) * weight (the weight
+ * rounded to x's dtype, out rounded to out's dtype). It has no counterpart among the reference's
+ * plugin hooks: it replaces the block's residual add (mamba3/model.py:511-512), the RMSNorm that
+ * follows it (the next block's norm, model.py:48-55, 499-510, or norm_f, 591, 607) and, under
+ * autocast, the cast of the normed rows to the projection's dtype.
+ * dim is 256, 512, 768, 1024 or 2048; x, add and out of one 16-bit dtype, or an FP32 x with any
+ * add and out dtype; sum_out has x's dtype and may equal x; out overlaps nothing. Rows start
+ * 4-element aligned, innermost stride 1.
+ */
+typedef struct {
+  int64_t rows, dim;
+  float eps;
+  int32_t reserved;
+  m3_tensor x;          /* [rows, dim] */
+  m3_tensor add;        /* [rows, dim] optional */
+  m3_tensor weight;     /* [dim] */
+  m3_tensor sum_out;    /* [rows, dim] optional (needs add): x + add in x's dtype */
+  m3_tensor out;        /* [rows, dim] */
+} m3_rms_norm_args;
+
+int m3_rms_norm(const m3_rms_norm_args* args, hipStream_t stream);
 
 const char* m3_last_error(void);
 int m3_abi_version(void);

@@ -14,7 +14,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmamba3_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, BF16, F16 = 0, 1, 2
 PHASE_NONE, PHASE_GIVEN, PHASE_ANGLES = 0, 1, 2
@@ -87,8 +87,17 @@ class LinearArgs(ctypes.Structure):
     ]
 
 
+class RmsNormArgs(ctypes.Structure):
+    _fields_ = [
+        *[(n, ctypes.c_int64) for n in ("rows", "dim")],
+        ("eps", ctypes.c_float), ("reserved", ctypes.c_int32),
+        *[(n, _T) for n in ("x", "add", "weight", "sum_out", "out")],
+    ]
+
+
 ENTRY_POINTS = ("m3_scan_fwd", "m3_scan_workspace_size", "m3_chunk_state", "m3_step",
-                "m3_linear", "m3_linear_workspace_size", "m3_last_error", "m3_abi_version")
+                "m3_linear", "m3_linear_workspace_size", "m3_rms_norm", "m3_last_error",
+                "m3_abi_version")
 
 _lib: ctypes.CDLL | None = None
 
@@ -102,7 +111,7 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is not built; run `python -m mamba3_amd.build` (hipcc, gfx950)")
     lib = ctypes.CDLL(LIB_PATH)
-    for name in ("m3_scan_fwd", "m3_chunk_state", "m3_step", "m3_linear"):
+    for name in ("m3_scan_fwd", "m3_chunk_state", "m3_step", "m3_linear", "m3_rms_norm"):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]

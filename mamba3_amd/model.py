@@ -312,13 +312,44 @@ class Mamba3(nn.Module):
         dependency = sum(parameter.sum() * 0.0 for parameter in self.parameters())
         return x + dependency.to(dtype=x.dtype)
 
+    def _norm_dtype(self, h: torch.Tensor) -> torch.dtype:
+        """The dtype the next in_proj computes in: autocast's for FP32 rows, else the rows'."""
+        if h.dtype == torch.float32 and torch.is_autocast_enabled(h.device.type):
+            return torch.get_autocast_dtype(h.device.type)
+        return h.dtype
+
+    def _add_norm(self, h: torch.Tensor, mixed: torch.Tensor | None, norm: _RMSNorm,
+                  out_dtype: torch.dtype, keep_sum: bool):
+        """``(norm(h + mixed) as out_dtype, h + mixed)`` in one ``m3_rms_norm`` pass where it
+        applies (ROCm rows, no autograd, a supported width), else the reference's ops."""
+        sum_dtype = h.dtype if mixed is None else torch.promote_types(h.dtype, mixed.dtype)
+        if sum_dtype == h.dtype and ops.rms_norm_supported(h, norm.weight, mixed, out_dtype):
+            out, s = ops.rms_norm(h, norm.weight, norm.eps, add=mixed,
+                                  keep_sum=keep_sum and mixed is not None, out_dtype=out_dtype)
+            return out, (h if mixed is None else s)
+        s = h if mixed is None else h + mixed
+        return norm(s), s
+
+    def _run_layers(self, x: torch.Tensor, *, return_cache: bool):
+        """The layer loop of forward / prefill (reference ``model.py:585-607``): each block's
+        residual add runs fused with the RMSNorm after it (the next block's, or norm_f)."""
+        h, mixed, cache = x, None, []
+        for layer in self.layers:
+            normed, h = self._add_norm(h, mixed, layer.norm, self._norm_dtype(h), keep_sum=True)
+            if return_cache:
+                mixed, layer_cache = layer.mixer(normed, return_cache=True)
+                cache.append(layer_cache)
+            else:
+                mixed = layer.mixer(normed)
+        out, _ = self._add_norm(h, mixed, self.norm_f, h.dtype if mixed is None else
+                                torch.promote_types(h.dtype, mixed.dtype), keep_sum=False)
+        return out, cache
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         self._validate_input(x)
         if x.shape[0] == 0 or x.shape[1] == 0:
             return self._empty_output(x)
-        for layer in self.layers:
-            x = layer(x)
-        return self.norm_f(x)
+        return self._run_layers(x, return_cache=False)[0]
 
     def prefill(self, x: torch.Tensor):
         """Process a causal prefix and return the constant-size decode cache."""
@@ -327,11 +358,7 @@ class Mamba3(nn.Module):
         self._validate_input(x)
         if x.shape[0] == 0 or x.shape[1] == 0:
             raise ValueError("prefill requires a non-empty batch and sequence")
-        cache: list[_LayerCache] = []
-        for layer in self.layers:
-            x, layer_cache = layer(x, return_cache=True)
-            cache.append(layer_cache)
-        return self.norm_f(x), cache
+        return self._run_layers(x, return_cache=True)
 
     def step(self, x: torch.Tensor, cache: list[_LayerCache] | None = None, *,
              inplace: bool = False):

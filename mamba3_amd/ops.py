@@ -569,6 +569,83 @@ def linear(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor | None 
     return out
 
 
+# --------------------------------------------------------------------------- residual stream
+
+RMS_NORM_DIMS = (256, 512, 768, 1024, 2048)
+_FLOAT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _rows_ok(t: torch.Tensor) -> bool:
+    return t.is_contiguous() and t.data_ptr() % (4 * t.element_size()) == 0
+
+
+def rms_norm_supported(x: torch.Tensor, weight: torch.Tensor, add: torch.Tensor | None = None,
+                       out_dtype: torch.dtype | None = None) -> bool:
+    """Whether ``rms_norm`` takes these operands: contiguous rows on one ROCm device, the last
+    axis in ``RMS_NORM_DIMS``, an FP32 ``x`` with any ``add`` / ``out_dtype`` or a 16-bit ``x``
+    with both of its own dtype, and no autograd."""
+    out_dtype = out_dtype or x.dtype
+    if x.device.type != "cuda" or x.dim() < 1 or x.shape[-1] not in RMS_NORM_DIMS:
+        return False
+    if x.dtype not in _FLOAT_DTYPES or out_dtype not in _FLOAT_DTYPES:
+        return False
+    if weight.device != x.device or tuple(weight.shape) != (x.shape[-1],):
+        return False
+    if weight.dtype not in _FLOAT_DTYPES or not _rows_ok(x):
+        return False
+    if add is not None:
+        if add.device != x.device or add.shape != x.shape or not _rows_ok(add):
+            return False
+        if add.dtype not in _FLOAT_DTYPES or (x.dtype != torch.float32 and add.dtype != x.dtype):
+            return False
+    if x.dtype != torch.float32 and out_dtype != x.dtype:
+        return False
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, weight, add)):
+        return False
+    return True
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = NORM_EPS, *,
+             add: torch.Tensor | None = None, keep_sum: bool = False,
+             out_dtype: torch.dtype | None = None):
+    """One pass of the residual stream (``m3_rms_norm``): ``s = x + add`` (or ``x``), then
+    ``F.rms_norm(s, (d,), weight.to(s.dtype), eps)`` written as ``out_dtype`` (default
+    ``x.dtype``). Returns ``(out, s)`` with ``s`` only when ``keep_sum`` (``add`` given).
+
+    ``s`` is the reference's ``hidden_states + mixed`` (``model.py:511-512``; an FP32 ``x``
+    takes an ``add`` of any dtype), ``out`` its next RMSNorm (``model.py:48-55``) already in
+    the dtype the next projection computes in, so the add, the norm and autocast's cast are one
+    pass over the rows instead of three.
+    """
+    out_dtype = out_dtype or x.dtype
+    device = _require_device(x, weight, add)
+    _require_inference(x, weight, add)
+    if not rms_norm_supported(x, weight, add, out_dtype):
+        raise ValueError(f"rms_norm: unsupported operands x {tuple(x.shape)} {x.dtype}, add "
+                         f"{None if add is None else (tuple(add.shape), add.dtype)}, out "
+                         f"{out_dtype}")
+    if keep_sum and add is None:
+        raise ValueError("rms_norm: keep_sum needs add")
+    d = x.shape[-1]
+    rows = x.numel() // d
+    w = weight.detach()
+    if w.data_ptr() % (4 * w.element_size()) or not w.is_contiguous():
+        w = w.contiguous().clone()
+    out = torch.empty(x.shape, dtype=out_dtype, device=device)
+    s = torch.empty_like(x) if keep_sum else None
+    if rows == 0:
+        return out, s
+    args = _hip.RmsNormArgs()
+    args.rows, args.dim, args.eps = rows, d, float(eps)
+    args.x = _hip.tensor(x.view(rows, d))
+    args.add = _hip.tensor(None if add is None else add.view(rows, d))
+    args.weight = _hip.tensor(w)
+    args.sum_out = _hip.tensor(None if s is None else s.view(rows, d))
+    args.out = _hip.tensor(out.view(rows, d))
+    _hip.call("m3_rms_norm", args, device)
+    return out, s
+
+
 __all__ = ["heavy_tail_activation", "mamba3_scan", "mamba3_step", "fused_step", "chunk_state",
            "ScanCall", "scan_projection", "step_projection", "split_projection", "linear",
-           "linear_supported"]
+           "linear_supported", "rms_norm", "rms_norm_supported"]

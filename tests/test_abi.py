@@ -46,7 +46,7 @@ def _c_layout() -> dict[str, tuple[int, dict[str, int]]]:
         pytest.skip("gcc not available")
     structs = {"m3_tensor": _hip.Tensor, "m3_scan_args": _hip.ScanArgs,
                "m3_step_args": _hip.StepArgs, "m3_chunk_state_args": _hip.ChunkStateArgs,
-               "m3_linear_args": _hip.LinearArgs}
+               "m3_linear_args": _hip.LinearArgs, "m3_rms_norm_args": _hip.RmsNormArgs}
     lines = ['#include "mamba3_hip.h"', "#include <stdio.h>", "#include <stddef.h>",
              "int main(void) {"]
     for cname, py in structs.items():
@@ -79,7 +79,8 @@ def test_ctypes_structs_match_the_header_layout():
     for cname, py in (("m3_tensor", _hip.Tensor), ("m3_scan_args", _hip.ScanArgs),
                       ("m3_step_args", _hip.StepArgs),
                       ("m3_chunk_state_args", _hip.ChunkStateArgs),
-                      ("m3_linear_args", _hip.LinearArgs)):
+                      ("m3_linear_args", _hip.LinearArgs),
+                      ("m3_rms_norm_args", _hip.RmsNormArgs)):
         size, fields = layout[cname]
         assert ctypes.sizeof(py) == size, cname
         for field, _ in py._fields_:
@@ -87,7 +88,7 @@ def test_ctypes_structs_match_the_header_layout():
 
 
 def test_null_arguments_are_rejected_without_touching_the_device(lib):
-    for name in ("m3_scan_fwd", "m3_step", "m3_chunk_state", "m3_linear"):
+    for name in ("m3_scan_fwd", "m3_step", "m3_chunk_state", "m3_linear", "m3_rms_norm"):
         rc = getattr(lib, name)(None, None)
         assert rc == 1, name
         assert b"NULL" in lib.m3_last_error()
@@ -233,3 +234,38 @@ def test_scan_backwards_token_strides_on_the_host(lib):
     args.value.stride[1] = -args.value.stride[1]
     assert lib.m3_scan_fwd(ctypes.byref(args), None) == 1
     assert b"run the same way" in lib.m3_last_error()
+
+
+def _norm_args(rows: int, dim: int, x_dtype=_hip.F32, out_dtype=_hip.BF16) -> _hip.RmsNormArgs:
+    """m3_rms_norm arguments with fake, aligned device pointers: only host checks run on them."""
+    args = _hip.RmsNormArgs(rows=rows, dim=dim, eps=1e-5)
+    for name, ptr, dt in (("x", 0x100000, x_dtype), ("weight", 0x200000, _hip.F32),
+                          ("out", 0x300000, out_dtype)):
+        t = getattr(args, name)
+        t.ptr, t.dtype = ptr, dt
+        t.stride[0], t.stride[1] = (dim, 1) if name != "weight" else (1, 0)
+    return args
+
+
+def test_rms_norm_validation_on_the_host(lib):
+    args = _norm_args(0, 1024)
+    assert lib.m3_rms_norm(ctypes.byref(args), None) == 0  # no rows: nothing to launch
+    args = _norm_args(8, 384)
+    assert lib.m3_rms_norm(ctypes.byref(args), None) == 2
+    assert b"multiple of 256" in lib.m3_last_error()
+    args = _norm_args(8, 1024)
+    args.sum_out.ptr, args.sum_out.dtype = 0x400000, _hip.F32
+    args.sum_out.stride[0], args.sum_out.stride[1] = 1024, 1
+    assert lib.m3_rms_norm(ctypes.byref(args), None) == 1
+    assert b"sum_out needs add" in lib.m3_last_error()
+    args = _norm_args(8, 1024)
+    args.out.ptr = 0x100000 + 4 * 1024  # inside x's rows
+    assert lib.m3_rms_norm(ctypes.byref(args), None) == 1
+    assert b"overlaps" in lib.m3_last_error()
+    args = _norm_args(8, 1024, x_dtype=_hip.BF16, out_dtype=_hip.F32)
+    assert lib.m3_rms_norm(ctypes.byref(args), None) == 2
+    assert b"own dtype" in lib.m3_last_error()
+    args = _norm_args(8, 1024)
+    args.x.stride[0] = 1026  # rows not 4-element aligned
+    assert lib.m3_rms_norm(ctypes.byref(args), None) == 2
+    assert b"aligned" in lib.m3_last_error()
