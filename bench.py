@@ -380,8 +380,8 @@ def main() -> None:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: the Mamba-3 hot path of this build runs on a single "
-              "MI355X (batch and heads shard without communication; see DESIGN.md).",
-              file=sys.stderr)
+              "MI355X (the (batch, head) recurrences shard over GPUs without communication; a "
+              "multi-GPU run is not part of this build).", file=sys.stderr)
         sys.exit(2)
 
     def log(msg):
