@@ -42,6 +42,17 @@ def _default_chunk_sizes(mimo_rank: int) -> tuple[int, int]:
     return training, inference
 
 
+_SIDE_STREAMS: dict[torch.device, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for the reverse scan of a bidirectional
+    layer."""
+    if device not in _SIDE_STREAMS:
+        _SIDE_STREAMS[device] = torch.cuda.Stream(device=device)
+    return _SIDE_STREAMS[device]
+
+
 class _RMSNorm(nn.Module):
     def __init__(self, dim: int, eps: float = 1e-5) -> None:
         super().__init__()
@@ -162,6 +173,16 @@ class _Mamba3Mixer(nn.Module):
                              "prefill and step require causal=True")
         self._check_inference(hidden_states)
         proj = self.in_proj(hidden_states)
+        if not self.causal:
+            # the reverse scan on a side stream, concurrent with the forward one: each direction
+            # alone may leave CUs idle in its last round of workgroups
+            main = torch.cuda.current_stream(proj.device)
+            side = _side_stream(proj.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                mixed_r, _, _, _ = ops.scan_projection(proj, self, chunk_size=self._chunk(),
+                                                       reverse=True)
+            proj.record_stream(side)
         mixed, state, final_phase, final_k = ops.scan_projection(
             proj, self, cache=cache, want_cache=return_cache and self.causal,
             chunk_size=self._chunk())
@@ -173,11 +194,11 @@ class _Mamba3Mixer(nn.Module):
                 -1, (self.nheads, self.headdim)).clone()
             return output, (final_phase, state, final_k, last_value)
         # Bidirectional (model.py:330-362): the reversed sequence with the same weights. The
-        # projection is per token, so in_proj(flip(x)) = flip(in_proj(x)): the reverse scan reads
-        # this projection backwards and writes its output back in forward order (no flip, no
-        # second projection).
-        mixed_r, _, _, _ = ops.scan_projection(proj, self, chunk_size=self._chunk(),
-                                               reverse=True)
+        # projection is per token, so in_proj(flip(x)) = flip(in_proj(x)): the reverse scan
+        # (launched above) reads this projection backwards and writes its output back in forward
+        # order (no flip, no second projection).
+        main.wait_stream(side)
+        mixed_r.record_stream(main)
         backward = self.out_proj(mixed_r.flatten(-2))
         blend = torch.sigmoid(self.direction_logit).to(dtype=output.dtype)
         return output * blend + backward * (1.0 - blend)
