@@ -607,10 +607,13 @@ struct Feed {
 
 // Column of angle `col` in the cos / sin table row of token tt. SWZ (64-token sub-chunks, 32
 // angles): blocks of 4 angles are XOR-swizzled by the token's 16-token block, spreading the
-// phase stage's column writes over the LDS banks while a reader's 4-angle block stays whole.
+// phase stage's column writes over the LDS banks, and the two angle pairs of a block swap places
+// in every other token pair, so the 16-byte reads of two token rows 2 apart (136 floats: the
+// same banks shifted by 8) fall into different halves of each 8-float group. A reader takes a
+// block as two pairs, each at its own cs_col.
 template <bool SWZ>
 __device__ __forceinline__ int cs_col(int col, int tt) {
-  return SWZ ? col ^ (4 * ((tt >> 4) & 3)) : col;
+  return SWZ ? col ^ (4 * ((tt >> 4) & 3)) ^ (2 * ((tt >> 1) & 1)) : col;
 }
 
 // Bounded phase (model.py:215-256) of tokens TPL pg .. TPL pg + TPL-1 of the sub-chunk at t0 for
@@ -1266,9 +1269,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         if constexpr (SPLIT) {
           // pairs (2j, 2j+1), j = n0/2 .. n0/2+3: the rotated columns are waves 0-3's
           if constexpr (ROT) {
-            const float* tr = CSt + tt * CST + 2 * cs_col<true>(n0 >> 1, tt);
-            const f4 c01 = *reinterpret_cast<const f4*>(tr);      // c0 s0 c1 s1
-            const f4 c23 = *reinterpret_cast<const f4*>(tr + 4);  // c2 s2 c3 s3
+            const float* tr = CSt + tt * CST;
+            const f4 c01 = *reinterpret_cast<const f4*>(tr + 2 * cs_col<true>(n0 >> 1, tt));
+            const f4 c23 = *reinterpret_cast<const f4*>(tr + 2 * cs_col<true>((n0 >> 1) + 2, tt));
+            // c01 = c0 s0 c1 s1, c23 = c2 s2 c3 s3
 #pragma unroll
             for (int pp = 0; pp < 4; ++pp) {
               const f4& cv = pp < 2 ? c01 : c23;
