@@ -255,6 +255,37 @@ def bench_prefill_config(name, d_model, depth, rank, causal, shape, seed, log, i
     return out
 
 
+def bench_chunk_state(log, batch=8, heads=32, width=256, rank=1, n=128, p=64):
+    """The standalone per-chunk state update (``m3_chunk_state``) at config 2's chunk shape:
+    one chunk of ``width`` tokens for every (batch, head), bf16 k / values, FP32 state."""
+    from mamba3_amd import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(5)
+    k = torch.randn(batch, heads, width, rank, n, device=dev, generator=gen).to(torch.bfloat16)
+    v = torch.randn(batch, heads, width, rank, p, device=dev, generator=gen).to(torch.bfloat16)
+    cum = -torch.rand(batch, heads, width, device=dev, generator=gen).cumsum(-1) * 0.01
+    scale = torch.rand(batch, heads, width, device=dev, generator=gen) * 0.1
+    state = torch.randn(batch, heads, p, n, device=dev, generator=gen)
+    out = torch.empty_like(state)
+
+    def call():
+        ops.chunk_state(k, v, cum, scale, state, out, width=width, rank=rank)
+
+    with torch.inference_mode():
+        for _ in range(50):
+            call()
+        t = _events_time(call, 200) / 200
+    nbytes = (batch * heads * width * rank * (n + p) * 2 + batch * heads * width * 8
+              + 2 * batch * heads * p * n * 4)
+    gbs = nbytes / t / 1e9
+    log(f"chunk_state B={batch} H={heads} W={width}: {t * 1e6:.2f} us, {gbs:.0f} GB/s")
+    return dict(us=round(t * 1e6, 2), bytes=nbytes, bound="hbm", achieved=round(gbs, 1),
+                peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
+                kernel="m3::chunk_state_kernel<__bf16>",
+                shape=f"[{batch}, {heads}] x {width} tokens, R={rank}, N={n}, P={p}")
+
+
 def bench_cpu(log, batch=8, length=8192):
     """The CPU oracle (portable-path restatement) on the prefill scan, ``x[batch, length]``."""
     from oracle import portable as op
@@ -372,7 +403,8 @@ def main() -> None:
     ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--extra", action="store_true",
                     help="also measure BASELINE configs 3, 5 and config 4 at B=1/64 and R=4")
-    ap.add_argument("--extra-only", choices=("config3", "config5", "config5_long", "decode"),
+    ap.add_argument("--extra-only", choices=("config3", "config5", "config5_long", "decode",
+                                             "chunk_state"),
                     help="with --extra: measure only this one of the extra configurations")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates PMC byte counters)")
@@ -403,6 +435,7 @@ def main() -> None:
             "config4_decode": ("decode", lambda: [
                 bench_decode(b, args.decode_steps, log, rank=r)
                 for b, r in ((1, 1), (64, 1), (256, 4), (64, 4), (1, 4))]),
+            "chunk_state_config2": ("chunk_state", lambda: bench_chunk_state(log)),
         }
         extra = {name: run() for name, (key, run) in runs.items()
                  if args.extra_only in (None, key)}

@@ -1,6 +1,8 @@
 // Standalone per-chunk state update (m3_chunk_state), the replacement of the reference's
 // chunk_state launcher (_triton.py:500-561) for callers that drive the chunk loop themselves.
 // The fused scan (scan.hip) carries the state in registers and does not use it.
+#include <type_traits>
+
 #include "m3_common.hpp"
 #include "m3_host.hpp"
 
@@ -84,6 +86,145 @@ __global__ __launch_bounds__(kCsThreads) void chunk_state_kernel(const m3_chunk_
   }
 }
 
+// The model's shape (N = 128, P = 64) with 16-bit activations, on MFMA: the update V^T ke of
+// (b, h) is 32 tiles of S'^T (16 columns n x 16 rows p), accumulated over passes of kCmRows
+// (token, rank) rows with bf16 / f16 16x16x32 MFMAs (exact products of the rounded operands,
+// FP32 sums, as the reference's bmm). Each pass stages ke (the same rounding points as above)
+// and v transposed into LDS ([n][row], [p][row]); a lane stores a row pair of 8 columns, with
+// the row pairs on consecutive lanes so a store instruction's 32 lanes hit 32 banks. The global
+// loads of pass i + 1 are issued before the MFMAs of pass i. Wave w owns
+// rows p = 16 w .. 16 w + 15, all 8 column tiles; lane l ends with S'[p][n .. n+3] of each tile
+// in the MFMA output layout, one 16-byte vector of the state row.
+constexpr int kCmRows = 64;
+
+template <typename T>
+__global__ __launch_bounds__(kCsThreads) void chunk_state_mma_kernel(const m3_chunk_state_args a) {
+  constexpr int N = 128, P = 64, LR = kCmRows + 8, NT = N / 16;
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  const int H = a.heads, W = a.width, R = a.rank;
+  const int b = blockIdx.x / H, h = blockIdx.x - (blockIdx.x / H) * H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+  __shared__ __align__(16) T KeT[N * LR];
+  __shared__ __align__(16) T VT[P * LR];
+  const float* cum = static_cast<const float*>(a.cumulative.ptr) + b * a.cumulative.stride[0] +
+                     h * a.cumulative.stride[1];
+  const float* scl = static_cast<const float*>(a.scale.ptr) + b * a.scale.stride[0] +
+                     h * a.scale.stride[1];
+  const T* kb = static_cast<const T*>(a.k.ptr) + b * a.k.stride[0] + h * a.k.stride[1];
+  const T* vb = static_cast<const T*>(a.value.ptr) + b * a.value.stride[0] + h * a.value.stride[1];
+  const float cl = cum[(W - 1) * a.cumulative.stride[2]];
+  const int rows = W * R;
+  f4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
+  const int rp = tid & 31;  // row pair of the staging tasks
+  // the raw operands of one pass: every load issues unconditionally (rows past the end re-read
+  // row 0 and stage zeros), so the next pass's loads fly during this pass's MFMAs
+  t8 kr[2][2], vr[2];
+  float sr[2], cr[2];
+  auto load = [&](int r0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int jr = 0; jr < 2; ++jr) {
+      const int row = r0 + 2 * rp + jr;
+      const int t = row < rows ? row / R : 0, r = row < rows ? row - t * R : 0;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n0 = 8 * ((tid >> 5) + 8 * j);
+        kr[j][jr] = *reinterpret_cast<const t8*>(kb + t * a.k.stride[2] + r * a.k.stride[3] + n0);
+      }
+      vr[jr] = *reinterpret_cast<const t8*>(vb + t * a.value.stride[2] + r * a.value.stride[3] +
+                                             8 * (tid >> 5));
+      sr[jr] = scl[t * a.scale.stride[2]];
+      cr[jr] = cum[t * a.cumulative.stride[2]];
+    }
+  };
+  load(0);
+  for (int r0 = 0; r0 < rows; r0 += kCmRows) {
+    __syncthreads();  // the previous pass's operands are read
+    // ke rows 2 rp, 2 rp + 1, columns 8 cg .. 8 cg + 7 (two column groups per thread), then v
+    typedef T t2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n0 = 8 * ((tid >> 5) + 8 * j);
+      float ke[2][8];
+#pragma unroll
+      for (int jr = 0; jr < 2; ++jr) {
+        const bool ok = r0 + 2 * rp + jr < rows;
+        const float sc = rnd<T>(sr[jr]);
+        const float ee = rnd<T>(expf(cl - cr[jr]));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          ke[jr][i] = ok ? mul_r<T>(mul_r<T>(to_f(kr[j][jr][i]), sc), ee) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        *reinterpret_cast<t2*>(&KeT[(n0 + i) * LR + 2 * rp]) =
+            t2{from_f<T>(ke[0][i]), from_f<T>(ke[1][i])};
+      }
+    }
+    {
+      const int p0 = 8 * (tid >> 5);
+      const bool ok0 = r0 + 2 * rp < rows, ok1 = r0 + 2 * rp + 1 < rows;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        *reinterpret_cast<t2*>(&VT[(p0 + i) * LR + 2 * rp]) =
+            t2{ok0 ? vr[0][i] : from_f<T>(0.f), ok1 ? vr[1][i] : from_f<T>(0.f)};
+      }
+    }
+    load(r0 + kCmRows < rows ? r0 + kCmRows : 0);  // (the last pass re-reads pass 0, unused)
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < kCmRows / 32; ++ks) {
+      const t8 bv = *reinterpret_cast<const t8*>(&VT[(16 * w + l16) * LR + 32 * ks + 8 * lg]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const t8 av = *reinterpret_cast<const t8*>(&KeT[(16 * nt + l16) * LR + 32 * ks + 8 * lg]);
+        if constexpr (std::is_same<T, __bf16>::value) {
+          acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[nt], 0, 0, 0);
+        } else {
+          acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[nt], 0, 0, 0);
+        }
+      }
+    }
+  }
+  const float ecl = expf(cl);
+  const int p = 16 * w + l16;
+  const float* sin_ = static_cast<const float*>(a.state_in.ptr) + b * a.state_in.stride[0] +
+                      h * a.state_in.stride[1] + p * a.state_in.stride[2];
+  float* sout = static_cast<float*>(a.state_out.ptr) + b * a.state_out.stride[0] +
+                h * a.state_out.stride[1] + p * a.state_out.stride[2];
+  f4 old[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) old[nt] = *reinterpret_cast<const f4*>(sin_ + 16 * nt + 4 * lg);
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    f4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = ecl * old[nt][i] + acc[nt][i];
+    *reinterpret_cast<f4*>(sout + 16 * nt + 4 * lg) = o;
+  }
+}
+
+// The MFMA form's operand conditions: the model's shape, 16-bit k / value with 16-byte aligned
+// rows of 8-element groups, 16-byte aligned state rows.
+bool chunk_state_mma_ok(const m3_chunk_state_args& a) {
+  if (a.act_dtype == M3_F32 || a.d_state != 128 || a.head_dim != 64) return false;
+  for (const m3_tensor* t : {&a.k, &a.value}) {
+    if (reinterpret_cast<uintptr_t>(t->ptr) % 16 != 0) return false;
+    for (int i = 0; i < 4; ++i) {
+      if (t->stride[i] % 8 != 0) return false;
+    }
+  }
+  for (const m3_tensor* t : {&a.state_in, &a.state_out}) {
+    if (reinterpret_cast<uintptr_t>(t->ptr) % 16 != 0) return false;
+    for (int i = 0; i < 3; ++i) {
+      if (t->stride[i] % 4 != 0) return false;
+    }
+  }
+  return true;
+}
+
 }  // namespace m3
 
 extern "C" int m3_chunk_state(const m3_chunk_state_args* args, hipStream_t stream) {
@@ -113,6 +254,14 @@ extern "C" int m3_chunk_state(const m3_chunk_state_args* args, hipStream_t strea
   }
   if (a.batch == 0) return M3_OK;
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kCsThreads);
+  if (chunk_state_mma_ok(a)) {
+    if (act == M3_BF16) {
+      hipLaunchKernelGGL(chunk_state_mma_kernel<__bf16>, grid, block, 0, stream, a);
+    } else {
+      hipLaunchKernelGGL(chunk_state_mma_kernel<_Float16>, grid, block, 0, stream, a);
+    }
+    return check_launch("m3_chunk_state");
+  }
   switch (act) {
     case M3_F32: hipLaunchKernelGGL(chunk_state_kernel<float>, grid, block, lds, stream, a); break;
     case M3_BF16: hipLaunchKernelGGL(chunk_state_kernel<__bf16>, grid, block, lds, stream, a); break;

@@ -189,10 +189,11 @@ def test_scan_continuation(rank):
     torch.testing.assert_close(s2, full_state, rtol=1e-4, atol=1e-4)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rank", [1, 4])
 def test_chunk_state_matches_oracle(dtype, rank):
-    """The standalone per-chunk state update (reference _triton.py:500-561)."""
+    """The standalone per-chunk state update (reference _triton.py:500-561); 16-bit operands at
+    this shape take the MFMA form (37 x rank rows: passes of 64 with a ragged last one)."""
     g = torch.Generator().manual_seed(4)
     batch, heads, width, p, n = 2, 3, 37, 64, 128
     k = torch.randn(batch, heads, width, rank, n, generator=g).to(dtype)
