@@ -286,6 +286,47 @@ def bench_chunk_state(log, batch=8, heads=32, width=256, rank=1, n=128, p=64):
                 shape=f"[{batch}, {heads}] x {width} tokens, R={rank}, N={n}, P={p}")
 
 
+def bench_hook_scan(log, batch=8, length=8192, heads=32, p=64, n=128):
+    """The reference's scan hook boundary (``mamba3_scan``: normed q / k, head-expanded value /
+    gate, FP32 adt / dt, trap logits and the materialized phases [B, L, H, S] FP32) at config 2's
+    shape, bf16: the generic kernel path, which reads the inputs as given."""
+    from mamba3_amd import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(6)
+    bf = torch.bfloat16
+    s = n // 4
+
+    def rnd(*shape, dtype=torch.float32):
+        return torch.randn(*shape, device=dev, generator=gen).to(dtype)
+
+    dt = torch.rand(batch, length, heads, device=dev, generator=gen) * 0.1 + 0.001
+    inp = dict(q=rnd(batch, length, 1, 1, n, dtype=bf), k=rnd(batch, length, 1, 1, n, dtype=bf),
+               value=rnd(batch, length, heads, p, dtype=bf),
+               gate=rnd(batch, length, heads, p, dtype=bf),
+               adt=-dt * torch.rand(batch, length, heads, device=dev, generator=gen), dt=dt,
+               trap_logits=rnd(batch, length, heads, dtype=bf), D=rnd(heads),
+               phase=(torch.rand(batch, length, heads, s, device=dev, generator=gen) * 2 - 1) * 6.28,
+               q_bias=1 + 0.1 * rnd(heads, 1, n), k_bias=1 + 0.1 * rnd(heads, 1, n))
+
+    def call():
+        ops.mamba3_scan(**inp, chunk_size=256)
+
+    with torch.inference_mode():
+        for _ in range(20):
+            call()
+        t = _events_time(call, 50) / 50
+    tokens = batch * length
+    nbytes = (tokens * (2 * n * 2 + 2 * heads * p * 2 + heads * (4 + 4 + 2) + heads * s * 4)
+              + tokens * heads * p * 2)
+    gbs = nbytes / t / 1e9
+    log(f"hook scan (mamba3_scan, given phases) {batch}x{length}: {t * 1e6:.1f} us, "
+        f"{tokens / t:.4e} tok/s, {gbs:.0f} GB/s")
+    return dict(us=round(t * 1e6, 1), tok_s=round(tokens / t, 1), bytes=nbytes, bound="hbm",
+                achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(gbs / HBM_PEAK_GBS, 4))
+
+
 def bench_cpu(log, batch=8, length=8192):
     """The CPU oracle (portable-path restatement) on the prefill scan, ``x[batch, length]``."""
     from oracle import portable as op
@@ -404,7 +445,7 @@ def main() -> None:
     ap.add_argument("--extra", action="store_true",
                     help="also measure BASELINE configs 3, 5 and config 4 at B=1/64 and R=4")
     ap.add_argument("--extra-only", choices=("config3", "config5", "config5_long", "decode",
-                                             "chunk_state"),
+                                             "chunk_state", "hook"),
                     help="with --extra: measure only this one of the extra configurations")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates PMC byte counters)")
@@ -436,6 +477,7 @@ def main() -> None:
                 bench_decode(b, args.decode_steps, log, rank=r)
                 for b, r in ((1, 1), (64, 1), (256, 4), (64, 4), (1, 4))]),
             "chunk_state_config2": ("chunk_state", lambda: bench_chunk_state(log)),
+            "hook_scan_config2": ("hook", lambda: bench_hook_scan(log)),
         }
         extra = {name: run() for name, (key, run) in runs.items()
                  if args.extra_only in (None, key)}
