@@ -941,7 +941,11 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
 // decay, last k and phase block sums but no outputs. The stores of Qs, VR, ZR, Sb and the output
 // are left out, and with them (dead code) the q math, the scores, the decay weights, the intra
 // and inter products and the epilogue; k, the carry tiles and products and the phase remain.
-template <typename T, int R, bool FULL, bool SO = false>
+//
+// SHAPE (without FULL): the model's shape (N = 128, P = 64, 32 angles when rotating, aligned
+// 16-byte rows) with the generic inputs (the hook form): the dimensions and the vector-load
+// choice are compile-time constants, the features and pointers stay runtime.
+template <typename T, int R, bool FULL, bool SO = false, bool SHAPE = false>
 __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, const ScanGeom g,
                                                         const float* __restrict__ prep) {
   using M = Mma<T>;
@@ -964,16 +968,17 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // 16 distinct bank groups (8- and 16-byte LDS accesses see 64 banks)
   constexpr int KSH = F32 ? 3 : 4, VSH = F32 ? 2 : 4;
   // FULL: the model's shape (N = 128, P = 64, S = 32) in projection form with vector loads
-  const int N = FULL ? kNPad : a.d_state;
-  const int P = FULL ? kPPad : a.head_dim;
-  const int S = FULL ? kSMax : a.num_angles;
+  constexpr bool FIX = FULL || SHAPE;  // the model's shape, fixed at compile time
+  const int N = FIX ? kNPad : a.d_state;
+  const int P = FIX ? kPPad : a.head_dim;
+  const int S = FIX ? kSMax : a.num_angles;
   const bool norm = FULL || g.ws_norm >= 0;
   const bool bias = FULL || a.q_bias.ptr != nullptr;
   const bool rotate = FULL || a.phase_mode != M3_PHASE_NONE;
   const bool angles = FULL || a.phase_mode == M3_PHASE_ANGLES;
   const bool raw_dt = FULL || a.raw_dt != 0;
   const bool mimo_rot = FULL ? (R > 1) : (a.mimo_rotation != 0);
-  const bool vec_qk = FULL || g.vec_qk, vec_vz = FULL || g.vec_vz;
+  const bool vec_qk = FIX || g.vec_qk, vec_vz = FIX || g.vec_vz;
   const int H = a.heads, L = a.length;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (wave-uniform)
@@ -1331,7 +1336,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int n = n0 + i;
-        if (FULL || n < N) {
+        if (FIX || n < N) {
           st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> KSH), kt[0][i] * e0, kt[1][i] * e1);
         }
       }
@@ -1366,7 +1371,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           const int p = p0 + i;
           const uint32_t pr = __builtin_amdgcn_perm(rv[1][i >> 1], rv[0][i >> 1],
                                                     (i & 1) ? 0x07060302u : 0x05040100u);
-          if (FULL || p < P) *reinterpret_cast<uint32_t*>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH)) = pr;
+          if (FIX || p < P) *reinterpret_cast<uint32_t*>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH)) = pr;
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -1378,7 +1383,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int p = p0 + i;
-          if (FULL || p < P) st_pair<T>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH), v[0][i], v[1][i]);
+          if (FIX || p < P) st_pair<T>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH), v[0][i], v[1][i]);
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -1414,7 +1419,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int p = p0 + i;
-          if (FULL || p < P) {
+          if (FIX || p < P) {
             st_pair<T>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH), vq[0][i], vq[1][i]);
           }
         }
@@ -2210,12 +2215,19 @@ static bool full_shape(const m3_scan_args& a, ScanGeom& g, int R) {
          g.vec_vz && projection_form(a, g, a.act_dtype == M3_F32 ? 4 : 2);
 }
 
-template <typename T, int R, bool FULL, bool SO = false>
+// The model's shape with the generic inputs (scan_kernel's SHAPE form): N = 128, P = 64, 32
+// angles when rotating, one group, vector-aligned q / k and value / gate rows.
+static bool model_shape(const m3_scan_args& a, const ScanGeom& g) {
+  return a.d_state == kNPad && a.head_dim == kPPad && a.groups == 1 && g.vec_qk && g.vec_vz &&
+         (a.phase_mode == M3_PHASE_NONE || a.num_angles == kSMax);
+}
+
+template <typename T, int R, bool FULL, bool SO = false, bool SHAPE = false>
 static int launch_kernel(const m3_scan_args& a, const ScanGeom& g, const float* prep, dim3 grid,
                          dim3 block, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel<T, R, FULL, SO>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel<T, R, FULL, SO, SHAPE>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        Layout<T>::BYTES);
     if (e != hipSuccess) {
@@ -2223,8 +2235,8 @@ static int launch_kernel(const m3_scan_args& a, const ScanGeom& g, const float* 
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((scan_kernel<T, R, FULL, SO>), grid, block, Layout<T>::BYTES, stream, a, g,
-                     prep);
+  hipLaunchKernelGGL((scan_kernel<T, R, FULL, SO, SHAPE>), grid, block, Layout<T>::BYTES, stream,
+                     a, g, prep);
   return check_launch("m3_scan_fwd");
 }
 
@@ -2270,6 +2282,7 @@ static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep,
     }
     return launch_kernel<T, R, true>(a, g, prep, grid, block, stream);
   }
+  if (model_shape(a, g)) return launch_kernel<T, R, false, false, true>(a, g, prep, grid, block, stream);
   return launch_kernel<T, R, false>(a, g, prep, grid, block, stream);
 }
 
