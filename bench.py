@@ -71,16 +71,16 @@ def _events_time(fn, iters):
     return start.elapsed_time(end) / 1000.0
 
 
-def _traffic_from_profile(path):
-    """HBM bytes per m3_scan_fwd call as recorded by the committed PMC summary (or None).
+def _traffic_from_profile(path, key="traffic_bytes_per_call:"):
+    """HBM bytes per call or launch as recorded by a committed PMC summary (or None).
 
-    The summary holds one line ``traffic_bytes_per_call: <int>``: FETCH_SIZE and WRITE_SIZE
-    of the prep and scan kernels, each scaled by the counter's reading for a copy of known size.
+    The summary holds one line ``<key> <int>``: FETCH_SIZE and WRITE_SIZE of the measured
+    kernels, each scaled by the counter's reading for a copy of known size.
     """
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_call:"):
+                if line.startswith(key):
                     return int(line.split(":", 1)[1].strip())
     except OSError:
         return None
@@ -206,10 +206,15 @@ def bench_decode(batch, steps, log, rank=1, prefix=2048):
     tok_s = steps * batch / t
     log(f"decode B={batch} R={rank}: {t / steps * 1e3:.3f} ms/step, {tok_s:.1f} tok/s; "
         f"step kernel {t_k * 1e6:.1f} us, {gbs:.0f} GB/s")
+    # HBM bytes per launch from the committed counter summary (rank 1 at B = 256 only)
+    traffic = None
+    if rank == 1 and batch == 256:
+        traffic = _traffic_from_profile(os.path.join(ROOT, "profiles", "step_decode_b256_pmc.txt"),
+                                        key="traffic_bytes_per_launch:")
     return dict(batch=batch, rank=rank, steps=steps, tok_s=round(tok_s, 1),
                 ms_per_step=round(t / steps * 1e3, 4),
                 step_kernel=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS,
-                                 unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
+                                 unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4), traffic=traffic,
                                  us_per_launch=round(t_k * 1e6, 2), bytes_per_launch=nb,
                                  kernel=step_kernel_name(batch * mixer.nheads, rank)))
 
