@@ -196,10 +196,28 @@ def bench_decode(batch, steps, log, rank=1, prefix=2048):
         def step_kernel():
             ops.step_projection(proj, mixer, layer_cache, inplace=True)
 
-        for _ in range(3):
-            step_kernel()
         iters = 20
-        t_k = _events_time(step_kernel, iters) / iters
+        if batch * mixer.nheads >= 1024:
+            # eager calls: the launch is GPU-bound at this size
+            for _ in range(3):
+                step_kernel()
+            t_k = _events_time(step_kernel, iters) / iters
+        else:
+            # small batches: eager calls would time the host, so a captured graph of
+            # back-to-back steps, as the decoder runs them
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    step_kernel()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(iters):
+                    step_kernel()
+            graph.replay()
+            torch.cuda.synchronize()
+            t_k = _events_time(graph.replay, 5) / (5 * iters)
     nb = decode_bytes_per_layer_row(mixer.nheads, mixer.headdim, 128, mixer.num_angles,
                                     rank) * batch
     gbs = nb / t_k / 1e9
