@@ -336,7 +336,7 @@ def bench_hook_scan(log, batch=8, length=8192, heads=32, p=64, n=128):
         ops.mamba3_scan(**inp, chunk_size=256)
 
     with torch.inference_mode():
-        for _ in range(20):
+        for _ in range(50):  # past the clock ramp of sustained load
             call()
         t = _events_time(call, 50) / 50
     tokens = batch * length

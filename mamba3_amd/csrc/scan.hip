@@ -397,9 +397,11 @@ __device__ __forceinline__ void bstore_elem(float x, __amdgpu_buffer_rsrc_t r, i
 // consecutive tokens of one angle per 16-byte word, TOK * S floats). FULL: every per-token input
 // is a slice of one projection row (host-checked), read at per-lane byte offsets through one
 // buffer resource per batch row whose extent ends at token L, so rows of tokens >= L read as
-// zero without guards; the workspace likewise through one resource. Otherwise element pointers
-// with explicit guards.
-template <typename T, int R, bool FULL>
+// zero without guards; the workspace likewise through one resource. BUF (the model's shape with
+// the generic inputs, host-checked): the same guard-free reads through one resource per input
+// tensor and (batch, head), whose extent ends at token L, at 32-bit per-lane offsets. Otherwise
+// element pointers with explicit guards.
+template <typename T, int R, bool FULL, bool BUF = false>
 struct Feed {
   static constexpr int ES = sizeof(T), W8 = Words<T>::W8, W4 = Words<T>::W4;
   static constexpr int ROWS = Mma<T>::ROWS, TOK = ROWS / R;
@@ -408,6 +410,10 @@ struct Feed {
   __amdgpu_buffer_rsrc_t rs_p, rs_w;
   int o_qk, o_vz, d_q1, d_k, d_z, tok_b;  // per-lane byte offsets at token 0, uniform deltas
   int side_o, side_s, ang_o, ang_s;        // per-lane workspace byte offsets at sub-chunk 0, strides
+  // BUF: resources of q, k, value, gate and the given phases; per-lane byte offsets at token 0,
+  // the byte strides of a token and the second row's delta
+  __amdgpu_buffer_rsrc_t rs_q, rs_k, rs_v, rs_z, rs_x;
+  int o_q, o_k, o_v, o_z, o_x, tq_b, tk_b, tv_b, tz_b, tx_b, d_q2, d_k2;
   // generic
   const T *q_row, *k_row, *v_row, *z_row;
   const float *side_p, *ang_p;  // this lane's side / angle word at sub-chunk 0 (null: none)
@@ -455,6 +461,56 @@ struct Feed {
       }
       ang_o = static_cast<int>(g.ws_ang + static_cast<int64_t>(b) * g.L4 * S * 4 + 4 * tid) * 4;
       ang_s = (TOK / 4) * S * 16;
+    } else if constexpr (BUF) {
+      rs_w = make_rsrc(prep, g.ws_bytes);
+      // every token stride is positive and a token's row ends below the next token's (host),
+      // so rows of tokens >= L lie past the extent L * stride and read as zero
+      const char* q0 = static_cast<const char*>(a.q.ptr) + b * a.q.stride[0] * ES;
+      const char* k0 = static_cast<const char*>(a.k.ptr) + b * a.k.stride[0] * ES;
+      const char* v0 = static_cast<const char*>(a.value.ptr) +
+                       (b * a.value.stride[0] + h * a.value.stride[2]) * ES;
+      const char* z0 = static_cast<const char*>(a.gate.ptr) +
+                       (b * a.gate.stride[0] + h * a.gate.stride[2]) * ES;
+      tq_b = static_cast<int>(a.q.stride[1]) * ES;
+      tk_b = static_cast<int>(a.k.stride[1]) * ES;
+      tv_b = static_cast<int>(a.value.stride[1]) * ES;
+      tz_b = static_cast<int>(a.gate.stride[1]) * ES;
+      rs_q = make_rsrc(q0, L * tq_b);
+      rs_k = make_rsrc(k0, L * tk_b);
+      rs_v = make_rsrc(v0, L * tv_b);
+      rs_z = make_rsrc(z0, L * tz_b);
+      const int qr_b = static_cast<int>(a.q.stride[3]) * ES, kr_b = static_cast<int>(a.k.stride[3]) * ES;
+      o_q = tt0 * tq_b + r0 * qr_b + n0 * ES;
+      o_k = tt0 * tk_b + r0 * kr_b + n0 * ES;
+      d_q2 = R == 1 ? tq_b : qr_b;  // row 2rp + 1: the next token (R = 1) or the next rank
+      d_k2 = R == 1 ? tk_b : kr_b;
+      const int tv = R == 1 ? 2 * vp : (2 * vp) / R;
+      o_v = tv * tv_b + p0 * ES;
+      o_z = tv * tz_b + p0 * ES;
+      // side and angle words as in the projection form (groups == 1); no norm: unused words
+      if (q2 < scw) {
+        side_o = static_cast<int>(sc0) * 4;
+        side_s = scw * 4;
+      } else if (q2 < scw + 2 * ROWS && g.ws_norm >= 0) {
+        side_o = static_cast<int>(g.ws_norm + static_cast<int64_t>(b) * L * GR * 2 + q2 - scw) * 4;
+        side_s = TOK * GR * 2 * 4;
+      } else {
+        side_o = side_s = 0;
+      }
+      ang_o = g.ws_ang >= 0
+                  ? static_cast<int>(g.ws_ang + static_cast<int64_t>(b) * g.L4 * S * 4 + 4 * tid) * 4
+                  : 0;
+      ang_s = (TOK / 4) * S * 16;
+      given = a.phase_mode == M3_PHASE_GIVEN;
+      if (given) {
+        // tile word tid = (group, angle): tokens 4 group .. + 3 of that angle
+        const char* x0 = static_cast<const char*>(a.phase.ptr) +
+                         (b * a.phase.stride[0] + h * a.phase.stride[2]) * 4;
+        tx_b = static_cast<int>(a.phase.stride[1]) * 4;
+        rs_x = make_rsrc(x0, L * tx_b);
+        const int grp4 = tid / S, sa = tid - grp4 * S;
+        o_x = 4 * grp4 * tx_b + sa * static_cast<int>(a.phase.stride[3]) * 4;
+      }
     } else {
       q_row = static_cast<const T*>(a.q.ptr) + b * a.q.stride[0] + grp * a.q.stride[2] + n0;
       k_row = static_cast<const T*>(a.k.ptr) + b * a.k.stride[0] + grp * a.k.stride[2] + n0;
@@ -521,6 +577,12 @@ struct Feed {
         bload_words<W8>(rq[j], rs_p, o_qk + tb + j * d_q1);
         bload_words<W8>(rk[j], rs_p, o_qk + tb + j * d_q1 + d_k);
       }
+    } else if constexpr (BUF) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        bload_words<W8>(rq[j], rs_q, o_q + t0 * tq_b + j * d_q2);
+        bload_words<W8>(rk[j], rs_k, o_k + t0 * tk_b + j * d_k2);
+      }
     } else {
       if (qk_on) {
 #pragma unroll
@@ -544,6 +606,12 @@ struct Feed {
         bload_words<W4>(rv[j], rs_p, o_vz + tb + j * tok_b);
         bload_words<W4>(rz[j], rs_p, o_vz + tb + j * tok_b + d_z);
       }
+    } else if constexpr (BUF) {
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) {
+        bload_words<W4>(rv[j], rs_v, o_v + (t0 + j) * tv_b);
+        bload_words<W4>(rz[j], rs_z, o_z + (t0 + j) * tz_b);
+      }
     } else {
       if (vz_on) {
 #pragma unroll
@@ -560,7 +628,7 @@ struct Feed {
 
   // this lane's side word of sub-chunk c (FULL: unconditional; unused words read anything)
   __device__ __forceinline__ float2 side_in(int c) const {
-    if constexpr (FULL) {
+    if constexpr (FULL || BUF) {
       const u32x2 v = __builtin_bit_cast(
           u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_w, side_o + c * side_s, 0, 0));
       return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
@@ -576,7 +644,14 @@ struct Feed {
   // this lane's angle word of sub-chunk c: in the tile order [TOK/4][S][4], 4-token group
   // tid / S of angle tid % S
   __device__ __forceinline__ float4 ang_in(int c) const {
-    if constexpr (FULL) {
+    if constexpr (BUF) {
+      if (given) {
+        const int o = o_x + c * TOK * tx_b;
+        return make_float4(bload_f32(rs_x, o), bload_f32(rs_x, o + tx_b),
+                           bload_f32(rs_x, o + 2 * tx_b), bload_f32(rs_x, o + 3 * tx_b));
+      }
+    }
+    if constexpr (FULL || BUF) {
       const u32x4 v = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_w, ang_o + c * ang_s, 0, 0));
       return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
@@ -944,7 +1019,8 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
 //
 // SHAPE (without FULL): the model's shape (N = 128, P = 64, 32 angles when rotating, aligned
 // 16-byte rows) with the generic inputs (the hook form): the dimensions and the vector-load
-// choice are compile-time constants, the features and pointers stay runtime.
+// choice are compile-time constants, the features stay runtime; every read and the output go
+// through buffer resources at per-lane offsets, issued unconditionally as in the FULL form.
 template <typename T, int R, bool FULL, bool SO = false, bool SHAPE = false>
 __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, const ScanGeom g,
                                                         const float* __restrict__ prep) {
@@ -1138,7 +1214,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   }
 
   // ---- per-token reads
-  Feed<T, R, FULL> fd;
+  Feed<T, R, FULL, SHAPE> fd;
   fd.init(a, g, prep, b, h, grp, rp, n0, vp, p0, N, P, norm);
   float* fph = a.final_phase.ptr != nullptr
                    ? static_cast<float*>(a.final_phase.ptr) + b * a.final_phase.stride[0] +
@@ -1150,11 +1226,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
                     : nullptr;
   const int64_t blk_stride = a.block_phase.stride[2];
   const __amdgpu_buffer_rsrc_t rs_o =
-      make_rsrc(FULL ? const_cast<char*>(g.out_base) + b * g.out_b : nullptr,
-                FULL ? L * (g.out_t < 0 ? -g.out_t : g.out_t) : 0);
+      make_rsrc(FIX ? const_cast<char*>(g.out_base) + b * g.out_b : nullptr,
+                FIX ? L * (g.out_t < 0 ? -g.out_t : g.out_t) : 0);
   T* out_row = nullptr;
   int out_t = 0, o_out = 0;
-  if constexpr (FULL) {
+  if constexpr (FIX) {
     out_t = g.out_t;
     o_out = h * g.out_h + g.out_o0;
   } else {
@@ -1469,7 +1545,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       ang = fd.ang_in(c + 2);
       __builtin_amdgcn_sched_barrier(0);
     };
-    if constexpr (!FULL) {
+    if constexpr (!FULL && !SHAPE) {
       if (c + 1 < nsub) fd.words(t0 + TOK, min(TOK, L - t0 - TOK), qk_on, vz_on, rq, rk, rv, rz);
       side = fd.side_in(c + 2);
       ang = fd.ang_in(c + 2);
@@ -1507,7 +1583,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
       }
     }
-    if constexpr (FULL) loads_qk();
+    if constexpr (FULL || SHAPE) loads_qk();
     // K~^T V products of the state carry, issued early (they depend only on staged tiles),
     // accumulated onto the decayed state
 #pragma unroll
@@ -1533,7 +1609,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
       }
     }
-    if constexpr (FULL) loads_vz();
+    if constexpr (FULL || SHAPE) loads_vz();
     // phases of sub-chunk c + 1 (its dt block was computed two iterations ago)
     if (ph_on && c + 1 < nsub) {
       float pa[TPL];
@@ -1542,7 +1618,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
                                        scb(c + 1) + SB_::DTV, t0 + TOK, L, pg, lane, angles, pa,
                                        fph, fblk, blk_stride);
     }
-    if constexpr (FULL) loads_side();
+    if constexpr (FULL || SHAPE) loads_side();
     if constexpr (SO) {
       __syncthreads();
       continue;
@@ -1682,7 +1758,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
       }
       if (rr == 0) {
-        if constexpr (FULL) {
+        if constexpr (FIX) {
           // rows of tokens >= L fall outside the buffer extent: the store is dropped
           bstore_quad<T>(y, rs_o,
                          (tq * out_t + o_out + pb * ES) +
@@ -2216,10 +2292,45 @@ static bool full_shape(const m3_scan_args& a, ScanGeom& g, int R) {
 }
 
 // The model's shape with the generic inputs (scan_kernel's SHAPE form): N = 128, P = 64, 32
-// angles when rotating, one group, vector-aligned q / k and value / gate rows.
-static bool model_shape(const m3_scan_args& a, const ScanGeom& g) {
-  return a.d_state == kNPad && a.head_dim == kPPad && a.groups == 1 && g.vec_qk && g.vec_vz &&
-         (a.phase_mode == M3_PHASE_NONE || a.num_angles == kSMax);
+// angles when rotating, one group, vector-aligned q / k and value / gate rows, a workspace
+// below 2^30 bytes. Its reads and the output go through one buffer resource per tensor and
+// (batch, head) at 32-bit byte offsets, so every token stride is positive, each token's row
+// (ranks, or heads for the output) ends below the next token's, and L plus two sub-chunks of
+// 64 tokens stay below 2^31 bytes. Sets the output geometry.
+static bool model_shape(const m3_scan_args& a, ScanGeom& g, int es) {
+  if (!(a.d_state == kNPad && a.head_dim == kPPad && a.groups == 1 && g.vec_qk && g.vec_vz &&
+        (a.phase_mode == M3_PHASE_NONE || a.num_angles == kSMax) && g.ws_bytes > 0 &&
+        g.ws_bytes < (1 << 30))) {
+    return false;
+  }
+  const int64_t rows = static_cast<int64_t>(a.length) + 2 * 64;
+  // a token's row of `span` elements below the next token's, L + 2 sub-chunks in 32 bits
+  auto fits = [&](const m3_tensor& t, int64_t span, int64_t esz) {
+    return t.stride[1] > 0 && span <= t.stride[1] && rows * t.stride[1] * esz < INT32_MAX;
+  };
+  for (const m3_tensor* t : {&a.q, &a.k}) {
+    if (t->stride[3] < 0 || !fits(*t, (a.rank - 1) * t->stride[3] + a.d_state, es)) return false;
+  }
+  // the output is stored 4 elements at a time
+  const int64_t o4 = 4 * es;
+  if (reinterpret_cast<uintptr_t>(a.out.ptr) % o4 != 0 || (a.out.stride[0] * es) % o4 != 0 ||
+      (a.out.stride[1] * es) % o4 != 0 || (a.out.stride[2] * es) % o4 != 0) {
+    return false;
+  }
+  if (!fits(a.value, a.head_dim, es) || !fits(a.gate, a.head_dim, es) ||
+      !fits(a.out, (a.heads - 1) * a.out.stride[2] + a.head_dim, es) || a.out.stride[2] < 0) {
+    return false;
+  }
+  if (a.phase_mode == M3_PHASE_GIVEN &&
+      (a.phase.stride[3] < 0 || !fits(a.phase, (a.num_angles - 1) * a.phase.stride[3] + 1, 4))) {
+    return false;
+  }
+  g.out_base = static_cast<const char*>(a.out.ptr);
+  g.out_b = a.out.stride[0] * es;
+  g.out_t = static_cast<int>(a.out.stride[1] * es);
+  g.out_h = static_cast<int>(a.out.stride[2] * es);
+  g.out_o0 = 0;
+  return true;
 }
 
 template <typename T, int R, bool FULL, bool SO = false, bool SHAPE = false>
@@ -2282,7 +2393,9 @@ static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep,
     }
     return launch_kernel<T, R, true>(a, g, prep, grid, block, stream);
   }
-  if (model_shape(a, g)) return launch_kernel<T, R, false, false, true>(a, g, prep, grid, block, stream);
+  if (prep != nullptr && model_shape(a, g, static_cast<int>(sizeof(T)))) {
+    return launch_kernel<T, R, false, false, true>(a, g, prep, grid, block, stream);
+  }
   return launch_kernel<T, R, false>(a, g, prep, grid, block, stream);
 }
 

@@ -148,6 +148,35 @@ def test_scan_ragged_lengths(length):
     _check(torch.float32, y, s, y_ref, s_ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rank", [1, 4])
+def test_scan_strided_views(dtype, rank):
+    """q / k, value / gate and the phases as column slices of wider rows (token strides longer
+    than the rows they hold, each at its own offset; NaN around them): the same results as the
+    contiguous inputs, against the oracle."""
+    length = 200
+    inp = _inputs(rank, dtype, seed=21 + rank, length=length)
+    dev = {n: (t.to(DEV) if isinstance(t, torch.Tensor) else t) for n, t in inp.items()}
+
+    def widen(t, extra):
+        wide = torch.full((*t.shape[:-1], t.shape[-1] + extra), float("nan"), dtype=t.dtype,
+                          device=DEV)
+        wide[..., extra // 2:extra // 2 + t.shape[-1]] = t
+        return wide[..., extra // 2:extra // 2 + t.shape[-1]]
+
+    for name in ("q", "k"):
+        dev[name] = widen(dev[name], 16)
+    for name in ("value", "gate"):
+        dev[name] = widen(dev[name], 64)
+    dev["phase"] = widen(dev["phase"], 8)
+    assert dev["value"].stride(1) > dev["value"].shape[2] * dev["value"].shape[3]
+    y_ref, s_ref = op.ssd_scan(**inp, chunk_size=_kernel_chunk(dtype, rank))
+    with torch.inference_mode():
+        y, s = ops.mamba3_scan(**dev, chunk_size=_kernel_chunk(dtype, rank))
+    assert ops._HIP_LAST_SCAN_DISPATCH
+    _check(dtype, y.cpu(), s.cpu(), y_ref, s_ref)
+
+
 def test_scan_head_groups():
     """q/k with one group per head (G = H), as ops.mamba3_scan allows."""
     inp = _inputs(1, torch.float32, seed=9, groups=3)
