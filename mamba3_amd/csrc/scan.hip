@@ -1036,7 +1036,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   using SB_ = ScBlk<TOK>;
   // SISO model shape: q / k lanes split by column half, waves 0-3 holding the rotated columns;
   // the phase on waves 0-3 only, 8 tokens per lane (their compute interval is the shorter one)
-  constexpr bool SPLIT = FULL && R == 1 && !F32;
+  constexpr bool SPLIT = (FULL || SHAPE) && R == 1 && !F32;
   constexpr int TPL = SPLIT ? 8 : 4;   // tokens per phase lane
   constexpr int PG = TOK / TPL;        // phase lanes per angle
   // swizzle keys of the transposed tiles, n >> KSH for KT and p >> VSH for VT. 16-bit: constant
@@ -1348,8 +1348,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           k[i] = fmaf(raw_get<T>(rk[j], i), fk[j] * wk[i], bk[R == 1 ? 0 : j][i]);
         }
         if constexpr (SPLIT) {
-          // pairs (2j, 2j+1), j = n0/2 .. n0/2+3: the rotated columns are waves 0-3's
-          if constexpr (ROT) {
+          // pairs (2j, 2j+1), j = n0/2 .. n0/2+3: the rotated columns are waves 0-3's (SHAPE:
+          // when the call rotates)
+          if (ROT && (FULL || rotate)) {
             const float* tr = CSt + tt * CST;
             const f4 c01 = *reinterpret_cast<const f4*>(tr + 2 * cs_col<true>(n0 >> 1, tt));
             const f4 c23 = *reinterpret_cast<const f4*>(tr + 2 * cs_col<true>((n0 >> 1) + 2, tt));
@@ -2298,8 +2299,10 @@ static bool full_shape(const m3_scan_args& a, ScanGeom& g, int R) {
 // (ranks, or heads for the output) ends below the next token's, and L plus two sub-chunks of
 // 64 tokens stay below 2^31 bytes. Sets the output geometry.
 static bool model_shape(const m3_scan_args& a, ScanGeom& g, int es) {
+  // (rank 1 rotates the pairs (2j, 2j+1) only)
   if (!(a.d_state == kNPad && a.head_dim == kPPad && a.groups == 1 && g.vec_qk && g.vec_vz &&
         (a.phase_mode == M3_PHASE_NONE || a.num_angles == kSMax) && g.ws_bytes > 0 &&
+        (a.rank > 1 || a.mimo_rotation == 0) &&
         g.ws_bytes < (1 << 30))) {
     return false;
   }

@@ -141,11 +141,12 @@ def test_scan_small_padded_dims(dtype, rank, dims):
     _check(dtype, y, s, y_ref, s_ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("length", [1, 2, 63, 64, 65, 300])
-def test_scan_ragged_lengths(length):
-    inp = _inputs(1, torch.float32, seed=length, length=length)
-    y, s, y_ref, s_ref = _run_both(inp)
-    _check(torch.float32, y, s, y_ref, s_ref)
+def test_scan_ragged_lengths(length, dtype):
+    inp = _inputs(1, dtype, seed=length, length=length)
+    y, s, y_ref, s_ref = _run_both(inp, chunk=_kernel_chunk(dtype, 1))
+    _check(dtype, y, s, y_ref, s_ref)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
