@@ -2296,8 +2296,9 @@ static bool full_shape(const m3_scan_args& a, ScanGeom& g, int R) {
 // angles when rotating, one group, vector-aligned q / k and value / gate rows, a workspace
 // below 2^30 bytes. Its reads and the output go through one buffer resource per tensor and
 // (batch, head) at 32-bit byte offsets, so every token stride is positive, each token's row
-// (ranks, or heads for the output) ends below the next token's, and L plus two sub-chunks of
-// 64 tokens stay below 2^31 bytes. Sets the output geometry.
+// (ranks, or heads for the output) ends below the next token's, and L + 256 rows (the loads
+// run up to two sub-chunks and a token group ahead) stay below 2^31 bytes. Sets the output
+// geometry.
 static bool model_shape(const m3_scan_args& a, ScanGeom& g, int es) {
   // (rank 1 rotates the pairs (2j, 2j+1) only)
   if (!(a.d_state == kNPad && a.head_dim == kPPad && a.groups == 1 && g.vec_qk && g.vec_vz &&
@@ -2306,8 +2307,8 @@ static bool model_shape(const m3_scan_args& a, ScanGeom& g, int es) {
         g.ws_bytes < (1 << 30))) {
     return false;
   }
-  const int64_t rows = static_cast<int64_t>(a.length) + 2 * 64;
-  // a token's row of `span` elements below the next token's, L + 2 sub-chunks in 32 bits
+  const int64_t rows = static_cast<int64_t>(a.length) + 256;
+  // a token's row of `span` elements below the next token's, L + 256 rows in 32 bits
   auto fits = [&](const m3_tensor& t, int64_t span, int64_t esz) {
     return t.stride[1] > 0 && span <= t.stride[1] && rows * t.stride[1] * esz < INT32_MAX;
   };
