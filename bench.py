@@ -309,6 +309,51 @@ def bench_chunk_state(log, batch=8, heads=32, width=256, rank=1, n=128, p=64):
                 shape=f"[{batch}, {heads}] x {width} tokens, R={rank}, N={n}, P={p}")
 
 
+def bench_hook_step(log, batch=256, heads=32, p=64, n=128, rank=1):
+    """The reference's decode hook boundary (``fused_step``: head-expanded, biased, unrotated
+    q / k [B, H, R, N] bf16, value / gate [B, H, P], FP32 adt / dt, the angle rates, cache tensors
+    updated out of place) at B=256 with 32 heads of config 2's shape: the step kernel's generic
+    form. Bytes: the FP32 state read and written plus the per-row vectors."""
+    from mamba3_amd import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(7)
+    bf = torch.bfloat16
+    s = n // 4
+
+    def rnd(*shape, dtype=torch.float32):
+        return torch.randn(*shape, device=dev, generator=gen).to(dtype)
+
+    dt = torch.rand(batch, heads, device=dev, generator=gen) * 0.1 + 0.001
+    inp = dict(q=rnd(batch, heads, rank, n, dtype=bf), k=rnd(batch, heads, rank, n, dtype=bf),
+               value=rnd(batch, heads, p, dtype=bf), gate=rnd(batch, heads, p, dtype=bf),
+               adt=-0.5 * dt, dt=dt, trap_logits=rnd(batch, heads, dtype=bf),
+               angle_rate=rnd(batch, s, dtype=bf), D=rnd(heads))
+    if rank > 1:
+        inp.update(mimo_x=rnd(heads, rank, p) / rank, mimo_z=rnd(heads, rank, p),
+                   mimo_out=rnd(heads, rank, p) / rank)
+    cache = (rnd(batch, heads, s), rnd(batch, heads, p, n), rnd(batch, heads, rank, n, dtype=bf),
+             rnd(batch, heads, p, dtype=bf))
+
+    def call():
+        ops.fused_step(**inp, cache=cache)
+
+    with torch.inference_mode():
+        for _ in range(50):
+            call()
+        t = _events_time(call, 50) / 50
+    rows = batch * heads
+    # state in / out, q / k, prev_k / k_out, value / gate / prev_value / value_out / y, phase
+    # in / out
+    nbytes = rows * (2 * p * n * 4 + 2 * 2 * rank * n * 2 + 2 * 2 * rank * n * 2 + 5 * p * 2
+                     + 2 * s * 4)
+    gbs = nbytes / t / 1e9
+    log(f"hook step (fused_step) B={batch} H={heads} R={rank}: {t * 1e6:.1f} us, {gbs:.0f} GB/s")
+    return dict(us=round(t * 1e6, 1), tok_s=round(batch / t, 1), bytes=nbytes, bound="hbm",
+                achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(gbs / HBM_PEAK_GBS, 4))
+
+
 def bench_hook_scan(log, batch=8, length=8192, heads=32, p=64, n=128):
     """The reference's scan hook boundary (``mamba3_scan``: normed q / k, head-expanded value /
     gate, FP32 adt / dt, trap logits and the materialized phases [B, L, H, S] FP32) at config 2's
@@ -468,7 +513,7 @@ def main() -> None:
     ap.add_argument("--extra", action="store_true",
                     help="also measure BASELINE configs 3, 5 and config 4 at B=1/64 and R=4")
     ap.add_argument("--extra-only", choices=("config3", "config5", "config5_long", "decode",
-                                             "chunk_state", "hook"),
+                                             "chunk_state", "hook", "hook_step"),
                     help="with --extra: measure only this one of the extra configurations")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB device copy (calibrates PMC byte counters)")
@@ -501,6 +546,7 @@ def main() -> None:
                 for b, r in ((1, 1), (64, 1), (256, 4), (64, 4), (1, 4))]),
             "chunk_state_config2": ("chunk_state", lambda: bench_chunk_state(log)),
             "hook_scan_config2": ("hook", lambda: bench_hook_scan(log)),
+            "hook_step_b256": ("hook_step", lambda: [bench_hook_step(log, rank=r) for r in (1, 4)]),
         }
         extra = {name: run() for name, (key, run) in runs.items()
                  if args.extra_only in (None, key)}
