@@ -240,7 +240,10 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const LinGeom g) {
   const int wm = w / WN, wn = w - wm * WN;
   const int n_base = blockIdx.x * NT, m_base = blockIdx.y * MT, split = blockIdx.z;
   const int k_begin = split * g.k_split;
-  const int nsteps = max(0, min(g.k, k_begin + g.k_split) - k_begin) / KS;
+  // K is a multiple of 32 but not always of KS: the last stage may be partial. Its 8-element
+  // chunks at or past the split's end read zero (they would otherwise read the next row).
+  const int range = max(0, min(g.k, k_begin + g.k_split) - k_begin);
+  const int nsteps = (range + KS - 1) / KS;
 
   // A stage's 16-byte chunks are handed out in wave units of 64: RU = 512 / KS tile rows of
   // KS / 8 chunks. Unit u = 4 j + wave holds x rows RU u.. when u < MT / RU, then weight rows;
@@ -265,8 +268,9 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const LinGeom g) {
     loff[j] = (RU * u + lane / CPR) * RS + 8 * (lane % CPR);
   }
   u32x4 rg[D][NCH];
+  const int lcol = 8 * (lane % CPR);
   auto load = [&](int slot, int s) __attribute__((always_inline)) {
-    const bool live = s < nsteps;
+    const bool live = s < nsteps && KS * s + lcol < range;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       rg[slot][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(

@@ -2158,6 +2158,20 @@ __global__ __launch_bounds__(kCompThreads) void gather_kernel(const m3_scan_args
           static_cast<const T*>(sg.seg_k)[sh * R * N + i];
     }
   }
+  // Segments start on 64-token block boundaries, so block j of segment g is block g * nbs + j
+  // of the sequence, and its increment sum does not depend on the carry: pass 1's sums are the
+  // call's.
+  if (a.block_phase.ptr != nullptr) {
+    const int nb = sg.G * sg.nbs;
+    for (int e = threadIdx.x; e < nb * S; e += kCompThreads) {
+      const int blk = e / S, i = e - blk * S, g = blk / sg.nbs, j = blk - g * sg.nbs;
+      const int64_t src = ((static_cast<int64_t>(b) * sg.G + g) * H + h) * sg.nbs + j;
+      static_cast<float*>(a.block_phase.ptr)[b * a.block_phase.stride[0] +
+                                             h * a.block_phase.stride[1] +
+                                             blk * a.block_phase.stride[2] +
+                                             i * a.block_phase.stride[3]] = sg.seg_blk[src * S + i];
+    }
+  }
 }
 
 // ------------------------------------------------------------------ host side

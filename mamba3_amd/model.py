@@ -25,12 +25,10 @@ from torch import nn
 from torch.nn import functional as F
 
 from . import ops
-from .ops import heavy_tail_activation
 
 _EXPANSION = 2
 _CANONICAL_HEAD_DIM = 64
 _ROPE_FRACTION = 0.5
-_A_FLOOR = 1e-4
 
 _LayerCache = tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]
 
@@ -121,37 +119,6 @@ class _Mamba3Mixer(nn.Module):
             self.register_parameter("direction_logit", None)
         else:
             self.direction_logit = nn.Parameter(torch.zeros(d_model))
-
-    # ---- API-compatible helpers (the kernels fuse these; kept for introspection)
-
-    def _split_projection(self, projected: torch.Tensor) -> tuple[torch.Tensor, ...]:
-        nr = self.d_state * self.ngroups * self.mimo_rank
-        return torch.split(projected, (self.d_inner, self.d_inner, nr, nr, self.nheads,
-                                       self.nheads, self.nheads, self.num_angles), dim=-1)
-
-    def _project(self, hidden_states: torch.Tensor):
-        """``(q, k, x, z, adt, dt, trap, angles)`` as in the reference ``model.py:165-199``."""
-        batch, length, _ = hidden_states.shape
-        z, x, b, c, ddt, da, trap, angles = self._split_projection(self.in_proj(hidden_states))
-        z = z.reshape(batch, length, self.nheads, self.headdim)
-        x = x.reshape(batch, length, self.nheads, self.headdim)
-        b = self.B_norm(b.reshape(batch, length, self.mimo_rank, self.ngroups, self.d_state))
-        c = self.C_norm(c.reshape(batch, length, self.mimo_rank, self.ngroups, self.d_state))
-        k = b.permute(0, 1, 3, 2, 4)
-        q = c.permute(0, 1, 3, 2, 4)
-        dt = F.softplus(ddt.float() + self.dt_bias.float())
-        decay = (-heavy_tail_activation(da.float())).clamp(max=-_A_FLOOR)
-        return q, k, x, z, decay * dt, dt, trap, angles
-
-    def _expand_qk(self, q: torch.Tensor, k: torch.Tensor):
-        if q.shape[2] == 1:
-            q = q.expand(-1, -1, self.nheads, -1, -1)
-            k = k.expand(-1, -1, self.nheads, -1, -1)
-        elif q.shape[2] != self.nheads:
-            repeats = self.nheads // q.shape[2]
-            q = q.repeat_interleave(repeats, dim=2)
-            k = k.repeat_interleave(repeats, dim=2)
-        return q + self.C_bias[None, None].to(q.dtype), k + self.B_bias[None, None].to(k.dtype)
 
     def _chunk(self) -> int:
         return (self.chunk_size if self.training and torch.is_grad_enabled()
@@ -323,15 +290,14 @@ class Mamba3(nn.Module):
             for layer in self.layers:
                 layer.mixer.out_proj.weight.div_(math.sqrt(depth))
 
-    def _validate_input(self, x: torch.Tensor, *, single_token: bool = False) -> None:
-        if x.ndim != 3 or x.shape[-1] != self.d_model:
-            raise ValueError(f"expected [batch, length, {self.d_model}], got {tuple(x.shape)}")
-        if single_token and x.shape[1:] != (1, self.d_model):
-            raise ValueError(f"expected [batch, 1, {self.d_model}], got {tuple(x.shape)}")
-
-    def _empty_output(self, x: torch.Tensor) -> torch.Tensor:
-        dependency = sum(parameter.sum() * 0.0 for parameter in self.parameters())
-        return x + dependency.to(dtype=x.dtype)
+    def _check_tokens(self, x: torch.Tensor, *, one_token: bool = False) -> None:
+        """The input contract: ``[batch, length, d_model]``; length 1 for a decode step. The
+        messages are the reference's (``model.py:570-579``), which callers match on."""
+        shape = tuple(x.shape)
+        if len(shape) != 3 or shape[2] != self.d_model:
+            raise ValueError(f"expected [batch, length, {self.d_model}], got {shape}")
+        if one_token and shape[1] != 1:
+            raise ValueError(f"expected [batch, 1, {self.d_model}], got {shape}")
 
     def _norm_dtype(self, h: torch.Tensor) -> torch.dtype:
         """The dtype the next in_proj computes in: autocast's for FP32 rows, else the rows'."""
@@ -367,17 +333,20 @@ class Mamba3(nn.Module):
         return out, cache
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        self._validate_input(x)
-        if x.shape[0] == 0 or x.shape[1] == 0:
-            return self._empty_output(x)
+        self._check_tokens(x)
+        if x.numel() == 0:
+            # no token to mix (batch or length 0): an empty result of the input's kind, with
+            # no launch (this package computes no gradients, so nothing needs to depend on
+            # the parameters)
+            return torch.empty_like(x)
         return self._run_layers(x, return_cache=False)[0]
 
     def prefill(self, x: torch.Tensor):
         """Process a causal prefix and return the constant-size decode cache."""
         if not self.causal:
             raise ValueError("prefill requires causal=True")
-        self._validate_input(x)
-        if x.shape[0] == 0 or x.shape[1] == 0:
+        self._check_tokens(x)
+        if x.numel() == 0:
             raise ValueError("prefill requires a non-empty batch and sequence")
         return self._run_layers(x, return_cache=True)
 
@@ -390,31 +359,31 @@ class Mamba3(nn.Module):
         """
         if not self.causal:
             raise ValueError("step requires causal=True")
-        self._validate_input(x, single_token=True)
-        if cache is None:
-            layer_caches: list[_LayerCache | None] = [None] * len(self.layers)
-        else:
-            if len(cache) != len(self.layers):
-                raise ValueError(f"expected cache for {len(self.layers)} layers")
-            layer_caches = list(cache)
-        next_cache: list[_LayerCache] = []
-        for layer, layer_cache in zip(self.layers, layer_caches):
-            x, updated = layer.step(x, layer_cache, inplace=inplace and layer_cache is not None)
-            next_cache.append(updated)
-        return self.norm_f(x), next_cache
+        self._check_tokens(x, one_token=True)
+        depth = len(self.layers)
+        if cache is not None and len(cache) != depth:
+            raise ValueError(f"expected cache for {depth} layers")
+        updated: list[_LayerCache] = []
+        for i, layer in enumerate(self.layers):
+            layer_cache = None if cache is None else cache[i]
+            x, layer_cache = layer.step(x, layer_cache,
+                                        inplace=inplace and layer_cache is not None)
+            updated.append(layer_cache)
+        return self.norm_f(x), updated
 
     def set_chunk_sizes(self, *, training: int | None = None,
                         inference: int | None = None) -> Mamba3:
-        """Override the scan chunk sizes (advisory for the HIP scan, which tiles itself)."""
-        if training is not None and training <= 0:
-            raise ValueError("training chunk size must be positive")
-        if inference is not None and inference <= 0:
-            raise ValueError("inference chunk size must be positive")
+        """Set every mixer's chunk sizes. The HIP scan tiles the sequence itself; the chunk is
+        validated, passed to the library as the caller's chunk, and used by the oracle."""
+        sizes = {"training": training, "inference": inference}
+        for name, size in sizes.items():
+            if size is not None and size <= 0:
+                raise ValueError(f"{name} chunk size must be positive")
         for layer in self.layers:
-            if training is not None:
-                layer.mixer.chunk_size = training
-            if inference is not None:
-                layer.mixer.inference_chunk_size = inference
+            mixer = layer.mixer
+            mixer.chunk_size = mixer.chunk_size if training is None else training
+            mixer.inference_chunk_size = (mixer.inference_chunk_size if inference is None
+                                          else inference)
         return self
 
     def compile_layers(self, **kwargs: object) -> Mamba3:
@@ -431,52 +400,57 @@ class Mamba3(nn.Module):
 
 
 class _HipGraphDecoder:
-    """Replays a captured decode step over a static, in-place updated cache.
+    """A decode step of the whole stack, captured once in a hipGraph and replayed.
 
-    Mirrors the reference's ``_CudaGraphDecoder`` (``model.py:691-774``). The captured step
-    updates the cache tensors in place, so the replay copies no cache back.
+    The graph reads the static ``input`` buffer and updates the static per-layer ``cache``
+    (``(phase, state, k_rot, value)``, the layer-cache layout) in place, so a replay is one
+    input copy plus one graph launch. Decoding starts from zeros (``reset``) or from a
+    prefill's cache (``load_cache``). The graph holds the addresses of the parameters it was
+    captured with; ``validate`` refuses a model whose parameters were replaced or modified
+    since. Interface of the reference's ``cuda_graph`` decoder (``model.py:691-774``).
     """
 
     def __init__(self, model: Mamba3, batch_size: int) -> None:
         if batch_size <= 0:
             raise ValueError("batch_size must be positive")
-        parameter = next(model.parameters())
-        if parameter.device.type != "cuda":
+        weights = list(model.parameters())
+        device, dtype = weights[0].device, weights[0].dtype
+        if device.type != "cuda":
             raise ValueError("cuda_graph requires a ROCm (cuda) model")
         if model.training:
             raise ValueError("cuda_graph requires model.eval()")
         self.model = model
-        self.parameters = tuple(model.parameters())
-        self.parameter_signature = self._parameter_signature()
-        device = parameter.device
-        self.input = torch.zeros(batch_size, 1, model.d_model, device=device,
-                                 dtype=parameter.dtype)
-        self.cache = [layer.mixer.allocate_cache(batch_size, device=device, dtype=parameter.dtype)
+        # the captured tensors themselves and their version counters at capture time
+        self._captured = [(w, w._version) for w in weights]
+        self.input = torch.zeros(batch_size, 1, model.d_model, device=device, dtype=dtype)
+        self.cache = [layer.mixer.allocate_cache(batch_size, device=device, dtype=dtype)
                       for layer in model.layers]
-        with torch.cuda.device(device):
-            warmup = torch.cuda.Stream(device=device)
-            warmup.wait_stream(torch.cuda.current_stream(device))
-            with torch.cuda.stream(warmup), torch.inference_mode():
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.device(device), torch.inference_mode():
+            # One eager step first, on a side stream: the libraries' lazy set-up (handles,
+            # workspaces, first-use allocations) must happen outside the capture.
+            side = torch.cuda.Stream(device=device)
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.stream(side):
                 model.step(self.input, self.cache, inplace=True)
-            torch.cuda.current_stream(device).wait_stream(warmup)
-            capture = torch.cuda.Stream(device=device)
-            self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph, stream=capture), torch.inference_mode():
+            torch.cuda.current_stream(device).wait_stream(side)
+            with torch.cuda.graph(self.graph, stream=torch.cuda.Stream(device=device)):
                 self.output, _ = model.step(self.input, self.cache, inplace=True)
         self.reset()
 
     def __call__(self, x: torch.Tensor, validate: bool = False) -> torch.Tensor:
-        if x.shape != self.input.shape:
-            raise ValueError(f"expected {tuple(self.input.shape)}, got {tuple(x.shape)}")
-        if x.device != self.input.device or x.dtype != self.input.dtype:
-            raise ValueError(f"expected {self.input.dtype} on {self.input.device}, "
+        want = self.input
+        if x.shape != want.shape:
+            raise ValueError(f"expected {tuple(want.shape)}, got {tuple(x.shape)}")
+        if (x.device, x.dtype) != (want.device, want.dtype):
+            raise ValueError(f"expected {want.dtype} on {want.device}, "
                              f"got {x.dtype} on {x.device}")
         if x.requires_grad:
             raise ValueError("CUDA graph decoding does not support gradient inputs")
         if validate:
             self.validate()
-        with torch.inference_mode(), torch.cuda.device(self.input.device):
-            self.input.copy_(x)
+        with torch.inference_mode(), torch.cuda.device(want.device):
+            want.copy_(x)
             self.graph.replay()
         return self.output
 
@@ -486,14 +460,31 @@ class _HipGraphDecoder:
         return self.output
 
     def validate(self) -> None:
-        if self._parameter_signature() != self.parameter_signature:
+        current = list(self.model.parameters())
+        same = len(current) == len(self._captured) and all(
+            now is then and now._version == version
+            for now, (then, version) in zip(current, self._captured))
+        if not same:
             raise RuntimeError("model state changed; recreate the CUDA graph decoder")
 
     def reset(self) -> None:
-        for layer_cache in self.cache:
-            for tensor in layer_cache:
-                tensor.zero_()
+        """Start the next replay from an all-zero cache."""
+        with torch.inference_mode():
+            for layer_cache in self.cache:
+                for t in layer_cache:
+                    t.zero_()
 
-    def _parameter_signature(self):
-        return tuple((id(p), p._version, p.data_ptr(), p.device, p.dtype, tuple(p.shape))
-                     for p in self.model.parameters())
+    def load_cache(self, cache: list[_LayerCache]) -> None:
+        """Continue decoding from ``cache`` (e.g. ``prefill``'s): copied into the static cache,
+        whose tensors the graph holds."""
+        if len(cache) != len(self.cache):
+            raise ValueError(f"expected cache for {len(self.cache)} layers")
+        with torch.inference_mode():
+            for mine, given in zip(self.cache, cache):
+                if len(given) != len(mine) or any(a.shape != b.shape
+                                                  for a, b in zip(mine, given)):
+                    raise ValueError(
+                        f"expected cache shapes {tuple(tuple(t.shape) for t in mine)}, got "
+                        f"{tuple(tuple(t.shape) for t in given)}")
+                for a, b in zip(mine, given):
+                    a.copy_(b)

@@ -356,9 +356,13 @@ def step_update(q, k, value, gate, adt, dt, trap_logits, D, cache, *, mimo_x=Non
 
 
 def project(params, pre: str, h: torch.Tensor, dims: Dims):
-    """model.py:147-199: in_proj, split, B/C RMSNorm, dt, adt."""
-    batch, length, _ = h.shape
-    proj = F.linear(h, params[pre + "in_proj.weight"])
+    """model.py:165-199: in_proj, then ``split_projection``."""
+    return split_projection(params, pre, F.linear(h, params[pre + "in_proj.weight"]), dims)
+
+
+def split_projection(params, pre: str, proj: torch.Tensor, dims: Dims):
+    """model.py:147-199 after in_proj: split, B/C RMSNorm, dt, adt of ``proj [B, L, proj]``."""
+    batch, length, _ = proj.shape
     z, x, b, c, ddt, da, trap, ang = torch.split(proj, dims.split_sizes, dim=-1)
     h_, p_, r_, n_ = dims.nheads, dims.headdim, dims.mimo_rank, dims.d_state
     z = z.reshape(batch, length, h_, p_)
@@ -383,34 +387,40 @@ def _mimo(params, pre):
     return (params.get(pre + "mimo_x"), params.get(pre + "mimo_z"), params.get(pre + "mimo_out"))
 
 
-def mixer_forward(params, pre: str, h: torch.Tensor, dims: Dims, *, causal: bool = True,
-                  cache=None, return_cache: bool = False, chunk: int | None = None):
-    """model.py:270-362: one mixer over a full sequence (optionally with cache)."""
+def mixer_scan(params, pre: str, proj: torch.Tensor, dims: Dims, cache=None, *,
+               chunk: int | None = None):
+    """model.py:282-327: the mixer's scan from its in_proj output ``proj [B, L, proj]``.
+
+    Returns ``(mixed [B, L, H, P], cache)`` where ``cache`` is the layer cache the
+    sequence leaves (``(phase, state, k_rot, value)`` of the last token, model.py:315-327).
+    """
     chunk = chunk or dims.inference_chunk
     mx, mz, mo = _mimo(params, pre)
     mimo = dims.mimo_rank > 1
+    q, k, x, z, adt, dt, trap, ang = split_projection(params, pre, proj, dims)
+    phase = phase_scan(ang, dt, cache[0] if cache is not None else None)
+    mixed, state = ssd_scan(
+        q, k, x, z, adt, dt, trap, params[pre + "D"], mimo_x=mx, mimo_z=mz, mimo_out=mo,
+        chunk_size=chunk, initial_state=cache[1] if cache is not None else None,
+        initial_k=cache[2] if cache is not None else None,
+        initial_value=cache[3] if cache is not None else None, phase=phase,
+        mimo_rotation=mimo, q_bias=params[pre + "C_bias"], k_bias=params[pre + "B_bias"])
+    fq, fk = expand_bias(params, pre, q[:, -1:], k[:, -1:], dims.nheads)
+    _, fk = rotate(fq, fk, phase[:, -1:], mimo=mimo)
+    return mixed, (phase[:, -1].clone(), state, fk[:, 0].clone(), x[:, -1].clone())
 
-    def scan(hh, init):
-        q, k, x, z, adt, dt, trap, ang = project(params, pre, hh, dims)
-        phase = phase_scan(ang, dt, init[0] if init is not None else None)
-        mixed, state = ssd_scan(
-            q, k, x, z, adt, dt, trap, params[pre + "D"], mimo_x=mx, mimo_z=mz, mimo_out=mo,
-            chunk_size=chunk, initial_state=init[1] if init is not None else None,
-            initial_k=init[2] if init is not None else None,
-            initial_value=init[3] if init is not None else None, phase=phase,
-            mimo_rotation=mimo, q_bias=params[pre + "C_bias"], k_bias=params[pre + "B_bias"])
-        return q, k, x, phase, mixed, state
 
-    q, k, x, phase, mixed, state = scan(h, cache)
+def mixer_forward(params, pre: str, h: torch.Tensor, dims: Dims, *, causal: bool = True,
+                  cache=None, return_cache: bool = False, chunk: int | None = None):
+    """model.py:270-362: one mixer over a full sequence (optionally with cache)."""
+    w_in = params[pre + "in_proj.weight"]
+    mixed, next_cache = mixer_scan(params, pre, F.linear(h, w_in), dims, cache, chunk=chunk)
     w_out = params[pre + "out_proj.weight"]
     out = F.linear(mixed.flatten(-2), w_out)
     if causal:
-        if not return_cache:
-            return out
-        fq, fk = expand_bias(params, pre, q[:, -1:], k[:, -1:], dims.nheads)
-        _, fk = rotate(fq, fk, phase[:, -1:], mimo=mimo)
-        return out, (phase[:, -1].clone(), state, fk[:, 0].clone(), x[:, -1].clone())
-    _, _, _, _, mixed_r, _ = scan(torch.flip(h, dims=(1,)), None)
+        return (out, next_cache) if return_cache else out
+    mixed_r, _ = mixer_scan(params, pre, F.linear(torch.flip(h, dims=(1,)), w_in), dims,
+                            chunk=chunk)
     back = F.linear(torch.flip(mixed_r, dims=(1,)).flatten(-2), w_out)
     blend = torch.sigmoid(params[pre + "direction_logit"]).to(dtype=out.dtype)
     return out * blend + back * (1.0 - blend)

@@ -41,6 +41,8 @@ SHAPES = [
     (256, 8672, 2048),  # decode B = 256 in_proj (config 4)
     (256, 2048, 4096),  # decode B = 256 out_proj (K split)
     (3, 24, 32),        # one K step, fewer columns than a wave unit
+    (40, 96, 96),       # the tile kernel with K % 64 == 32: a half last stage
+    (100, 200, 160),    # the same with the 128-row tile and ragged rows / columns
 ]
 
 
@@ -167,3 +169,20 @@ def test_bf16_weight_decode_matches_oracle(rank, batch, per_layer, monkeypatch):
     d = got.float().cpu() - want
     assert d.abs().max().item() <= 2e-2 * want.abs().max().item()
     assert d.norm().item() <= 1e-2 * want.norm().item()
+
+
+def test_decode_with_a_half_last_stage_matches_oracle():
+    """``Mamba3(48)`` with bf16 weights at batch 40: out_proj has K = 96 (a multiple of 32,
+    not of 64) and 40 rows, so it takes the tile kernel with a 32-wide last stage."""
+    torch.manual_seed(90)
+    model = Mamba3(48, d_state=16, depth=2, mimo_rank=1).eval()
+    params = {k: v.detach().clone().to(torch.bfloat16) for k, v in model.state_dict().items()}
+    model = model.to(DEV, torch.bfloat16)
+    dims = op.Dims(48, 16, 1)
+    x = torch.randn(40, 4, 48).to(torch.bfloat16)
+    cache, want_cache = None, None
+    with torch.inference_mode():
+        for t in range(4):
+            got, cache = model.step(x[:, t:t + 1].to(DEV), cache)
+            want, want_cache = op.model_step(params, x[:, t:t + 1], dims, want_cache)
+            torch.testing.assert_close(got.float().cpu(), want.float(), rtol=2e-2, atol=2e-2)

@@ -9,6 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from conftest import bf16_parity
 from mamba3_amd import Mamba3, ops
 from oracle import portable as op
 
@@ -158,25 +159,34 @@ def test_prefill_cache_does_not_retain_prefix_storage():
 
 
 def test_graph_decoder_matches_forward_and_resets():
-    """Reference tests/test_model.py:338-379 (hipGraph capture)."""
-    model, _, _ = _model(64, 128, 1, 1, seed=5)
+    """Reference tests/test_model.py:338-379 (hipGraph capture), plus the oracle: the replayed
+    outputs and every cache tensor against ``oracle.model_step``'s chain."""
+    model, params, dims = _model(64, 128, 1, 1, seed=5)
     torch.manual_seed(5)
-    x = torch.randn(2, 5, 64, device=DEV)
+    x_cpu = torch.randn(2, 5, 64)
+    x = x_cpu.to(DEV)
     ref_cache = None
     ref_outs = []
     with torch.inference_mode():
         for t in range(5):
             o, ref_cache = model.step(x[:, t:t + 1], ref_cache)
             ref_outs.append(o)
+        oracle_cache = None
+        oracle_outs = []
+        for t in range(5):
+            o, oracle_cache = op.model_step(params, x_cpu[:, t:t + 1], dims, oracle_cache)
+            oracle_outs.append(o)
     decoder = model.cuda_graph(batch_size=2)
     with torch.inference_mode():
         want = model(x)
         got = torch.cat([decoder(x[:, t:t + 1]).clone() for t in range(5)], 1)
     torch.testing.assert_close(got, want, rtol=2e-4, atol=2e-5 * 5)
     torch.testing.assert_close(got, torch.cat(ref_outs, 1), rtol=2e-4, atol=2e-5)
-    for g_layer, r_layer in zip(decoder.cache, ref_cache):
-        for a, b in zip(g_layer, r_layer):
+    torch.testing.assert_close(got.cpu(), torch.cat(oracle_outs, 1), **F32)
+    for g_layer, r_layer, o_layer in zip(decoder.cache, ref_cache, oracle_cache):
+        for a, b, c in zip(g_layer, r_layer, o_layer):
             torch.testing.assert_close(a, b, rtol=2e-4, atol=2e-5)
+            torch.testing.assert_close(a.cpu(), c, **F32)
     decoder.reset()
     with torch.inference_mode():
         again = decoder(x[:, :1]).clone()
@@ -190,22 +200,49 @@ def test_graph_decoder_matches_forward_and_resets():
 
 
 @pytest.mark.parametrize("rank", [1, 4])
-def test_graph_decoder_bf16_weights_replays(rank):
-    """bf16 weights, FP32 state; several replays with eager work in between."""
-    model, _, _ = _model(128, 128, 2, rank, seed=6)
+def test_graph_decoder_bf16_weights_against_oracle(rank):
+    """bf16 weights, FP32 state: a prefill loaded into the graph decoder (``load_cache``), then
+    40 replays with eager work in between. Against the eager HIP steps: outputs within 1e-2,
+    states within 1e-4. Against the oracle: the bf16 parity bar (``conftest.bf16_parity``) on the
+    outputs, with the oracle's chain in bf16 and in FP32 (same bf16-valued weights), and the
+    FP32 states at least as close to the FP32 chain as the oracle's bf16 chain is."""
+    model, params, dims = _model(128, 128, 2, rank, seed=6)
     model = model.to(torch.bfloat16)
     torch.manual_seed(6)
-    x = torch.randn(3, 6, 128, device=DEV, dtype=torch.bfloat16)
+    x_cpu = torch.randn(3, 70, 128).to(torch.bfloat16)
+    x = x_cpu.to(DEV)
+    split = 30
     decoder = model.cuda_graph(batch_size=3)
-    ref_cache = None
     with torch.inference_mode():
-        for t in range(6):
-            want, ref_cache = model.step(x[:, t:t + 1], ref_cache)
-            got = decoder(x[:, t:t + 1]).clone()
-            torch.cuda.synchronize()
-            torch.testing.assert_close(got.float(), want.float(), rtol=1e-2, atol=1e-2)
-    for g_layer, r_layer in zip(decoder.cache, ref_cache):
-        torch.testing.assert_close(g_layer[1], r_layer[1], rtol=1e-4, atol=1e-4)
+        _, cache = model.prefill(x[:, :split])
+    decoder.load_cache(cache)
+    eager_cache = [tuple(t.clone() for t in layer) for layer in cache]
+    got, eager = [], []
+    with torch.inference_mode():
+        for t in range(split, x.shape[1]):
+            got.append(decoder(x[:, t:t + 1]).clone())
+            e, eager_cache = model.step(x[:, t:t + 1], eager_cache)
+            eager.append(e)
+    torch.cuda.synchronize()
+    got, eager = torch.cat(got, 1), torch.cat(eager, 1)
+    torch.testing.assert_close(got.float(), eager.float(), rtol=1e-2, atol=1e-2)
+    for g_layer, e_layer in zip(decoder.cache, eager_cache):
+        torch.testing.assert_close(g_layer[1], e_layer[1], rtol=1e-4, atol=1e-4)
+    chains = {}
+    for dtype in (torch.bfloat16, torch.float32):
+        p_run = {k: v.to(torch.bfloat16).to(dtype) for k, v in params.items()}
+        with torch.inference_mode():
+            _, c = op.model_prefill(p_run, x_cpu[:, :split].to(dtype), dims)
+            outs = []
+            for t in range(split, x.shape[1]):
+                o, c = op.model_step(p_run, x_cpu[:, t:t + 1].to(dtype), dims, c)
+                outs.append(o)
+        chains[dtype] = (torch.cat(outs, 1), c)
+    (w16, c16), (w32, c32) = chains[torch.bfloat16], chains[torch.float32]
+    bf16_parity(f"graph bf16 R={rank} outputs", got, w16, w32)
+    for i, layer in enumerate(decoder.cache):
+        bf16_parity(f"graph bf16 R={rank} layer {i} state", layer[1], c16[i][1], c32[i][1],
+                    elementwise=False, slack=1.5)
 
 
 @pytest.mark.parametrize("rank", [1, 4])

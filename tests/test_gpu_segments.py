@@ -12,6 +12,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from conftest import bf16_parity
 from mamba3_amd import Mamba3, ops
 from oracle import portable as op
 from test_gpu_scan import _inputs
@@ -72,6 +73,10 @@ def test_bf16_split_matches_unsplit(rank, segments):
     _scale_close(s2, s1)
     y_ref, s_ref = op.ssd_scan(**inp, chunk_size=chunk)
     _scale_close(y2, y_ref)
+    y32, s32 = op.ssd_scan(**{n: (t.float() if isinstance(t, torch.Tensor) else t)
+                              for n, t in inp.items()}, chunk_size=chunk)
+    bf16_parity(f"split bf16 R={rank} output", y2, y_ref, y32)
+    bf16_parity(f"split bf16 R={rank} state", s2, s_ref, s32, elementwise=False)
 
 
 def test_explicit_segments_must_divide_the_length(segments):
@@ -145,3 +150,25 @@ def test_split_scan_continues_from_a_cache(segments):
     torch.testing.assert_close(torch.cat((first, second), 1), full, **F32)
     for a, b in zip(cache2, full_cache):
         torch.testing.assert_close(a, b, **F32)
+
+
+def test_split_scan_writes_the_callers_block_phase(segments):
+    """``block_phase`` (each 64-token block's phase-increment sum) of a call split into
+    segments equals the unsplit call's: every segment's sums reach the caller's buffer."""
+    model, _, _ = _model(1, seed=72)
+    torch.manual_seed(73)
+    x = torch.randn(1, 4096, 128, device=DEV)
+    mixer = model.layers[0].mixer
+    blocks = {}
+    with torch.inference_mode():
+        proj = mixer.in_proj(model.layers[0].norm(x))
+        for g in (1, 8):
+            segments(g)
+            call = ops.ScanCall(proj, mixer)
+            buf = torch.full((1, mixer.nheads, 64, mixer.num_angles), float("nan"), device=DEV)
+            call.args.block_phase = ops._hip.tensor(buf)
+            call.launch()
+            torch.cuda.synchronize()
+            blocks[g] = buf.cpu()
+    assert torch.isfinite(blocks[1]).all()
+    torch.testing.assert_close(blocks[8], blocks[1], rtol=0, atol=0)

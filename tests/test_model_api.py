@@ -52,8 +52,11 @@ def test_has_canonical_mamba3_parameters(rank):
         assert mixer.mimo_x is None
     else:
         assert mixer.mimo_x.shape == (2, rank, 64)
-    q, k, *_ = mixer._project(torch.randn(1, 3, 64))
-    assert q.shape == k.shape == (1, 3, 1, rank, 128)
+    views = ops.split_projection(mixer.in_proj(torch.randn(1, 3, 64)), mixer)
+    assert views["q"].shape == views["k"].shape == (1, 3, 1, rank, 128)
+    assert views["x"].shape == views["z"].shape == (1, 3, 2, 64)
+    assert views["dt"].shape == views["a"].shape == views["trap"].shape == (1, 3, 2)
+    assert views["angles"].shape == (1, 3, 32)
 
 
 def test_canonical_initialization():
