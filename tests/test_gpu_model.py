@@ -240,9 +240,9 @@ def test_graph_decoder_bf16_weights_against_oracle(rank):
         chains[dtype] = (torch.cat(outs, 1), c)
     (w16, c16), (w32, c32) = chains[torch.bfloat16], chains[torch.float32]
     bf16_parity(f"graph bf16 R={rank} outputs", got, w16, w32)
-    for i, layer in enumerate(decoder.cache):
-        bf16_parity(f"graph bf16 R={rank} layer {i} state", layer[1], c16[i][1], c32[i][1],
-                    elementwise=False, slack=1.5)
+    bf16_parity(f"graph bf16 R={rank} states", torch.stack([c[1] for c in decoder.cache]),
+                torch.stack([c[1] for c in c16]), torch.stack([c[1] for c in c32]),
+                elementwise=False, max_slack=1.5)
 
 
 @pytest.mark.parametrize("rank", [1, 4])
