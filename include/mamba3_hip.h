@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define M3_ABI_VERSION 3
+#define M3_ABI_VERSION 4
 
 /* Element types. */
 enum { M3_F32 = 0, M3_BF16 = 1, M3_F16 = 2 };
@@ -120,6 +120,19 @@ typedef struct {
 /* Bytes of device workspace m3_scan_fwd needs for these arguments (0 is possible). */
 int m3_scan_workspace_size(const m3_scan_args* args, size_t* bytes);
 int m3_scan_fwd(const m3_scan_args* args, hipStream_t stream);
+
+/*
+ * m3_scan_fwd without a caller workspace. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under hipGraph stream capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The call uses the library's own device scratch, one static
+ * array of M3_SCRATCH_BYTES per GPU, held until the process ends; args->workspace and
+ * args->workspace_bytes are ignored. It allocates, frees and synchronises nothing. A call that
+ * needs more than M3_SCRATCH_BYTES (m3_scan_workspace_size) fails with M3_EWORKSPACE. Every call
+ * on one GPU uses that GPU's one scratch, which keeps the last call's contents: calls that overlap
+ * in time on one GPU (on different streams) race, so the caller must order them.
+ */
+#define M3_SCRATCH_BYTES (64u << 20)
+int m3_scan_fwd_noalloc(const m3_scan_args* args, hipStream_t stream);
 
 /*
  * One chunk's state update, _triton.py:294-413:

@@ -14,7 +14,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmamba3_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, BF16, F16 = 0, 1, 2
 PHASE_NONE, PHASE_GIVEN, PHASE_ANGLES = 0, 1, 2
@@ -95,9 +95,10 @@ class RmsNormArgs(ctypes.Structure):
     ]
 
 
-ENTRY_POINTS = ("m3_scan_fwd", "m3_scan_workspace_size", "m3_chunk_state", "m3_step",
-                "m3_linear", "m3_linear_workspace_size", "m3_rms_norm", "m3_last_error",
-                "m3_abi_version")
+ENTRY_POINTS = ("m3_scan_fwd", "m3_scan_workspace_size", "m3_scan_fwd_noalloc",
+                "m3_chunk_state", "m3_step", "m3_linear", "m3_linear_workspace_size",
+                "m3_rms_norm", "m3_last_error", "m3_abi_version")
+SCRATCH_BYTES = 64 << 20  # M3_SCRATCH_BYTES: the no-alloc scan's per-GPU scratch
 
 _lib: ctypes.CDLL | None = None
 
@@ -111,7 +112,8 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is not built; run `python -m mamba3_amd.build` (hipcc, gfx950)")
     lib = ctypes.CDLL(LIB_PATH)
-    for name in ("m3_scan_fwd", "m3_chunk_state", "m3_step", "m3_linear", "m3_rms_norm"):
+    for name in ("m3_scan_fwd", "m3_scan_fwd_noalloc", "m3_chunk_state", "m3_step", "m3_linear",
+                 "m3_rms_norm"):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]

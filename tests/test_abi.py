@@ -269,3 +269,20 @@ def test_rms_norm_validation_on_the_host(lib):
     args.x.stride[0] = 1026  # rows not 4-element aligned
     assert lib.m3_rms_norm(ctypes.byref(args), None) == 2
     assert b"aligned" in lib.m3_last_error()
+
+
+def test_noalloc_scan_rejects_calls_beyond_its_scratch(lib):
+    """m3_scan_fwd_noalloc refuses a call whose workspace would exceed M3_SCRATCH_BYTES before
+    touching the device (the size check needs only the dimensions and which inputs are set)."""
+    args = _hip.ScanArgs(batch=64, length=65536, heads=32, groups=1, rank=1, d_state=128,
+                         head_dim=64, num_angles=32, chunk=256, act_dtype=_hip.BF16,
+                         mimo_rotation=0, raw_dt=1, phase_mode=_hip.PHASE_ANGLES, norm_eps=1e-5,
+                         segments=1)
+    args.q_norm_w.ptr = args.k_norm_w.ptr = 256  # set, never dereferenced by the size query
+    need = ctypes.c_size_t(0)
+    assert lib.m3_scan_workspace_size(ctypes.byref(args), ctypes.byref(need)) == 0
+    assert need.value > _hip.SCRATCH_BYTES
+    rc = lib.m3_scan_fwd_noalloc(ctypes.byref(args), None)
+    assert rc == 4  # M3_EWORKSPACE
+    assert b"scratch" in lib.m3_last_error()
+    assert lib.m3_scan_fwd_noalloc(None, None) == 1
