@@ -21,7 +21,7 @@ LIB_NAME = "libmamba3_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 OBJ_DIR = os.path.join(ROOT, "_build")
 SOURCES = ("abi.hip", "step.hip", "scan.hip", "chunk_state.hip", "linear.hip", "norm.hip",
-           "noalloc.hip")
+           "noalloc.hip", "rscan.hip")
 ARCH = os.environ.get("MAMBA3_OFFLOAD_ARCH", "gfx950")
 
 # Packed FP32 ops are disabled in device code (a hardware-correctness precaution on this pool).

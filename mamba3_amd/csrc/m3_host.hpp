@@ -25,4 +25,11 @@ int check_tensor(const m3_tensor& t, const char* name, int dims, int64_t inner_e
 // After a launch: translate hipGetLastError into a status.
 int check_launch(const char* what);
 
+// The recurrent scan (rscan.hip) for the shapes the chunked MFMA kernel does not tile, and a
+// decode step run as a one-token recurrent scan for the shapes the step kernels do not take.
+bool rscan_fits(const m3_scan_args& a);
+int launch_recurrent_scan(const m3_scan_args& a, hipStream_t stream);
+m3_scan_args step_as_scan(const m3_step_args& s);
+int launch_recurrent_step(const m3_step_args& s, hipStream_t stream);
+
 }  // namespace m3

@@ -89,7 +89,7 @@ template <> struct Mma<float> {
 // Compile-time LDS layout. Operand tiles are padded to N = 128 and P = 64 (the largest shapes
 // the kernel takes; every Mamba3 configuration has P <= 64), so every offset and loop bound is a
 // constant; smaller shapes run on zero padding.
-constexpr int kNPad = 128, kPPad = 64, kSMax = 32, kRMax = 4;
+constexpr int kNPad = 128, kPPad = 64, kSMax = 32, kRMax = 8;
 constexpr int kNT = kNPad / 16, kPT = kPPad / 16;  // 16-row tiles of N and P
 
 template <typename T> struct Layout {
@@ -2445,7 +2445,17 @@ static bool segmentable(const m3_scan_args& a) {
 // half of the 256 CUs: the largest power of 2 G with B*H*G <= 256 that cuts L into equal
 // segments of at least 8 sub-chunks (whole 64-token phase blocks with angle phases), taken from
 // G = 4 up (the split scans the sequence twice).
+static bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// The shapes the chunked MFMA kernel tiles: d_state a power of 2 up to 128, head_dim up to 64,
+// up to 32 angles, ranks 1, 2, 4 and 8. Others take the recurrent scan (rscan.hip).
+static bool tiled_shape(const m3_scan_args& a) {
+  return pow2(a.d_state) && a.d_state >= 4 && a.d_state <= kNPad && a.head_dim <= kPPad &&
+         a.num_angles <= kSMax && (a.rank == 1 || a.rank == 2 || a.rank == 4 || a.rank == 8);
+}
+
 static int segments_for(const m3_scan_args& a) {
+  if (!tiled_shape(a)) return a.segments > 1 ? -1 : 1;
   if (a.segments == 1 || a.length <= 0 || a.batch <= 0) return 1;
   if (a.segments < 0) return -1;
   if (!segmentable(a)) return a.segments > 1 ? -1 : 1;
@@ -2621,11 +2631,10 @@ static int launch_scan(const m3_scan_args& a, hipStream_t stream) {
     case 1: return launch_scan_r<T, 1>(a, stream);
     case 2: return launch_scan_r<T, 2>(a, stream);
     case 4: return launch_scan_r<T, 4>(a, stream);
-    default: return fail(M3_EUNSUPPORTED, "m3_scan_fwd: rank %d not in {1, 2, 4}", a.rank);
+    case 8: return launch_scan_r<T, 8>(a, stream);
+    default: return fail(M3_EUNSUPPORTED, "m3_scan_fwd: rank %d not in {1, 2, 4, 8}", a.rank);
   }
 }
-
-static bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
 // A per-token tensor may run backwards (stride[1] < 0: token t at ptr + t * stride[1]; the
 // reverse direction of a bidirectional layer reads the forward projection this way); the
@@ -2644,15 +2653,15 @@ static int validate_scan(const m3_scan_args& a) {
   }
   if (a.heads % a.groups != 0) return fail(M3_EINVAL, "m3_scan_fwd: heads %% groups != 0");
   if (!valid_dtype(a.act_dtype)) return fail(M3_EINVAL, "m3_scan_fwd: invalid act_dtype");
-  if (!pow2(a.d_state) || a.d_state < 4 || a.d_state > 128) {
-    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: d_state %d must be a power of 2 in [4, 128]",
-                a.d_state);
+  if (a.d_state < 4) return fail(M3_EUNSUPPORTED, "m3_scan_fwd: d_state %d < 4", a.d_state);
+  if (!tiled_shape(a) && !rscan_fits(a)) {
+    return fail(M3_EUNSUPPORTED,
+                "m3_scan_fwd: rank %d, d_state %d, head_dim %d, %d angles: above 8 ranks or "
+                "160 KiB of LDS for the recurrent scan",
+                a.rank, a.d_state, a.head_dim, a.num_angles);
   }
-  if (a.head_dim > kPPad) {
-    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: head_dim %d > %d", a.head_dim, kPPad);
-  }
-  if (a.num_angles > kSMax) {
-    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: num_angles %d > %d", a.num_angles, kSMax);
+  if (!tiled_shape(a) && a.segments > 1) {
+    return fail(M3_EUNSUPPORTED, "m3_scan_fwd: segments > 1 need a shape the MFMA kernel tiles");
   }
   if (a.phase_mode < M3_PHASE_NONE || a.phase_mode > M3_PHASE_ANGLES) {
     return fail(M3_EINVAL, "m3_scan_fwd: invalid phase_mode");
@@ -2739,6 +2748,10 @@ extern "C" int m3_scan_workspace_size(const m3_scan_args* args, size_t* bytes) {
     return m3::fail(M3_EINVAL, "m3_scan_workspace_size: NULL argument");
   }
   m3::ScanGeom g{};
+  if (!m3::tiled_shape(*args)) {  // the recurrent scan needs no workspace
+    *bytes = 0;
+    return M3_OK;
+  }
   const int G = m3::segments_for(*args);
   *bytes = G > 1 ? m3::plan_segments(*args, G).total_bytes : m3::ws_layout(*args, g);
   return M3_OK;
@@ -2752,6 +2765,7 @@ extern "C" int m3_scan_fwd(const m3_scan_args* args, hipStream_t stream) {
   int rc = validate_scan(a);
   if (rc != M3_OK) return rc;
   if (a.batch == 0) return M3_OK;
+  if (!tiled_shape(a)) return launch_recurrent_scan(a, stream);
   switch (a.act_dtype) {
     case M3_F32: return launch_scan<float>(a, stream);
     case M3_BF16: return launch_scan<__bf16>(a, stream);

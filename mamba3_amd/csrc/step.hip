@@ -1139,11 +1139,7 @@ extern "C" int m3_step(const m3_step_args* args, hipStream_t stream) {
   }
   if (a.heads % a.groups != 0) return fail(M3_EINVAL, "m3_step: heads %% groups != 0");
   if (!valid_dtype(a.act_dtype)) return fail(M3_EINVAL, "m3_step: invalid act_dtype");
-  if (!pow2(a.d_state) || a.d_state < 4 || a.d_state > 256) {
-    return fail(M3_EUNSUPPORTED, "m3_step: d_state %d must be a power of 2 in [4, 256]",
-                a.d_state);
-  }
-  if (a.head_dim > 256) return fail(M3_EUNSUPPORTED, "m3_step: head_dim > 256");
+  if (a.d_state < 4) return fail(M3_EUNSUPPORTED, "m3_step: d_state %d < 4", a.d_state);
   if (a.phase_mode != M3_PHASE_NONE && a.phase_mode != M3_PHASE_ANGLES) {
     return fail(M3_EINVAL, "m3_step: phase_mode must be NONE or ANGLES");
   }
@@ -1152,9 +1148,17 @@ extern "C" int m3_step(const m3_step_args* args, hipStream_t stream) {
     return fail(M3_EUNSUPPORTED, "m3_step: num_angles %d does not fit d_state %d (mimo=%d)",
                 a.num_angles, a.d_state, a.mimo_rotation);
   }
-  if (a.num_angles > 256) return fail(M3_EUNSUPPORTED, "m3_step: num_angles > 256");
-  if (step_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles) > 64 * 1024) {
-    return fail(M3_EUNSUPPORTED, "m3_step: shape needs more than 64 KiB of LDS");
+  // The step kernels take d_state a power of 2 up to 256, head_dim and num_angles up to 256,
+  // ranks 1, 2, 4 and 8, within 64 KiB of LDS; other shapes run as a one-token recurrent scan.
+  const bool native = pow2(a.d_state) && a.d_state <= 256 && a.head_dim <= 256 &&
+                      a.num_angles <= 256 &&
+                      (a.rank == 1 || a.rank == 2 || a.rank == 4 || a.rank == 8) &&
+                      step_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles) <= 64 * 1024;
+  if (!native && !rscan_fits(step_as_scan(a))) {
+    return fail(M3_EUNSUPPORTED,
+                "m3_step: rank %d, d_state %d, head_dim %d, %d angles: above 8 ranks or 160 KiB "
+                "of LDS",
+                a.rank, a.d_state, a.head_dim, a.num_angles);
   }
   const int act = a.act_dtype;
   const int N = a.d_state, P = a.head_dim;
@@ -1191,6 +1195,8 @@ extern "C" int m3_step(const m3_step_args* args, hipStream_t stream) {
       (a.q_bias.ptr == nullptr) != (a.k_bias.ptr == nullptr)) {
     return fail(M3_EINVAL, "m3_step: q/k norm weights and biases come in pairs");
   }
+  if (a.batch == 0) return M3_OK;
+  if (!native) return launch_recurrent_step(a, stream);
   // 16-byte state vectors.
   for (const m3_tensor* t : {&a.state_in, &a.state_out}) {
     if (reinterpret_cast<uintptr_t>(t->ptr) % 16 != 0 || t->stride[0] % 4 != 0 ||
@@ -1198,7 +1204,6 @@ extern "C" int m3_step(const m3_step_args* args, hipStream_t stream) {
       return fail(M3_EUNSUPPORTED, "m3_step: state tensors need 16-byte aligned rows");
     }
   }
-  if (a.batch == 0) return M3_OK;
   switch (act) {
     case M3_F32: return launch_step<float>(a, stream);
     case M3_BF16: return launch_step<__bf16>(a, stream);

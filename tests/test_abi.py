@@ -95,10 +95,13 @@ def test_null_arguments_are_rejected_without_touching_the_device(lib):
 
 
 def test_scan_validation_on_the_host(lib):
-    args = _hip.ScanArgs(batch=1, length=4, heads=2, groups=1, rank=1, d_state=12,
-                         head_dim=8, num_angles=3)
+    args = _hip.ScanArgs(batch=1, length=4, heads=2, groups=1, rank=1, d_state=2,
+                         head_dim=8, num_angles=1)
     rc = lib.m3_scan_fwd(ctypes.byref(args), None)
-    assert rc == 2 and b"power of 2" in lib.m3_last_error()
+    assert rc == 2 and b"d_state 2 < 4" in lib.m3_last_error()
+    args.d_state = 12  # not a power of 2: the recurrent scan, which checks the same tensors
+    rc = lib.m3_scan_fwd(ctypes.byref(args), None)
+    assert rc == 1 and b"q: required tensor is NULL" in lib.m3_last_error()
     args.d_state = 16
     rc = lib.m3_scan_fwd(ctypes.byref(args), None)
     assert rc == 1 and b"q: required tensor is NULL" in lib.m3_last_error()
@@ -110,7 +113,7 @@ def test_scan_validation_on_the_host(lib):
 def test_step_validation_on_the_host(lib):
     args = _hip.StepArgs(batch=1, heads=2, groups=1, rank=3, d_state=16, head_dim=8,
                          num_angles=4, phase_mode=_hip.PHASE_ANGLES, mimo_rotation=1)
-    # rank 3 is rejected only at launch; the angle count check comes first for MIMO
+    # rank 3 runs as a one-token recurrent scan; the angle count check comes first for MIMO
     args.num_angles = 3
     assert lib.m3_step(ctypes.byref(args), None) == 2
     assert b"num_angles" in lib.m3_last_error()
@@ -286,3 +289,24 @@ def test_noalloc_scan_rejects_calls_beyond_its_scratch(lib):
     assert rc == 4  # M3_EWORKSPACE
     assert b"scratch" in lib.m3_last_error()
     assert lib.m3_scan_fwd_noalloc(None, None) == 1
+
+
+def test_recurrent_shapes_need_no_workspace(lib):
+    """Shapes the MFMA scan does not tile take the recurrent scan, which needs no workspace and
+    cannot be split into segments; d_state below 4 is refused."""
+    def args(**kw):
+        base = dict(batch=2, length=100, heads=2, groups=1, rank=1, d_state=96, head_dim=32,
+                    num_angles=24, chunk=64, act_dtype=_hip.BF16, mimo_rotation=0, raw_dt=0,
+                    phase_mode=_hip.PHASE_GIVEN, norm_eps=1e-5, segments=0)
+        base.update(kw)
+        return _hip.ScanArgs(**base)
+    need = ctypes.c_size_t(123)
+    assert lib.m3_scan_workspace_size(ctypes.byref(args()), ctypes.byref(need)) == 0
+    assert need.value == 0
+    assert lib.m3_scan_workspace_size(ctypes.byref(args(d_state=128, num_angles=32, head_dim=64)),
+                                      ctypes.byref(need)) == 0
+    assert need.value > 0
+    assert lib.m3_scan_fwd(ctypes.byref(args(segments=4)), None) == 2
+    assert b"segments" in lib.m3_last_error()
+    assert lib.m3_scan_fwd(ctypes.byref(args(d_state=2, num_angles=0)), None) == 2
+    assert lib.m3_scan_fwd(ctypes.byref(args(rank=9, mimo_rotation=1)), None) == 2

@@ -36,7 +36,8 @@ def _gpu_ctx(bf16: bool):
         "cuda", enabled=False)
 
 
-CASES = [(64, 16, 2, 1), (64, 16, 2, 4), (128, 128, 2, 1), (128, 128, 1, 4), (32, 8, 2, 1)]
+CASES = [(64, 16, 2, 1), (64, 16, 2, 4), (128, 128, 2, 1), (128, 128, 1, 4), (32, 8, 2, 1),
+         (64, 16, 2, 8), (128, 128, 1, 8)]
 
 
 @pytest.mark.parametrize("bf16", [False, True])
@@ -298,3 +299,46 @@ def test_config1_parity():
     torch.testing.assert_close(got.cpu(), want, **F32)
     torch.testing.assert_close(prefix.cpu(), want[:, :960], **F32)
     torch.testing.assert_close(steps, want[:, 960:], **F32)
+
+
+# Models whose shapes the MFMA scan does not tile (the recurrent scan), and whose decode step
+# runs on the step kernels (d_state 256) or as a one-token recurrent scan (d_state not a power
+# of 2, rank 3): forward, prefill and steps against the oracle.
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("case", [(64, 256, 1, 1), (48, 96, 2, 1), (32, 8, 2, 3), (64, 64, 1, 6)])
+def test_recurrent_shapes_match_oracle(case, bf16):
+    d_model, d_state, depth, rank = case
+    model, params, dims = _model(d_model, d_state, depth, rank, seed=30 + rank)
+    torch.manual_seed(31)
+    x = torch.randn(2, 75, d_model)
+    split = 66
+    with torch.inference_mode(), _oracle_ctx(bf16):
+        want = op.model_forward(params, x, dims)
+        want_prefix, want_cache = op.model_prefill(params, x[:, :split], dims)
+        want_steps = []
+        for t in range(split, x.shape[1]):
+            o, want_cache = op.model_step(params, x[:, t:t + 1], dims, want_cache)
+            want_steps.append(o)
+        want_steps = torch.cat(want_steps, 1)
+    xd = x.to(DEV)
+    with torch.inference_mode(), _gpu_ctx(bf16):
+        got = model(xd)
+        assert ops._HIP_LAST_SCAN_DISPATCH
+        prefix, cache = model.prefill(xd[:, :split])
+        steps = []
+        for t in range(split, x.shape[1]):
+            o, cache = model.step(xd[:, t:t + 1], cache)
+            assert ops._HIP_LAST_DISPATCH
+            steps.append(o)
+        steps = torch.cat(steps, 1)
+    torch.cuda.synchronize()
+    tol = BF16 if bf16 else F32
+    print(f"recurrent model {case} bf16={bf16}: forward "
+          f"{(got.float().cpu() - want.float()).abs().max():.2e} steps "
+          f"{(steps.float().cpu() - want_steps.float()).abs().max():.2e}", flush=True)
+    torch.testing.assert_close(got.float().cpu(), want.float(), **tol)
+    torch.testing.assert_close(prefix.float().cpu(), want_prefix.float(), **tol)
+    torch.testing.assert_close(steps.float().cpu(), want_steps.float(), **tol)
+    for layer, want_layer in zip(cache, want_cache):
+        for a, b in zip(layer, want_layer):
+            torch.testing.assert_close(a.float().cpu(), b.float(), **tol)

@@ -125,7 +125,7 @@ def _check(dtype, y, s, y_ref, s_ref, inp=None, chunk=None):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("rank", [1, 2, 4])
+@pytest.mark.parametrize("rank", [1, 2, 4, 8])
 def test_scan_matches_oracle(dtype, rank):
     inp = _inputs(rank, dtype, seed=rank)
     y, s, y_ref, s_ref = _run_both(inp, chunk=_kernel_chunk(dtype, rank))
@@ -134,7 +134,7 @@ def test_scan_matches_oracle(dtype, rank):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("rank", [1, 2, 4])
+@pytest.mark.parametrize("rank", [1, 2, 4, 8])
 def test_scan_matches_oracle_at_reference_chunk(dtype, rank):
     inp = _inputs(rank, dtype, seed=rank, length=300)
     y, s, y_ref, s_ref = _run_both(inp, chunk=_reference_chunk(rank))
@@ -265,3 +265,35 @@ def test_chunk_state_matches_oracle(dtype, rank):
         ops.chunk_state(k.to(DEV), v.to(DEV), cum.to(DEV), scale.to(DEV), state.to(DEV), out,
                         width=width, rank=rank)
     torch.testing.assert_close(out.cpu(), want, rtol=1e-4, atol=1e-4)
+
+
+# Shapes outside the MFMA kernel's tiles (d_state not a power of 2 or above 128, head_dim above
+# 64, ranks 3, 5, 6, 7): the recurrent scan. FP32 within 1e-4 of the oracle's chunked scan (the
+# same recurrence, summed in another order); 16-bit at the 16-bit parity bar.
+RECURRENT = [
+    # (rank, d_state, head_dim, heads, length)
+    (1, 256, 64, 2, 150),
+    (1, 96, 32, 3, 130),
+    (1, 20, 24, 2, 70),
+    (1, 64, 128, 2, 90),
+    (4, 256, 64, 2, 70),
+    (3, 16, 16, 3, 80),
+    (8, 256, 32, 1, 40),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", RECURRENT)
+def test_recurrent_scan_matches_oracle(shape, dtype):
+    rank, d_state, head_dim, heads, length = shape
+    inp = _inputs(rank, dtype, seed=rank + d_state, heads=heads, head_dim=head_dim,
+                  d_state=d_state, length=length)
+    chunk = 32
+    dev = {n: (t.to(DEV) if isinstance(t, torch.Tensor) else t) for n, t in inp.items()}
+    with torch.inference_mode():
+        y, s = ops.mamba3_scan(**dev, chunk_size=chunk)
+    assert ops._HIP_LAST_SCAN_DISPATCH
+    torch.cuda.synchronize()
+    y_ref, s_ref = op.ssd_scan(**inp, chunk_size=chunk)
+    _report(f"recurrent scan {dtype} {shape}", y.cpu(), s.cpu(), y_ref, s_ref)
+    _check(dtype, y.cpu(), s.cpu(), y_ref, s_ref, inp, chunk)
