@@ -409,6 +409,7 @@ struct Feed {
   // FULL
   __amdgpu_buffer_rsrc_t rs_p, rs_w;
   int o_qk, o_vz, d_q1, d_k, d_z, tok_b;  // per-lane byte offsets at token 0, uniform deltas
+  int d_hi = 8;  // MIMO projection form: byte offset of a row's second 4-column chunk
   int side_o, side_s, ang_o, ang_s;        // per-lane workspace byte offsets at sub-chunk 0, strides
   // BUF: resources of q, k, value, gate and the given phases; per-lane byte offsets at token 0,
   // the byte strides of a token and the second row's delta
@@ -568,7 +569,20 @@ struct Feed {
 
   __device__ __forceinline__ void words_qk(int t0, int nw, bool qk_on, uint32_t (&rq)[2][W8],
                                            uint32_t (&rk)[2][W8]) const {
-    if constexpr (FULL) {
+    if constexpr (FULL && R > 1 && ES == 2) {
+      // MIMO: two 4-column chunks per row, d_hi apart (a rotation pair's partners, or adjacent)
+      const int tb = t0 * tok_b;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        uint32_t lo[2], hi[2];
+        bload_words<2>(lo, rs_p, o_qk + tb + j * d_q1);
+        bload_words<2>(hi, rs_p, o_qk + tb + j * d_q1 + d_hi);
+        rq[j][0] = lo[0]; rq[j][1] = lo[1]; rq[j][2] = hi[0]; rq[j][3] = hi[1];
+        bload_words<2>(lo, rs_p, o_qk + tb + j * d_q1 + d_k);
+        bload_words<2>(hi, rs_p, o_qk + tb + j * d_q1 + d_k + d_hi);
+        rk[j][0] = lo[0]; rk[j][1] = lo[1]; rk[j][2] = hi[0]; rk[j][3] = hi[1];
+      }
+    } else if constexpr (FULL) {
       // unconditional, also for lanes without a q/k or v/z role: every offset stays inside a
       // buffer or past its extent, where the load returns zero
       const int tb = t0 * tok_b;
@@ -1037,6 +1051,12 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // SISO model shape: q / k lanes split by column half, waves 0-3 holding the rotated columns;
   // the phase on waves 0-3 only, 8 tokens per lane (their compute interval is the shorter one)
   constexpr bool SPLIT = (FULL || SHAPE) && R == 1 && !F32;
+  // MIMO model shape in projection form: q / k lanes split by rotation role as well. Waves 0-3
+  // hold the rotated pairs (n, n + 64), n < 32, four pairs per lane (the MIMO rotation pairs
+  // quarter 1 with quarter 3, model.py:201-213, ops.py:35-84), waves 4-7 eight consecutive
+  // columns of the unrotated quarters 2 and 4: no lane exchanges a partner, and only the rotated
+  // half does rotation arithmetic.
+  constexpr bool MSPLIT = FULL && R > 1 && !F32;
   constexpr int TPL = SPLIT ? 8 : 4;   // tokens per phase lane
   constexpr int PG = TOK / TPL;        // phase lanes per angle
   // swizzle keys of the transposed tiles, n >> KSH for KT and p >> VSH for VT. 16-bit: constant
@@ -1084,11 +1104,18 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // ---- lane roles
   // q / k: row pair rp (rows 2rp, 2rp+1), columns n0 .. n0+7 (SPLIT: waves 0-3 columns 0-63,
   // waves 4-7 columns 64-127)
-  const int rp = SPLIT ? (tid & 255) >> 3 : tid >> 4;
-  const int n0 = SPLIT ? 64 * (tid >> 8) + 8 * (tid & 7) : 8 * (tid & 15);
-  // (SPLIT: every lane has both roles, 512 threads covering 64 rows x 128 columns and 64 tokens x
-  // 64 columns)
-  const bool qk_on = SPLIT || (rp < ROWS / 2 && n0 < N);
+  const int rp = (SPLIT || MSPLIT) ? (tid & 255) >> 3 : tid >> 4;
+  const int n0 = SPLIT    ? 64 * (tid >> 8) + 8 * (tid & 7)
+                 : MSPLIT ? (tid < 256 ? 4 * (tid & 7)
+                                       : ((tid & 7) < 4 ? 32 + 8 * (tid & 7) : 64 + 8 * (tid & 7)))
+                          : 8 * (tid & 15);
+  // the lane's i-th column (MSPLIT rotated lanes: n0 .. n0+3, then their partners n0+64 ..)
+  auto col_of = [&](int i) {
+    return (MSPLIT && tid < 256) ? (i < 4 ? n0 + i : n0 + 60 + i) : n0 + i;
+  };
+  // (SPLIT / MSPLIT: every lane has both roles, 512 threads covering 64 rows x 128 columns and
+  // 64 rows x 64 columns)
+  const bool qk_on = SPLIT || MSPLIT || (rp < ROWS / 2 && n0 < N);
   const int qk_n = min(8, N - n0);
   // v / z: row pair vp (rows 2vp, 2vp+1; tokens 2vp, 2vp+1 for R = 1), columns p0 .. p0+3
   constexpr int P4 = kPPad / 4;
@@ -1132,7 +1159,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   float wq[8], wk[8], bq[NB][8], bk[NB][8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int n = n0 + i;
+    const int n = col_of(i);
     const bool ok = qk_on && n < N;
     wq[i] = (ok && norm) ? rnd<T>(ldx(a.q_norm_w.ptr, a.q_norm_w.dtype, n * a.q_norm_w.stride[0]))
                          : 1.f;
@@ -1216,6 +1243,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // ---- per-token reads
   Feed<T, R, FULL, SHAPE> fd;
   fd.init(a, g, prep, b, h, grp, rp, n0, vp, p0, N, P, norm);
+  if constexpr (MSPLIT) fd.d_hi = (col_of(4) - n0) * ES;
   float* fph = a.final_phase.ptr != nullptr
                    ? static_cast<float*>(a.final_phase.ptr) + b * a.final_phase.stride[0] +
                          h * a.final_phase.stride[1] + ps * a.final_phase.stride[2]
@@ -1347,7 +1375,25 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           q[i] = fmaf(raw_get<T>(rq[j], i), fq[j] * wq[i], bq[R == 1 ? 0 : j][i]);
           k[i] = fmaf(raw_get<T>(rk[j], i), fk[j] * wk[i], bk[R == 1 ? 0 : j][i]);
         }
-        if constexpr (SPLIT) {
+        if constexpr (MSPLIT) {
+          // pairs (n0 + i, n0 + 64 + i), angles n0 + i, i < 4 (waves 0-3)
+          if (ROT) {
+            const float* tr = CSt + tt * CST;
+            const f4 c01 = *reinterpret_cast<const f4*>(tr + 2 * n0);
+            const f4 c23 = *reinterpret_cast<const f4*>(tr + 2 * n0 + 4);
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+              const f4& cv = pp < 2 ? c01 : c23;
+              const float cc = cv[2 * (pp & 1)], ss = cv[2 * (pp & 1) + 1];
+              const float q0 = q[pp], q1 = q[pp + 4];
+              const float k0 = k[pp], k1 = k[pp + 4];
+              q[pp] = fmaf(q0, cc, -(q1 * ss));
+              q[pp + 4] = fmaf(q0, ss, q1 * cc);
+              k[pp] = fmaf(k0, cc, -(k1 * ss));
+              k[pp + 4] = fmaf(k0, ss, k1 * cc);
+            }
+          }
+        } else if constexpr (SPLIT) {
           // pairs (2j, 2j+1), j = n0/2 .. n0/2+3: the rotated columns are waves 0-3's (SHAPE:
           // when the call rotates)
           if (ROT && (FULL || rotate)) {
@@ -1399,8 +1445,22 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
             k[i] = fmaf(kp[i], ss, k[i] * cc);
           }
         }
-        if constexpr (!SO) st_row8<T>(Qs + row * LQ + n0, q);
-        st_row8<T>(Ks + row * LQ + n0, k);
+        if (MSPLIT && ROT) {
+          f4 lo, hi;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) { lo[i] = q[i]; hi[i] = q[i + 4]; }
+          if constexpr (!SO) {
+            st_quad<T>(Qs + row * LQ + n0, lo);
+            st_quad<T>(Qs + row * LQ + n0 + 64, hi);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) { lo[i] = k[i]; hi[i] = k[i + 4]; }
+          st_quad<T>(Ks + row * LQ + n0, lo);
+          st_quad<T>(Ks + row * LQ + n0 + 64, hi);
+        } else {
+          if constexpr (!SO) st_row8<T>(Qs + row * LQ + n0, q);
+          st_row8<T>(Ks + row * LQ + n0, k);
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
       }
@@ -1412,13 +1472,13 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       const float e1 = SC[SB_::SCL + r1] * __expf(cl - SC[SB_::CUM + r1]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int n = n0 + i;
+        const int n = col_of(i);
         if (FIX || n < N) {
           st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> KSH), kt[0][i] * e0, kt[1][i] * e1);
         }
       }
     };
-    if constexpr (SPLIT) {
+    if constexpr (SPLIT || MSPLIT) {
       if (w < 4) {
         stage_qk(std::true_type{});
       } else {
@@ -1749,12 +1809,21 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         if (R > 1) y[i] *= F[Lay::MO + rr * kPPad + pb + i];
       }
       if constexpr (R > 1) {
-        // MIMO rank sum over the R consecutive lanes of one token (within a 16-lane row)
+        // MIMO rank sum over the R consecutive lanes of one token (within a 16-lane row): DPP
+        // quad permutes for lane ^ 1 and lane ^ 2, a swizzle for lane ^ 4 (no LDS access)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float t = y[i];
-#pragma unroll
-          for (int o = 1; o < R; o <<= 1) t += __shfl_xor(t, o, 16);
+          t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                             0, __builtin_bit_cast(int, t), 0xb1, 0xf, 0xf, false));
+          if constexpr (R >= 4) {
+            t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                               0, __builtin_bit_cast(int, t), 0x4e, 0xf, 0xf, false));
+          }
+          if constexpr (R >= 8) {
+            t += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, t),
+                                                                       0x101f));
+          }
           y[i] = t;
         }
       }
