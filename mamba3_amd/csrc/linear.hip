@@ -11,6 +11,14 @@
 // into registers: no LDS staging, no barrier in the K loop. A workgroup owns 16 * TN columns;
 // its waves split the K range and add their sums through LDS at the end.
 //
+// gemv kernel (M <= 4, K a multiple of 512 up to 4096): the same weight stream without MFMA.
+// Each wave owns RW weight rows whose K range it reads whole, lane l taking the 16-byte chunks
+// 8 (l + 64 c): one load instruction covers 1 KB of one row, and all of a lane's chunks are in
+// flight at once (K / 512 per row). x goes to LDS once per workgroup (normed as in the rows
+// kernel); each wave reduces its rows over its 64 lanes, so no sums cross waves. Measured on the
+// decode shapes (N 8672, K 2048: 35.5 MB), this layout streams about 1.6x faster than 16 rows of
+// 64-byte pieces per instruction.
+//
 // tile kernel (M > 32): one 256-thread workgroup (4 waves) owns MT rows x NT columns; x and
 // weight tiles are staged through LDS (double buffered, KS elements of K per stage, rows padded
 // by 8 elements so the 16 rows one MFMA operand reads fall in distinct 16-byte bank groups).
@@ -219,6 +227,142 @@ __global__ __launch_bounds__(64 * WAVES) void linear_rows_kernel(const LinGeom g
   }
 }
 
+// ----------------------------------------------------------------------------- gemv kernel
+
+constexpr int kGemvRows = 4;  // x rows (M) the gemv kernel takes
+
+// Sum over the 64 lanes of a wave: DPP rotations within each 16-lane row, then the rows.
+__device__ __forceinline__ float lin_wave_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128,
+                                                             0xf, 0xf, false));  // row_ror:8
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124,
+                                                             0xf, 0xf, false));  // row_ror:4
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122,
+                                                             0xf, 0xf, false));  // row_ror:2
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121,
+                                                             0xf, 0xf, false));  // row_ror:1
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// Wave w of workgroup b owns weight rows RW (4 b + w) .. + RW - 1 (rows past N are read as zeros
+// through the buffer extent and never written). CH >= K / 512 chunks per lane and row.
+template <typename T, int RW, int CH, bool NORM>
+__global__ __launch_bounds__(256) void linear_gemv_kernel(const LinGeom g) {
+  using V8 = typename LinMma<T>::v8;
+  constexpr int XU = (64 * CH + 255) / 256;  // x chunks per thread and row
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = (4 * blockIdx.x + w) * RW;
+  const int nk = g.k / 512, xk = g.k / 8;  // chunks per lane and row; chunks per x row
+
+  // x (and the norm weight) first: small, mostly from L2; then every weight chunk of the wave
+  const __amdgpu_buffer_rsrc_t rx = lin_rsrc(g.x, lin_extent(g.m, g.x_ld, g.k));
+  const __amdgpu_buffer_rsrc_t rn = lin_rsrc(g.nw, NORM ? int64_t{2} * g.k : 0);
+  const __amdgpu_buffer_rsrc_t rw = lin_rsrc(g.w, lin_extent(g.n, g.w_ld, g.k));
+  u32x4 xv[kGemvRows][XU], nv[XU];
+#pragma unroll
+  for (int u = 0; u < XU; ++u) {
+    const int kc = tid + 256 * u;
+#pragma unroll
+    for (int m = 0; m < kGemvRows; ++m) {
+      xv[m][u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rx, m < g.m && kc < xk ? (m * g.x_ld + 8 * kc) * 2
+                                                                      : kOff, 0, 0));
+    }
+    if constexpr (NORM) {
+      nv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rn, kc < xk ? 16 * kc : kOff, 0, 0));
+    }
+  }
+  u32x4 wv[RW][CH];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const bool live = n0 + r < g.n && c < nk;
+      wv[r][c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rw, live ? ((n0 + r) * g.w_ld + 8 * (lane + 64 * c)) * 2
+                                                        : kOff, 0, 0));
+    }
+  }
+
+  // x rows to LDS: a = rnd(x * nw) with NORM (the RMS factor is applied to the sums), else x.
+  // Branch-free: chunks past M or K were loaded as zeros and land in rows / columns no lane
+  // reads (256 XU chunks = 512 CH elements per row), so no load is sunk behind a branch whose
+  // wait would also wait for the weight stream.
+  __shared__ __attribute__((aligned(16))) T xs[kGemvRows][512 * CH];
+  __shared__ float red[4][kGemvRows];
+  static_assert(256 * XU * 8 <= 512 * CH, "x chunks fit the LDS rows");
+  float ssq[kGemvRows];
+#pragma unroll
+  for (int m = 0; m < kGemvRows; ++m) {
+    ssq[m] = 0.f;
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+      const int kc = tid + 256 * u;
+      V8 a = __builtin_bit_cast(V8, xv[m][u]);
+      if constexpr (NORM) {
+        const V8 nw = __builtin_bit_cast(V8, nv[u]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float xf = static_cast<float>(a[e]);
+          ssq[m] = fmaf(xf, xf, ssq[m]);
+          a[e] = static_cast<T>(xf * static_cast<float>(nw[e]));
+        }
+      }
+      *reinterpret_cast<V8*>(&xs[m][8 * kc]) = a;
+    }
+    if constexpr (NORM) {
+      const float v = lin_wave_sum(ssq[m]);
+      if (lane == 0) red[w][m] = v;
+    }
+  }
+  __syncthreads();
+
+  float acc[RW][kGemvRows];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+#pragma unroll
+    for (int m = 0; m < kGemvRows; ++m) acc[r][m] = 0.f;
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    if (c < nk) {
+#pragma unroll
+      for (int m = 0; m < kGemvRows; ++m) {
+        if (m < g.m) {
+          const V8 a = *reinterpret_cast<const V8*>(&xs[m][8 * (lane + 64 * c)]);
+#pragma unroll
+          for (int r = 0; r < RW; ++r) {
+            const V8 wr = __builtin_bit_cast(V8, wv[r][c]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              acc[r][m] = fmaf(static_cast<float>(a[e]), static_cast<float>(wr[e]), acc[r][m]);
+            }
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kGemvRows; ++m) {
+    if (m < g.m) {
+      float scale = 1.f;
+      if constexpr (NORM) {
+        scale = rsqrtf((red[0][m] + red[1][m] + red[2][m] + red[3][m]) /
+                           static_cast<float>(g.k) + g.eps);
+      }
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        const float y = lin_wave_sum(acc[r][m]);
+        if (lane == 0 && n0 + r < g.n) lin_emit<T>(g, 0, m, n0 + r, y * scale);
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------------------------- tile kernel
 
 // Workgroup tile MT x NT, WM x WN waves, each wave (MT / WM) x (NT / WN) of 16x16 MFMA tiles;
@@ -367,8 +511,8 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const LinGeom g) {
 // A launch: the kernel and its shape. rows kernel: cfg = TM, TN, WAVES and ring depth d; tile
 // kernel: cfg = MT, NT, KS (wave layout and ring depth follow from them).
 struct LinPlan {
-  bool rows;
-  int a, b, c, d;     // rows: TM, TN, WAVES, D; tile: MT, NT, KS
+  bool rows, gemv;
+  int a, b, c, d;     // rows: TM, TN, WAVES, D; tile: MT, NT, KS; gemv: RW, CH
   int gx, gy, splits, k_split;
 };
 
@@ -384,6 +528,17 @@ void split_k(LinPlan& p, int64_t k, int64_t tiles, int64_t want, int64_t unit) {
 
 LinPlan plan(int64_t m, int64_t n, int64_t k, bool norm) {
   LinPlan p{};
+  if (m <= kGemvRows && k % 512 == 0 && k <= 4096) {
+    // gemv kernel: two rows per wave while that leaves 1024 or more workgroups, else one
+    p.gemv = true;
+    p.a = cdiv(n, 8) >= 1024 ? 2 : 1;
+    p.b = k <= 2048 ? 4 : 8;
+    p.gx = static_cast<int>(cdiv(n, 4 * p.a));
+    p.gy = 1;
+    p.splits = 1;
+    p.k_split = static_cast<int>(k);
+    return p;
+  }
   if (m <= 32) {
     // rows kernel: 16 columns per workgroup, 4 waves splitting K. Measured on the decode shapes
     // (N 8672 / 2048, K 2048 / 4096, cold weights), one launch that keeps K whole beats a K
@@ -505,10 +660,31 @@ void launch_tile(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
                      dim3(256), 0, stream, g);
 }
 
+template <typename T, int RW, int CH>
+void launch_gemv(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
+  if (g.nw != nullptr) {
+    hipLaunchKernelGGL((linear_gemv_kernel<T, RW, CH, true>), dim3(p.gx), dim3(256), 0, stream, g);
+  } else {
+    hipLaunchKernelGGL((linear_gemv_kernel<T, RW, CH, false>), dim3(p.gx), dim3(256), 0, stream, g);
+  }
+}
+
 // The compiled shapes; a plan naming any other is refused.
 template <typename T>
 int launch_plan(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
-  if (p.rows) {
+  if (p.gemv) {
+    if (p.a == 2 && p.b == 4) {
+      launch_gemv<T, 2, 4>(g, p, stream);
+    } else if (p.a == 2 && p.b == 8) {
+      launch_gemv<T, 2, 8>(g, p, stream);
+    } else if (p.a == 1 && p.b == 4) {
+      launch_gemv<T, 1, 4>(g, p, stream);
+    } else if (p.a == 1 && p.b == 8) {
+      launch_gemv<T, 1, 8>(g, p, stream);
+    } else {
+      return fail(M3_EUNSUPPORTED, "m3_linear: no gemv kernel %d/%d", p.a, p.b);
+    }
+  } else if (p.rows) {
     if (p.a == 1 && p.b == 1 && p.c == 4) {
       launch_rows<T, 1, 1, 4>(g, p, stream);
     } else if (p.a == 2 && p.b == 1 && p.c == 4) {

@@ -145,8 +145,9 @@ def _linear_args(m: int, n: int, k: int) -> _hip.LinearArgs:
 
 def test_linear_validation_and_workspace_on_the_host(lib):
     size = ctypes.c_size_t(0)
-    # one row against 512 x 4096: 32 column workgroups, K split in two -> two FP32 partials
-    args = _linear_args(1, 512, 4096)
+    # one row against 512 x 4064 (K not a multiple of 512: the rows kernel): 32 column
+    # workgroups, K split in two -> two FP32 partials
+    args = _linear_args(1, 512, 4064)
     assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 0
     assert size.value == 2 * 1 * 512 * 4
     # ... unless the RMSNorm is fused in, which keeps K whole in one workgroup
@@ -154,13 +155,14 @@ def test_linear_validation_and_workspace_on_the_host(lib):
     args.norm_weight.stride[0] = 1
     assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 0
     assert size.value == 0
-    # the decode shapes run unsplit: 542 / 128 column workgroups, 2 x 136 tiles of 256 rows
-    for m, n, k in ((1, 8672, 2048), (16, 2048, 4096), (256, 8672, 2048)):
+    # the decode shapes run unsplit: the gemv kernel up to 4 rows (K a multiple of 512), 542 /
+    # 128 column workgroups, 2 x 136 tiles of 256 rows
+    for m, n, k in ((1, 8672, 2048), (4, 512, 4096), (16, 2048, 4096), (256, 8672, 2048)):
         args = _linear_args(m, n, k)
         assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 0
         assert size.value == 0
     # a split call without its workspace is refused before any launch
-    args = _linear_args(1, 512, 4096)
+    args = _linear_args(1, 512, 4064)
     assert lib.m3_linear(ctypes.byref(args), None) == 4
     assert b"workspace" in lib.m3_last_error()
     args = _linear_args(33, 64, 2048)
@@ -310,3 +312,4 @@ def test_recurrent_shapes_need_no_workspace(lib):
     assert b"segments" in lib.m3_last_error()
     assert lib.m3_scan_fwd(ctypes.byref(args(d_state=2, num_angles=0)), None) == 2
     assert lib.m3_scan_fwd(ctypes.byref(args(rank=9, mimo_rotation=1)), None) == 2
+

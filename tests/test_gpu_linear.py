@@ -32,7 +32,12 @@ def _check(got: torch.Tensor, x, w, residual=None):
 
 
 SHAPES = [
-    (1, 8672, 2048),    # decode B = 1 in_proj (K split)
+    (1, 8672, 2048),    # decode B = 1 in_proj (the gemv kernel, two rows per wave)
+    (2, 2048, 4096),    # decode B = 2 out_proj (gemv, one row per wave, 8 chunks per lane)
+    (3, 1001, 512),     # gemv: one chunk per lane, N not a multiple of the 4 rows a workgroup owns
+    (4, 7, 1536),       # gemv: fewer rows than one workgroup, K / 512 odd
+    (4, 8195, 1024),    # gemv: two rows per wave, the last wave half past N
+    (5, 2048, 2048),    # five rows: the rows kernel
     (7, 2048, 4096),    # out_proj, ragged rows
     (16, 1000, 2048),   # N not a multiple of the tile
     (33, 8672, 2048),   # the 64-row tile, ragged
@@ -60,7 +65,8 @@ def test_linear_matches_fp32_reference(shape, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shape", [(1, 8672, 2048), (5, 2048, 4096), (16, 1000, 2048),
+@pytest.mark.parametrize("shape", [(1, 8672, 2048), (2, 8672, 2048), (3, 1001, 4096),
+                                   (4, 13, 512), (5, 2048, 4096), (16, 1000, 2048),
                                    (32, 4144, 1024)])
 def test_linear_fused_rms_norm_matches_fp32_reference(shape, dtype):
     """norm_weight: x is RMS-normalised first. The kernel rounds x * norm_weight (not the
@@ -95,6 +101,21 @@ def test_linear_strided_views_and_in_place_residual():
     keep = res.clone()
     with torch.inference_mode():
         out = ops.linear(x, w, res, out=res)  # out aliases the residual
+    assert out.data_ptr() == res.data_ptr()
+    _check(out, x, w, keep)
+
+
+def test_linear_gemv_strided_rows_and_in_place_residual():
+    """The gemv kernel (M <= 4) with strided x / weight rows and out aliasing the residual."""
+    g = torch.Generator(device="cpu").manual_seed(5)
+    big_x = torch.randn(9, 2048 + 64, generator=g).to(torch.bfloat16).to(DEV)
+    big_w = (torch.randn(1030, 2048 + 32, generator=g) / 45).to(torch.bfloat16).to(DEV)
+    x, w = big_x[1:8:2, :2048], big_w[:, 32:]  # 4 rows of stride 4224, weight stride 2080
+    assert x.stride(0) == 4224 and w.stride(0) == 2080
+    res = torch.randn(4, 1030, generator=g).to(torch.bfloat16).to(DEV)
+    keep = res.clone()
+    with torch.inference_mode():
+        out = ops.linear(x, w, res, out=res)
     assert out.data_ptr() == res.data_ptr()
     _check(out, x, w, keep)
 
