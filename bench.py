@@ -207,8 +207,9 @@ def bench_decode(batch, steps, log, rank=1, prefix=2048):
             ops.step_projection(proj, mixer, layer_cache, inplace=True)
 
         iters = 20
-        if batch * mixer.nheads >= 1024:
-            # eager calls: the launch is GPU-bound at this size
+        if batch * mixer.nheads >= 8192:
+            # eager calls: the launch is GPU-bound at this size (at 1024 pairs a 10 us kernel
+            # would time the host's launch rate instead)
             for _ in range(3):
                 step_kernel()
             t_k = _events_time(step_kernel, iters) / iters

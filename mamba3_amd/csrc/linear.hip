@@ -137,8 +137,9 @@ __global__ __launch_bounds__(64 * WAVES) void linear_rows_kernel(const LinGeom g
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
+      // non-temporal (aux bit 1): the weight is streamed once per call
       rb[slot][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  rw, live ? woff[j] + 2 * kStep * s : kOff, 0, 0));
+                                                  rw, live ? woff[j] + 2 * kStep * s : kOff, 0, 2));
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -282,9 +283,10 @@ __global__ __launch_bounds__(256) void linear_gemv_kernel(const LinGeom g) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const bool live = n0 + r < g.n && c < nk;
+      // non-temporal (aux bit 1): each weight byte is read once per call
       wv[r][c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                rw, live ? ((n0 + r) * g.w_ld + 8 * (lane + 64 * c)) * 2
-                                                        : kOff, 0, 0));
+                                                        : kOff, 0, 2));
     }
   }
 
