@@ -31,8 +31,8 @@ SCAN_SEGMENTS = 0
 def heavy_tail_activation(x: torch.Tensor) -> torch.Tensor:
     """``1 + x`` for ``x >= 0``, ``1 / (1 - x)`` otherwise (reference ``ops.py:28-32``).
 
-    Elementwise helper kept for API compatibility (``_Mamba3Mixer._project``); the
-    kernels apply it to the raw ``dd_A`` logits themselves.
+    Kept under the reference's name for callers that import it; no path of this package
+    calls it: the kernels apply the activation to the raw ``dd_A`` logits themselves.
     """
     return torch.where(x >= 0, 1.0 + x, torch.reciprocal(1.0 - x.clamp_max(0)))
 
@@ -377,8 +377,9 @@ class ScanCall:
 
     Holds the argument block, the outputs, the workspace and references to every tensor the
     block points at; ``launch()`` enqueues the call on the device's current stream and may be
-    repeated (each launch rewrites the outputs). Fuses ``_project`` (B/C RMSNorm, dt, adt),
-    ``_phase``, bias, rotation and the chunked SSD (reference ``model.py:282-309``).
+    repeated (each launch rewrites the outputs). Fuses the reference mixer's ``_project`` (B/C
+    RMSNorm, dt, adt; ``model.py:165``), ``_phase`` (``model.py:215``), bias, rotation and the
+    chunked SSD (reference ``model.py:282-309``).
 
     ``reverse=True`` scans the sequence from its last token to its first, reading ``proj`` and
     writing ``out`` through backwards token strides: ``out`` then holds, in forward order,
@@ -449,8 +450,8 @@ def scan_projection(proj: torch.Tensor, mixer, *, cache=None, want_cache: bool =
                     chunk_size: int = 256, reverse: bool = False):
     """The whole mixer scan from the raw ``in_proj`` output ``[B, L, proj]``.
 
-    Fuses ``_project`` (B/C RMSNorm, dt, adt), ``_phase``, bias, rotation and the chunked
-    SSD (reference ``model.py:282-309``). Returns ``(mixed [B,L,H,P], state, final_phase,
+    Fuses the reference mixer's ``_project`` (B/C RMSNorm, dt, adt; ``model.py:165``),
+    ``_phase``, bias, rotation and the chunked SSD (reference ``model.py:282-309``). Returns ``(mixed [B,L,H,P], state, final_phase,
     final_k)``; the last two are ``None`` unless ``want_cache``. ``reverse``: see ``ScanCall``.
     """
     call = ScanCall(proj, mixer, cache=cache, want_cache=want_cache, chunk_size=chunk_size,
@@ -462,8 +463,8 @@ def scan_projection(proj: torch.Tensor, mixer, *, cache=None, want_cache: bool =
 def step_projection(proj: torch.Tensor, mixer, cache, *, inplace: bool = False):
     """One decode token from the raw ``in_proj`` output ``[B, 1, proj]``.
 
-    Fuses ``_project``, ``_expand_qk``, the phase advance, the rotation and the step
-    (reference ``model.py:431-484``). With ``inplace`` the cache tensors are updated in
+    Fuses the reference mixer's ``_project`` and ``_expand_qk`` (``model.py:165``, ``201``),
+    the phase advance, the rotation and the step (reference ``model.py:431-484``). With ``inplace`` the cache tensors are updated in
     place (the hipGraph decoder's static cache) and returned.
     """
     global _HIP_LAST_DISPATCH
