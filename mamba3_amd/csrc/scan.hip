@@ -1588,8 +1588,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     // words of sub-chunk c + 1 into registers; they fly while sub-chunk c computes. FULL issues
     // every load of the loop unconditionally (reads past token L return zero), which keeps the
     // compiler's in-order wait counts exact: no load is waited for before its use. FULL spreads
-    // them over the interval in three groups (q / k, value / gate, side and angle words) pinned
-    // between the compute stages, so the eight waves do not queue all their loads at once.
+    // them over the interval in three groups (q / k at its start, value / gate after the
+    // scores, side and angle words after the phases) pinned between the compute stages, so the
+    // eight waves do not queue all their loads at once.
     auto loads_qk = [&] {
       __builtin_amdgcn_sched_barrier(0);
       fd.words_qk(t0 + TOK, min(TOK, L - t0 - TOK), qk_on, rq, rk);
@@ -1611,6 +1612,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       side = fd.side_in(c + 2);
       ang = fd.ang_in(c + 2);
     }
+
+    // (q / k words first: they are waited for first, at the top of the next iteration)
+    if constexpr (FULL || SHAPE) loads_qk();
 
     // outputs for query row tile `it` and P tiles pj = wp, wp + WPR, ...
     const int it = w / WPR, wp = w - it * WPR;
@@ -1644,7 +1648,6 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         }
       }
     }
-    if constexpr (FULL || SHAPE) loads_qk();
     // K~^T V products of the state carry, issued early (they depend only on staged tiles),
     // accumulated onto the decayed state
 #pragma unroll

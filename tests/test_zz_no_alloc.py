@@ -10,6 +10,7 @@ segments. The calls allocate no device memory.
 from __future__ import annotations
 
 import ctypes
+import gc
 
 import pytest
 import torch
@@ -52,10 +53,18 @@ def test_noalloc_scan_equals_the_workspace_scan(case):
             for t in (call.out, call.final_state, call.final_phase, call.final_k):
                 t.fill_(float("nan"))
             torch.cuda.synchronize()
-            before = torch.cuda.memory_allocated(DEV)
-            _noalloc(call)
-            torch.cuda.synchronize()
-            assert torch.cuda.memory_allocated(DEV) == before
+            # garbage of earlier tests collected now, not during the call: the count below then
+            # moves only if the call allocates
+            gc.collect()
+            gc.disable()
+            try:
+                before = torch.cuda.memory_allocated(DEV)
+                _noalloc(call)
+                torch.cuda.synchronize()
+                after = torch.cuda.memory_allocated(DEV)
+            finally:
+                gc.enable()
+            assert after == before
             got = _outputs(call)
         print(f"noalloc d={d_model} R={rank} {dtype} B={batch} L={length}: workspace "
               f"{0 if call._keep[-1] is None else call._keep[-1].numel()} bytes", flush=True)
