@@ -1153,6 +1153,24 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
                            : 0.f;
   }
 
+  // per-lane constants of the value / gate role (R > 1): the rounded mimo_x / mimo_z of its rows
+  // ranks, (2 vp) % R and the next, at columns p0 .. p0+3, read once here instead of from LDS
+  // in every sub-chunk
+  float mxl[2][4], mzl[2][4];
+#pragma unroll
+  for (int jr = 0; jr < 2; ++jr) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (2 * vp + jr) % R, p = min(p0 + i, P - 1);
+      mxl[jr][i] = R > 1 ? rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
+                                      h * a.mimo_x.stride[0] + r * a.mimo_x.stride[1] + p))
+                         : 1.f;
+      mzl[jr][i] = R > 1 ? rnd<T>(ldx(a.mimo_z.ptr, a.mimo_z.dtype,
+                                      h * a.mimo_z.stride[0] + r * a.mimo_z.stride[1] + p))
+                         : 1.f;
+    }
+  }
+
   // per-lane constants of the q / k role: rounded norm weights and the biases of its rows
   // (rows 2rp, 2rp+1 have ranks (2rp) % R, (2rp+1) % R: one set suffices when R == 1)
   constexpr int NB = R == 1 ? 1 : 2;
@@ -1537,16 +1555,15 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       } else {
         // rows 2vp, 2vp+1: ranks r0, r0 + 1 of token 2vp / R (every lane of the workgroup has a
         // row pair, as for R = 1)
-        const int r0 = (2 * vp) % R;
         f4 vq[2];
 #pragma unroll
         for (int jr = 0; jr < 2; ++jr) {
-          const int r = r0 + jr, row = 2 * vp + jr;
+          const int row = 2 * vp + jr;
           f4 zq;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            vq[jr][i] = mul_r<T>(v[0][i], F[Lay::MX + r * kPPad + p0 + i]);
-            zq[i] = mul_r<T>(z[0][i], F[Lay::MZ + r * kPPad + p0 + i]);
+            vq[jr][i] = mul_r<T>(v[0][i], mxl[jr][i]);
+            zq[i] = mul_r<T>(z[0][i], mzl[jr][i]);
           }
           if constexpr (!SO) {
             st_quad<T>(VR + row * LP + p0, vq[jr]);
