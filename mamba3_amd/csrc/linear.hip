@@ -5,8 +5,9 @@
 // f16 MFMA 16x16x32 (FP32 accumulation), both keeping several K steps of loads in flight per
 // wave in a register ring:
 //
-// rows kernel (M <= 32): a weight stream. The B operand of a 16x16x32 MFMA is, per lane, 16
-// contiguous bytes of one weight row (lane l16 + 16 lg holds row l16, elements 8 lg .. 8 lg + 7
+// rows kernel (M <= 32 where the gemv and wide kernels do not apply): a weight stream. The B
+// operand of a 16x16x32 MFMA is, per lane, 16 contiguous bytes of one weight row (lane
+// l16 + 16 lg holds row l16, elements 8 lg .. 8 lg + 7
 // of the 32-element step), and the A operand the same of an x row, so both are loaded straight
 // into registers: no LDS staging, no barrier in the K loop. A workgroup owns 16 * TN columns;
 // its waves split the K range and add their sums through LDS at the end.
@@ -18,6 +19,15 @@
 // kernel); each wave reduces its rows over its 64 lanes, so no sums cross waves. Measured on the
 // decode shapes (N 8672, K 2048: 35.5 MB), this layout streams about 1.6x faster than 16 rows of
 // 64-byte pieces per instruction.
+//
+// wide kernel (4 < M <= 32, K a multiple of 512 up to 4096): the gemv kernel's weight stream
+// feeding MFMA. One workgroup per 16 weight rows, one wave per 512 elements of K; each wave
+// loads its 16 row pieces whole (1 KB per instruction), stages them in its own LDS region and
+// reads them back as MFMA B operands, with x as the A operands straight from L2. Timed in a
+// graph of 24 calls with distinct weights (N 8672, K 2048 / N 2048, K 4096): 9.7 / 6.4 us at
+// M = 5, 12.7 / 8.2 us at M = 16, 18.2 / 11.7 us at M = 32, against 12.1 / 8.3, 15.8 / 10.5 and
+// 22.3 / 15.4 us for the rows kernel and about 14 us for hipBLASLt. Above 32 rows it loses to
+// the tile kernel (its x reads per workgroup grow with M).
 //
 // tile kernel (M > 32): one 256-thread workgroup (4 waves) owns MT rows x NT columns; x and
 // weight tiles are staged through LDS (double buffered, KS elements of K per stage, rows padded
@@ -365,6 +375,135 @@ __global__ __launch_bounds__(256) void linear_gemv_kernel(const LinGeom g) {
   }
 }
 
+// ----------------------------------------------------------------------------- wide kernel
+
+// 4 < M <= 16 TM, K = 512 WAVES. One workgroup per 16 weight rows; wave w owns K elements
+// [512 w, 512 w + 512). Its 16 rows' pieces are loaded whole, one instruction per row (lane l
+// taking elements 8 l .. 8 l + 7: 1 KB of contiguous row per instruction, the gemv kernel's
+// stream), staged in the wave's own LDS region and read back as the MFMA B operands (row l16,
+// elements 32 s + 8 lg of K step s). The wave alone reads its region, and one wave's LDS
+// operations complete in order, so no barrier separates the two. The A operands come straight
+// from memory (x is small and stays in L2), D steps ahead. The waves' partial sums then meet in
+// their own regions. NORM as in the rows kernel.
+template <typename T, int TM, int WAVES, bool NORM>
+__global__ __launch_bounds__(64 * WAVES) void linear_wide_kernel(const LinGeom g) {
+  using M = LinMma<T>;
+  constexpr int KW = 512, LDW = KW + 8;  // K per wave; LDS row stride (16-byte reads of 16 rows
+                                         // at one column fall in 16 distinct bank groups)
+  // K steps per wave; steps of x in flight (all of them when they fit the registers)
+  constexpr int NS = KW / kStep, D = TM <= 2 ? NS : 4;
+  static_assert(NS % D == 0, "whole rings");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int kb = w * KW;
+  const int vn = min(16, g.n - n0);
+  const __amdgpu_buffer_rsrc_t rw =
+      lin_rsrc(g.w + static_cast<int64_t>(n0) * g.w_ld * 2, lin_extent(vn, g.w_ld, g.k));
+  const __amdgpu_buffer_rsrc_t rx = lin_rsrc(g.x, lin_extent(g.m, g.x_ld, g.k));
+  const __amdgpu_buffer_rsrc_t rn = lin_rsrc(g.nw, NORM ? int64_t{2} * g.k : 0);
+
+  // the wave's weight rows first (non-temporal: streamed once per call)
+  u32x4 wr[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    wr[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          rw, r < vn ? (r * g.w_ld + kb + 8 * lane) * 2 : kOff, 0,
+                                          2));
+  }
+  // x (and the norm weight) of the first D steps
+  int xoff[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) xoff[i] = (min(16 * i + l16, g.m - 1) * g.x_ld + kb + 8 * lg) * 2;
+  const int noff = (kb + 8 * lg) * 2;
+  u32x4 ra[D][TM], rnw[D];
+  auto load = [&](int slot, int s) __attribute__((always_inline)) {
+    const bool live = s < NS;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      ra[slot][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rx, live ? xoff[i] + 2 * kStep * s : kOff, 0, 0));
+    }
+    if constexpr (NORM) {
+      rnw[slot] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rn, live ? noff + 2 * kStep * s : kOff, 0, 0));
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(d, d);
+  __builtin_amdgcn_sched_barrier(0);  // every load above issues before the first wait
+
+  // the weight rows to the wave's LDS region
+  __shared__ __attribute__((aligned(16))) T wl[WAVES][16][LDW];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) *reinterpret_cast<u32x4*>(&wl[w][r][8 * lane]) = wr[r];
+
+  f4 acc[TM];
+  float ssq[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+    ssq[i] = 0.f;
+  }
+#pragma unroll
+  for (int s0 = 0; s0 < NS; s0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int s = s0 + d;
+      const typename M::v8 b =
+          *reinterpret_cast<const typename M::v8*>(&wl[w][l16][kStep * s + 8 * lg]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        typename M::v8 a = __builtin_bit_cast(typename M::v8, ra[d][i]);
+        if constexpr (NORM) {
+          const typename M::v8 nv = __builtin_bit_cast(typename M::v8, rnw[d]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float xf = static_cast<float>(a[e]);
+            ssq[i] = fmaf(xf, xf, ssq[i]);
+            a[e] = static_cast<T>(xf * static_cast<float>(nv[e]));
+          }
+        }
+        acc[i] = M::mma(a, b, acc[i]);
+      }
+      load(d, s + D);
+    }
+  }
+
+  // partial sums: lane holds rows 16 i + 4 lg + r of column n0 + l16; they go to the wave's own
+  // region (its reads of it are complete), and with NORM the sums of squares of rows 16 i + l16
+  float* red = reinterpret_cast<float*>(&wl[w][0][0]);
+  __shared__ float red_ssq[NORM ? WAVES : 1][TM][16];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(i * 4 + r) * 64 + lane] = acc[i][r];
+    if constexpr (NORM) {
+      float v = ssq[i] + __shfl_xor(ssq[i], 16);
+      v += __shfl_xor(v, 32);
+      if (lg == 0) red_ssq[w][i][l16] = v;
+    }
+  }
+  static_assert(TM * 4 * 64 * 4 <= 16 * LDW * 2, "partial sums fit a wave's region");
+  __syncthreads();
+  for (int e = tid; e < TM * 256; e += 64 * WAVES) {
+    const int q = e >> 6, ln = e & 63;
+    float y = 0.f;
+#pragma unroll
+    for (int v = 0; v < WAVES; ++v) y += reinterpret_cast<const float*>(&wl[v][0][0])[q * 64 + ln];
+    const int i = q >> 2, r = q & 3;
+    const int m = 16 * i + 4 * (ln >> 4) + r, n = n0 + (ln & 15);
+    if constexpr (NORM) {
+      float sq = 0.f;
+#pragma unroll
+      for (int v = 0; v < WAVES; ++v) sq += red_ssq[v][i][4 * (ln >> 4) + r];
+      y *= rsqrtf(sq / static_cast<float>(g.k) + g.eps);
+    }
+    if (m < g.m && n < g.n) lin_emit<T>(g, 0, m, n, y);
+  }
+}
+
 // ----------------------------------------------------------------------------- tile kernel
 
 // Workgroup tile MT x NT, WM x WN waves, each wave (MT / WM) x (NT / WN) of 16x16 MFMA tiles;
@@ -513,8 +652,8 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const LinGeom g) {
 // A launch: the kernel and its shape. rows kernel: cfg = TM, TN, WAVES and ring depth d; tile
 // kernel: cfg = MT, NT, KS (wave layout and ring depth follow from them).
 struct LinPlan {
-  bool rows, gemv;
-  int a, b, c, d;     // rows: TM, TN, WAVES, D; tile: MT, NT, KS; gemv: RW, CH
+  bool rows, gemv, wide;
+  int a, b, c, d;     // rows: TM, TN, WAVES, D; tile: MT, NT, KS; gemv: RW, CH; wide: TM, WAVES
   int gx, gy, splits, k_split;
 };
 
@@ -536,6 +675,17 @@ LinPlan plan(int64_t m, int64_t n, int64_t k, bool norm) {
     p.a = cdiv(n, 8) >= 1024 ? 2 : 1;
     p.b = k <= 2048 ? 4 : 8;
     p.gx = static_cast<int>(cdiv(n, 4 * p.a));
+    p.gy = 1;
+    p.splits = 1;
+    p.k_split = static_cast<int>(k);
+    return p;
+  }
+  if (m <= 2 * 16 && k % 512 == 0 && k <= 4096) {
+    // wide kernel: 16 weight rows per workgroup, one wave per 512 elements of K
+    p.wide = true;
+    p.a = static_cast<int>(cdiv(m, 16));
+    p.b = static_cast<int>(k / 512);
+    p.gx = static_cast<int>(cdiv(n, 16));
     p.gy = 1;
     p.splits = 1;
     p.k_split = static_cast<int>(k);
@@ -671,10 +821,51 @@ void launch_gemv(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
   }
 }
 
+template <typename T, int TM, int WAVES>
+void launch_wide(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
+  // (the fused norm takes at most 32 rows: validate)
+  if constexpr (TM <= 2) {
+    if (g.nw != nullptr) {
+      hipLaunchKernelGGL((linear_wide_kernel<T, TM, WAVES, true>), dim3(p.gx), dim3(64 * WAVES), 0,
+                         stream, g);
+      return;
+    }
+  }
+  {
+    hipLaunchKernelGGL((linear_wide_kernel<T, TM, WAVES, false>), dim3(p.gx), dim3(64 * WAVES), 0,
+                       stream, g);
+  }
+}
+
+template <typename T, int TM>
+int launch_wide_k(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
+  switch (p.b) {
+    case 1: launch_wide<T, TM, 1>(g, p, stream); return M3_OK;
+    case 2: launch_wide<T, TM, 2>(g, p, stream); return M3_OK;
+    case 3: launch_wide<T, TM, 3>(g, p, stream); return M3_OK;
+    case 4: launch_wide<T, TM, 4>(g, p, stream); return M3_OK;
+    case 5: launch_wide<T, TM, 5>(g, p, stream); return M3_OK;
+    case 6: launch_wide<T, TM, 6>(g, p, stream); return M3_OK;
+    case 7: launch_wide<T, TM, 7>(g, p, stream); return M3_OK;
+    case 8: launch_wide<T, TM, 8>(g, p, stream); return M3_OK;
+    default: return fail(M3_EUNSUPPORTED, "m3_linear: no wide kernel for %d waves", p.b);
+  }
+}
+
 // The compiled shapes; a plan naming any other is refused.
 template <typename T>
 int launch_plan(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
-  if (p.gemv) {
+  if (p.wide) {
+    int rc = M3_OK;
+    switch (p.a) {
+      case 1: rc = launch_wide_k<T, 1>(g, p, stream); break;
+      case 2: rc = launch_wide_k<T, 2>(g, p, stream); break;
+      case 3: rc = launch_wide_k<T, 3>(g, p, stream); break;
+      case 4: rc = launch_wide_k<T, 4>(g, p, stream); break;
+      default: return fail(M3_EUNSUPPORTED, "m3_linear: no wide kernel for %d row tiles", p.a);
+    }
+    if (rc != M3_OK) return rc;
+  } else if (p.gemv) {
     if (p.a == 2 && p.b == 4) {
       launch_gemv<T, 2, 4>(g, p, stream);
     } else if (p.a == 2 && p.b == 8) {

@@ -155,8 +155,8 @@ def test_linear_validation_and_workspace_on_the_host(lib):
     args.norm_weight.stride[0] = 1
     assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 0
     assert size.value == 0
-    # the decode shapes run unsplit: the gemv kernel up to 4 rows (K a multiple of 512), 542 /
-    # 128 column workgroups, 2 x 136 tiles of 256 rows
+    # the decode shapes run unsplit: the gemv kernel up to 4 rows and the wide kernel up to 32
+    # (K a multiple of 512 up to 4096), 2 x 136 tiles of 256 rows
     for m, n, k in ((1, 8672, 2048), (4, 512, 4096), (16, 2048, 4096), (256, 8672, 2048)):
         args = _linear_args(m, n, k)
         assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 0

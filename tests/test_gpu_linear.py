@@ -37,9 +37,14 @@ SHAPES = [
     (3, 1001, 512),     # gemv: one chunk per lane, N not a multiple of the 4 rows a workgroup owns
     (4, 7, 1536),       # gemv: fewer rows than one workgroup, K / 512 odd
     (4, 8195, 1024),    # gemv: two rows per wave, the last wave half past N
-    (5, 2048, 2048),    # five rows: the rows kernel
-    (7, 2048, 4096),    # out_proj, ragged rows
-    (16, 1000, 2048),   # N not a multiple of the tile
+    (5, 2048, 2048),    # five rows: the wide kernel, one 16-row tile, four waves
+    (7, 2048, 4096),    # out_proj, ragged rows (wide, eight waves)
+    (16, 1000, 2048),   # N not a multiple of the wide kernel's 16 rows
+    (17, 8672, 2048),   # wide, two row tiles, the second one row
+    (32, 2048, 4096),   # wide, two full row tiles, eight waves
+    (9, 37, 512),       # wide, one wave, fewer weight rows than a workgroup
+    (24, 3000, 1536),   # wide, three waves
+    (5, 100, 800),      # K not a multiple of 512: the rows kernel
     (33, 8672, 2048),   # the 64-row tile, ragged
     (64, 2048, 4096),
     (200, 4144, 1024),  # the 128-row tile, ragged rows and columns
@@ -67,7 +72,8 @@ def test_linear_matches_fp32_reference(shape, dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(1, 8672, 2048), (2, 8672, 2048), (3, 1001, 4096),
                                    (4, 13, 512), (5, 2048, 4096), (16, 1000, 2048),
-                                   (32, 4144, 1024)])
+                                   (32, 4144, 1024), (17, 8672, 2048), (30, 77, 4096),
+                                   (12, 500, 1536)])
 def test_linear_fused_rms_norm_matches_fp32_reference(shape, dtype):
     """norm_weight: x is RMS-normalised first. The kernel rounds x * norm_weight (not the
     normalised value) to the operand dtype, one rounding per element either way, so the bound
@@ -118,6 +124,33 @@ def test_linear_gemv_strided_rows_and_in_place_residual():
         out = ops.linear(x, w, res, out=res)
     assert out.data_ptr() == res.data_ptr()
     _check(out, x, w, keep)
+
+
+def test_linear_wide_strided_rows_and_in_place_residual():
+    """The wide kernel (4 < M <= 32) with strided x / weight rows and out aliasing the
+    residual, with and without the fused RMSNorm."""
+    g = torch.Generator(device="cpu").manual_seed(7)
+    big_x = torch.randn(41, 4096 + 64, generator=g).to(torch.bfloat16).to(DEV)
+    big_w = (torch.randn(700, 4096 + 32, generator=g) / 64).to(torch.bfloat16).to(DEV)
+    x, w = big_x[1:41:2, :4096], big_w[:, 32:]  # 20 rows of stride 8320, weight stride 4128
+    assert x.stride(0) == 8320 and w.stride(0) == 4128
+    res = torch.randn(20, 700, generator=g).to(torch.bfloat16).to(DEV)
+    keep = res.clone()
+    with torch.inference_mode():
+        out = ops.linear(x, w, res, out=res)
+    assert out.data_ptr() == res.data_ptr()
+    _check(out, x, w, keep)
+    nw = (1 + 0.1 * torch.randn(4096, generator=g)).to(torch.bfloat16).to(DEV)
+    with torch.inference_mode():
+        got = ops.linear(x, w, norm_weight=nw, norm_eps=1e-5)
+    # the bound of test_linear_fused_rms_norm_matches_fp32_reference
+    xf, wf = x.float().cpu(), w.float().cpu()
+    xn = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5) * nw.float().cpu()
+    want = xn @ wf.T
+    bound = ULP[torch.bfloat16] * (want.abs() + xn.abs() @ wf.abs().T) + 2.0 ** -16 * (
+        xn.abs() @ wf.abs().T) + 1e-30
+    worst = ((got.float().cpu() - want).abs() / bound).max().item()
+    assert worst <= 1.0, f"max error / bound = {worst:.3f}"
 
 
 def test_linear_repeated_calls_are_deterministic():
