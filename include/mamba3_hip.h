@@ -194,7 +194,8 @@ int m3_step(const m3_step_args* args, hipStream_t stream);
  * A linear layer of the decode path, out[M, N] = x'[M, K] * weight[N, K]^T (+ residual[M, N]),
  * for few rows (M <= 256, one row per batch element): 16-bit x, weight, residual and out of one
  * dtype, FP32 accumulation, one rounding. x' is x, or with norm_weight the RMS-normalised
- * x * rsqrt(mean_k x^2 + norm_eps) * norm_weight (M <= 32 only). It has no counterpart among the
+ * x * rsqrt(mean_k x^2 + norm_eps) * norm_weight (M <= 32, or M <= 64 with K a multiple of
+ * 256). It has no counterpart among the
  * reference's plugin hooks: it replaces the block's RMSNorm, the in_proj / out_proj nn.Linear
  * calls and the residual add of a decode step (mamba3/model.py:441-458, 514-520), where a
  * general GEMM leaves most of the GPU idle.

@@ -1,42 +1,48 @@
 // m3_linear: out[M, N] = x[M, K] * weight[N, K]^T (+ residual) for the few rows of a decode step.
 //
 // A general GEMM tiles M = 1..256 rows poorly: its large tiles leave most of the 256 CUs idle
-// and each streams the weight at a fraction of HBM bandwidth. Two kernels, both on the bf16 /
-// f16 MFMA 16x16x32 (FP32 accumulation), both keeping several K steps of loads in flight per
-// wave in a register ring:
+// and each streams the weight at a fraction of HBM bandwidth. Five kernels, the MFMA ones on the
+// bf16 / f16 16x16x32 (FP32 accumulation); the first that applies runs:
 //
-// rows kernel (M <= 32 where the gemv and wide kernels do not apply): a weight stream. The B
-// operand of a 16x16x32 MFMA is, per lane, 16 contiguous bytes of one weight row (lane
-// l16 + 16 lg holds row l16, elements 8 lg .. 8 lg + 7
-// of the 32-element step), and the A operand the same of an x row, so both are loaded straight
-// into registers: no LDS staging, no barrier in the K loop. A workgroup owns 16 * TN columns;
-// its waves split the K range and add their sums through LDS at the end.
-//
-// gemv kernel (M <= 4, K a multiple of 512 up to 4096): the same weight stream without MFMA.
-// Each wave owns RW weight rows whose K range it reads whole, lane l taking the 16-byte chunks
+// gemv kernel (M <= 4, K a multiple of 512 up to 4096): a weight stream without MFMA. Each wave
+// owns RW weight rows whose K range it reads whole, lane l taking the 16-byte chunks
 // 8 (l + 64 c): one load instruction covers 1 KB of one row, and all of a lane's chunks are in
 // flight at once (K / 512 per row). x goes to LDS once per workgroup (normed as in the rows
 // kernel); each wave reduces its rows over its 64 lanes, so no sums cross waves. Measured on the
 // decode shapes (N 8672, K 2048: 35.5 MB), this layout streams about 1.6x faster than 16 rows of
 // 64-byte pieces per instruction.
 //
-// wide kernel (4 < M <= 32, K a multiple of 512 up to 4096): the gemv kernel's weight stream
-// feeding MFMA. One workgroup per 16 weight rows, one wave per 512 elements of K; each wave
-// loads its 16 row pieces whole (1 KB per instruction), stages them in its own LDS region and
-// reads them back as MFMA B operands, with x as the A operands straight from L2. Timed in a
-// graph of 24 calls with distinct weights (N 8672, K 2048 / N 2048, K 4096): 9.7 / 6.4 us at
-// M = 5, 12.7 / 8.2 us at M = 16, 18.2 / 11.7 us at M = 32, against 12.1 / 8.3, 15.8 / 10.5 and
-// 22.3 / 15.4 us for the rows kernel and about 14 us for hipBLASLt. Above 32 rows it loses to
-// the tile kernel (its x reads per workgroup grow with M).
+// wide kernel (M <= 16, K a multiple of 512 up to 4096, N <= 16 x 256): the gemv kernel's
+// weight stream feeding MFMA. One workgroup per 16 weight rows, one wave per 512 elements of K;
+// each wave loads its 16 row pieces whole (1 KB per instruction), stages them in its own LDS
+// region and reads them back as MFMA B operands, with x as the A operands straight from L2.
+// Every workgroup reads all of x, so it takes the shapes whose workgroups fit one pass over the
+// CUs: the out_proj shape (N 2048, K 4096) in 6.4 us at M = 5 and 8.2 us at M = 16.
 //
-// tile kernel (M > 32): one 256-thread workgroup (4 waves) owns MT rows x NT columns; x and
-// weight tiles are staged through LDS (double buffered, KS elements of K per stage, rows padded
-// by 8 elements so the 16 rows one MFMA operand reads fall in distinct 16-byte bank groups).
+// stream kernel (M <= 64, K a multiple of 256): all the x rows and 16-48 weight rows per
+// workgroup, x and weight tiles loaded straight into an LDS ring (no registers held in flight),
+// the K steps of a stage split over the waves. Fewer workgroups than the wide kernel read x.
+// Timed in a graph of 24 calls with distinct weights: in_proj (N 8672, K 2048) 9.4-10.5 us at
+// M = 5-32 and 13.5 us at M = 64, 9.6-11.0 / 14.7 us with the RMSNorm fused, against about
+// 14-15.4 us for hipBLASLt and 5 us more for a separate norm; out_proj 8.4-9.0 us at M = 17-32
+// and 12.1 us at M = 64.
 //
-// When the output tiles alone do not fill the GPU, the K axis is also split over workgroups:
-// FP32 partial sums go to the workspace and a reduce kernel adds them (and the residual) and
-// rounds once. Loads go through buffer resources whose extents end at the last byte of the
-// last valid row, so nothing outside the operands is ever read.
+// rows kernel (M <= 32 where the kernels above do not apply): a weight stream. The B operand of
+// a 16x16x32 MFMA is, per lane, 16 contiguous bytes of one weight row (lane l16 + 16 lg holds
+// row l16, elements 8 lg .. 8 lg + 7 of the 32-element step), and the A operand the same of an
+// x row, so both are loaded straight into registers: no LDS staging, no barrier in the K loop.
+// A workgroup owns 16 * TN columns; its waves split the K range and add their sums through LDS
+// at the end.
+//
+// tile kernel (M > 64, or M > 32 with K not a multiple of 256): one 256-thread workgroup
+// (4 waves) owns MT rows x NT columns; x and weight tiles are staged through LDS (double
+// buffered, KS elements of K per stage, rows padded by 8 elements so the 16 rows one MFMA
+// operand reads fall in distinct 16-byte bank groups).
+//
+// When the output tiles alone do not fill the GPU, the rows and tile kernels also split the K
+// axis over workgroups: FP32 partial sums go to the workspace and a reduce kernel adds them (and
+// the residual) and rounds once. Loads go through buffer resources whose extents end at the last
+// byte of the last valid row, so nothing outside the operands is ever read.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -377,7 +383,7 @@ __global__ __launch_bounds__(256) void linear_gemv_kernel(const LinGeom g) {
 
 // ----------------------------------------------------------------------------- wide kernel
 
-// 4 < M <= 16 TM, K = 512 WAVES. One workgroup per 16 weight rows; wave w owns K elements
+// 4 < M <= 16 TM (the plan takes TM = 1), K = 512 WAVES. One workgroup per 16 weight rows; wave w owns K elements
 // [512 w, 512 w + 512). Its 16 rows' pieces are loaded whole, one instruction per row (lane l
 // taking elements 8 l .. 8 l + 7: 1 KB of contiguous row per instruction, the gemv kernel's
 // stream), staged in the wave's own LDS region and read back as the MFMA B operands (row l16,
@@ -633,6 +639,241 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const LinGeom g) {
   }
 }
 
+// ----------------------------------------------------------------------------- stream kernel
+
+// Waits until at most N of this wave's vector-memory operations are outstanding. The stream
+// kernel's loads write LDS directly and return nothing to registers; the kernel waits for them
+// itself, counting its own loads.
+template <int N>
+__device__ __forceinline__ void lin_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void lin_wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// An LDS read the compiler does not track, and the wait that makes its value usable (the "+v"
+// operand keeps every use of v after the wait). The compiler would otherwise wait for all of the
+// wave's loads into LDS still in flight before any LDS read, which undoes the ring.
+__device__ __forceinline__ u32x4 lin_ds_read(const char* p) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1"
+               : "=v"(v)
+               : "v"(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+                     (__attribute__((address_space(3))) const char*)p))));
+  return v;
+}
+__device__ __forceinline__ void lin_ds_wait(u32x4& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); }
+
+// A buffer load of 16 bytes per lane written straight to LDS: lane l's bytes land at
+// dst + 16 l (dst wave-uniform). The builtin exists only in the device pass of the compiler
+// (the host pass, which emits the launch stubs, would drop the kernel).
+template <int AUX>
+__device__ __forceinline__ void lin_load_lds(__amdgpu_buffer_rsrc_t r, char* dst, int voff,
+                                             int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
+                                           voff, soff, 0, AUX);
+#endif
+}
+
+// 4 < M <= 64: every x row (MT = 32 or 64) and NT weight rows per 512-thread workgroup over
+// the whole K range (one rounding, no reduce launch). Stages of KB elements of K hold the MT x
+// rows and NT weight rows in LDS, S stages in a ring, loaded straight into LDS (buffer loads
+// with the LDS destination): a load unit is one instruction, 64 lanes x 16 bytes = RPU whole
+// row pieces, contiguous in memory and in LDS, and the ring keeps S - 1 stages in flight with no
+// registers held. Within a row piece the 16-byte chunk c sits at position c ^ (row & 15), so the
+// 16 rows one MFMA operand reads at one chunk fall in 16 distinct bank groups. Each wave takes
+// every WK-th K step of a stage for TMW of the M tiles and all NT columns; the waves' partial
+// sums meet in LDS at the end. NORM (x RMS-normalised, as in the rows kernel): one more unit per
+// stage brings that stage's norm weights, the A operands are multiplied by them and the squares
+// of x are summed on the way.
+template <typename T, int MT, int NT, int KB, int S, bool NORM>
+__global__ __launch_bounds__(512) void linear_stream_kernel(const LinGeom g) {
+  using M = LinMma<T>;
+  constexpr int WAVES = 8;
+  constexpr int CPR = KB / 8;                          // 16-byte chunks per row piece
+  constexpr int RPU = 64 / CPR;                        // row pieces per load unit
+  constexpr int XU = MT / RPU, U = (MT + NT) / RPU;    // x units, x and weight units
+  constexpr int UN = U + (NORM ? 1 : 0);               // + the norm-weight unit
+  constexpr int UPW = (UN + WAVES - 1) / WAVES;        // units per wave (past UN: dummies)
+  constexpr int XJ = XU / WAVES;                       // a wave's first XJ units are x
+  constexpr int SB = UN * 1024;                        // stage bytes
+  constexpr int KS = KB / kStep;                       // K steps per stage
+  constexpr int WK = KS < WAVES ? KS : WAVES;          // waves splitting a stage's K steps
+  constexpr int WT = WAVES / WK;                       // wave groups splitting the M tiles
+  constexpr int QS = KS / WK;                          // K steps per wave per stage
+  constexpr int TMW = MT / 16 / WT, TN = NT / 16;      // a wave's tiles
+  constexpr int RB = CPR * 16;                         // LDS bytes per row piece
+  static_assert(CPR >= 16 && CPR <= 64 && XU % WAVES == 0, "stage shape");
+  static_assert(KS % WK == 0 && (MT / 16) % WT == 0 && TMW >= 1 && TN >= 1, "wave tiling");
+  static_assert(S >= 3 && UPW * (S - 2) < 64, "ring depth");
+  static_assert(KB <= 512, "a stage's norm weights fit one unit");
+  static_assert(WAVES * TMW * TN * 1024 <= S * SB, "partial sums fit the ring");
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int kw = w % WK, tw = w / WK;
+  const int n0 = blockIdx.x * NT, m0 = blockIdx.y * MT;
+  const int ns = g.k / KB;  // stages (the plan keeps K a multiple of KB)
+
+  __shared__ __attribute__((aligned(1024))) char ring[S][SB];
+  __shared__ __attribute__((aligned(1024))) char spare[UPW * WAVES > UN ? 1024 : 16];
+  __shared__ float red_ssq[NORM ? WAVES : 1][TMW][16];
+
+  const __amdgpu_buffer_rsrc_t rx = lin_rsrc(g.x, lin_extent(g.m, g.x_ld, g.k));
+  const __amdgpu_buffer_rsrc_t rw = lin_rsrc(g.w, lin_extent(g.n, g.w_ld, g.k));
+  const __amdgpu_buffer_rsrc_t rn = lin_rsrc(g.nw, NORM ? int64_t{2} * g.k : 0);
+
+  // unit j of this wave is unit j * WAVES + w of the stage; lane offsets at stage 0. Rows past
+  // M / N repeat the last valid row (their sums are never written). With NORM, unit U holds the
+  // stage's KB norm weights (lane l loads chunk l % CPR). Dummy units (which keep every wave's
+  // count of loads per stage equal) and stages past the last read nothing (offsets past every
+  // extent); dummies land in one spare KB. So every wave issues UPW loads per stage, and
+  // nothing else in the loop touches memory.
+  int uoff[UPW];
+#pragma unroll
+  for (int j = 0; j < UPW; ++j) {
+    const int u = j * WAVES + w;
+    const int r = u * RPU + lane / CPR, c = (lane % CPR) ^ (r & 15);
+    if (j < XJ) {
+      uoff[j] = (min(m0 + r, g.m - 1) * g.x_ld + 8 * c) * 2;
+    } else if (u < U) {
+      uoff[j] = (min(n0 + r - MT, g.n - 1) * g.w_ld + 8 * c) * 2;
+    } else if (NORM && u == U) {
+      uoff[j] = 16 * (lane % CPR);
+    } else {
+      uoff[j] = kOff;
+    }
+  }
+  auto issue = [&](int s, int slot) __attribute__((always_inline)) {
+    const bool live = s < ns;
+#pragma unroll
+    for (int j = 0; j < UPW; ++j) {
+      const int u = j * WAVES + w;
+      char* dst = u < UN ? &ring[slot][1024 * u] : spare;
+      if (j < XJ) {
+        lin_load_lds<0>(rx, dst, live ? uoff[j] : kOff, 2 * KB * s);
+      } else if (u < U) {
+        lin_load_lds<2>(rw, dst, live ? uoff[j] : kOff, 2 * KB * s);
+      } else if (NORM && u == U) {
+        lin_load_lds<0>(rn, dst, live ? uoff[j] : kOff, 2 * KB * s);
+      } else {
+        lin_load_lds<0>(rx, dst, kOff, 0);
+      }
+    }
+  };
+
+  // lane's LDS offsets within a row piece for its K steps of a stage (chunk 4 ks + lg of row
+  // 16 t + l16 sits at position (4 ks + lg) ^ l16)
+  int roff[QS];
+#pragma unroll
+  for (int q = 0; q < QS; ++q) roff[q] = l16 * RB + 16 * ((4 * (kw + WK * q) + lg) ^ l16);
+
+  f4 acc[TMW][TN];
+  float ssq[TMW];
+#pragma unroll
+  for (int i = 0; i < TMW; ++i) {
+    ssq[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+  auto compute = [&](int slot) __attribute__((always_inline)) {
+    const char* base = ring[slot];
+#pragma unroll
+    for (int q = 0; q < QS; ++q) {
+      u32x4 ra[TMW], rb[TN], rn;
+#pragma unroll
+      for (int i = 0; i < TMW; ++i) ra[i] = lin_ds_read(base + (16 * (TMW * tw + i)) * RB + roff[q]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) rb[j] = lin_ds_read(base + (MT + 16 * j) * RB + roff[q]);
+      if constexpr (NORM) rn = lin_ds_read(base + 1024 * U + 16 * (4 * (kw + WK * q) + lg));
+#pragma unroll
+      for (int i = 0; i < TMW; ++i) lin_ds_wait(ra[i]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) lin_ds_wait(rb[j]);
+      typename M::v8 av[TMW], bv[TN];
+#pragma unroll
+      for (int i = 0; i < TMW; ++i) av[i] = __builtin_bit_cast(typename M::v8, ra[i]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bv[j] = __builtin_bit_cast(typename M::v8, rb[j]);
+      if constexpr (NORM) {
+        lin_ds_wait(rn);
+        const typename M::v8 nv = __builtin_bit_cast(typename M::v8, rn);
+#pragma unroll
+        for (int i = 0; i < TMW; ++i) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float xf = static_cast<float>(av[i][e]);
+            ssq[i] = fmaf(xf, xf, ssq[i]);
+            av[i][e] = static_cast<T>(xf * static_cast<float>(nv[e]));
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TMW; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = M::mma(av[i], bv[j], acc[i][j]);
+      }
+    }
+  };
+
+  // Stage t sits in slot t % S (the loop is unrolled S times, so slots are constants). It waits
+  // for its own loads (the S - 2 stages after it may still be in flight); the barrier then shows
+  // every wave's loads, and every wave is done with the slot of stage t - 1, which takes stage
+  // t + S - 1.
+#pragma unroll
+  for (int p = 0; p < S - 1; ++p) issue(p, p);
+  for (int t0 = 0; t0 < ns; t0 += S) {
+#pragma unroll
+    for (int d = 0; d < S; ++d) {
+      if (t0 + d < ns) {
+        lin_wait_vm<UPW * (S - 2)>();
+        lin_wait_lds();
+        __builtin_amdgcn_s_barrier();
+        issue(t0 + d + S - 1, (d + S - 1) % S);
+        compute(d);
+      }
+    }
+  }
+  lin_wait_vm<0>();
+  lin_wait_lds();
+  __syncthreads();
+
+  // partial sums: lane holds rows 16 i + 4 lg + r of column 16 j + l16 of the wave's tiles
+  float* red = reinterpret_cast<float*>(&ring[0][0]);
+#pragma unroll
+  for (int i = 0; i < TMW; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[((w * TMW + i) * TN + j) * 256 + r * 64 + lane] = acc[i][j][r];
+    }
+    if constexpr (NORM) {
+      float v = ssq[i] + __shfl_xor(ssq[i], 16);
+      v += __shfl_xor(v, 32);
+      if (lg == 0) red_ssq[w][i][l16] = v;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < MT * NT; e += 512) {
+    const int m = e / NT, n = e - m * NT;
+    const int ig = m >> 4, j = n >> 4, tg = ig / TMW, i = ig - tg * TMW;
+    const int ln = (n & 15) + 16 * ((m & 15) >> 2), r = m & 3;
+    float y = 0.f;
+#pragma unroll
+    for (int v = 0; v < WK; ++v) y += red[(((v + WK * tg) * TMW + i) * TN + j) * 256 + r * 64 + ln];
+    if constexpr (NORM) {
+      float sq = 0.f;
+#pragma unroll
+      for (int v = 0; v < WK; ++v) sq += red_ssq[v + WK * tg][i][m & 15];
+      y *= rsqrtf(sq / static_cast<float>(g.k) + g.eps);
+    }
+    if (m0 + m < g.m && n0 + n < g.n) lin_emit<T>(g, 0, m0 + m, n0 + n, y);
+  }
+}
+
 // out = sum over splits of the partial sums (+ residual), rounded once; one thread per element
 template <typename T>
 __global__ __launch_bounds__(256) void linear_reduce_kernel(const LinGeom g) {
@@ -652,12 +893,15 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const LinGeom g) {
 // A launch: the kernel and its shape. rows kernel: cfg = TM, TN, WAVES and ring depth d; tile
 // kernel: cfg = MT, NT, KS (wave layout and ring depth follow from them).
 struct LinPlan {
-  bool rows, gemv, wide;
-  int a, b, c, d;     // rows: TM, TN, WAVES, D; tile: MT, NT, KS; gemv: RW, CH; wide: TM, WAVES
+  bool rows, gemv, wide, stream;
+  int a, b, c, d;     // rows: TM, TN, WAVES, D; tile: MT, NT, KS; gemv: RW, CH; wide: TM, WAVES;
+                      // stream: MT, NT, KB, S
   int gx, gy, splits, k_split;
 };
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+constexpr int64_t kCUs = 256;  // compute units of the MI355X
 
 // Splits of K (each a multiple of `unit` elements) so that about `want` workgroups run.
 void split_k(LinPlan& p, int64_t k, int64_t tiles, int64_t want, int64_t unit) {
@@ -680,12 +924,26 @@ LinPlan plan(int64_t m, int64_t n, int64_t k, bool norm) {
     p.k_split = static_cast<int>(k);
     return p;
   }
-  if (m <= 2 * 16 && k % 512 == 0 && k <= 4096) {
-    // wide kernel: 16 weight rows per workgroup, one wave per 512 elements of K
+  if (m <= 16 && k % 512 == 0 && k <= 4096 && cdiv(n, 16) <= kCUs) {
+    // wide kernel: 16 weight rows per workgroup, one wave per 512 elements of K; x is read once
+    // per workgroup, so it takes the shapes whose workgroups fit one pass over the CUs
     p.wide = true;
-    p.a = static_cast<int>(cdiv(m, 16));
+    p.a = 1;
     p.b = static_cast<int>(k / 512);
     p.gx = static_cast<int>(cdiv(n, 16));
+    p.gy = 1;
+    p.splits = 1;
+    p.k_split = static_cast<int>(k);
+    return p;
+  }
+  if (m <= 64 && k % 256 == 0) {
+    // stream kernel: all the rows in one tile of 32 or 64, and the fewest weight rows per
+    // workgroup (16, 32 or 48) that keep the workgroups within one pass over the CUs (each
+    // workgroup reads all of x, so fewer of them read less of it)
+    p.stream = true;
+    p.a = m <= 32 ? 32 : 64;
+    p.b = cdiv(n, 16) <= kCUs ? 16 : cdiv(n, 32) <= kCUs ? 32 : 48;
+    p.gx = static_cast<int>(cdiv(n, p.b));
     p.gy = 1;
     p.splits = 1;
     p.k_split = static_cast<int>(k);
@@ -731,7 +989,10 @@ int validate(const m3_linear_args& a) {
     return rc;
   }
   if (a.norm_weight.ptr != nullptr) {
-    if (a.m > 32) return fail(M3_EUNSUPPORTED, "m3_linear: norm_weight needs M <= 32");
+    if (a.m > 64 || (a.m > 32 && a.k % 256 != 0)) {
+      return fail(M3_EUNSUPPORTED,
+                  "m3_linear: norm_weight needs M <= 32, or M <= 64 with K a multiple of 256");
+    }
     if (reinterpret_cast<uintptr_t>(a.norm_weight.ptr) % 16 != 0) {
       return fail(M3_EUNSUPPORTED, "m3_linear: norm_weight must be 16-byte aligned");
     }
@@ -823,15 +1084,10 @@ void launch_gemv(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
 
 template <typename T, int TM, int WAVES>
 void launch_wide(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
-  // (the fused norm takes at most 32 rows: validate)
-  if constexpr (TM <= 2) {
-    if (g.nw != nullptr) {
-      hipLaunchKernelGGL((linear_wide_kernel<T, TM, WAVES, true>), dim3(p.gx), dim3(64 * WAVES), 0,
-                         stream, g);
-      return;
-    }
-  }
-  {
+  if (g.nw != nullptr) {
+    hipLaunchKernelGGL((linear_wide_kernel<T, TM, WAVES, true>), dim3(p.gx), dim3(64 * WAVES), 0,
+                       stream, g);
+  } else {
     hipLaunchKernelGGL((linear_wide_kernel<T, TM, WAVES, false>), dim3(p.gx), dim3(64 * WAVES), 0,
                        stream, g);
   }
@@ -852,18 +1108,39 @@ int launch_wide_k(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
   }
 }
 
+template <typename T, int MT, int NT, int KB, int S>
+void launch_stream(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
+  if (g.nw != nullptr) {
+    hipLaunchKernelGGL((linear_stream_kernel<T, MT, NT, KB, S, true>), dim3(p.gx, p.gy),
+                       dim3(512), 0, stream, g);
+  } else {
+    hipLaunchKernelGGL((linear_stream_kernel<T, MT, NT, KB, S, false>), dim3(p.gx, p.gy),
+                       dim3(512), 0, stream, g);
+  }
+}
+
 // The compiled shapes; a plan naming any other is refused.
 template <typename T>
 int launch_plan(const LinGeom& g, const LinPlan& p, hipStream_t stream) {
-  if (p.wide) {
-    int rc = M3_OK;
-    switch (p.a) {
-      case 1: rc = launch_wide_k<T, 1>(g, p, stream); break;
-      case 2: rc = launch_wide_k<T, 2>(g, p, stream); break;
-      case 3: rc = launch_wide_k<T, 3>(g, p, stream); break;
-      case 4: rc = launch_wide_k<T, 4>(g, p, stream); break;
-      default: return fail(M3_EUNSUPPORTED, "m3_linear: no wide kernel for %d row tiles", p.a);
+  if (p.stream) {
+    if (p.a == 32 && p.b == 48) {
+      launch_stream<T, 32, 48, 128, 4>(g, p, stream);
+    } else if (p.a == 32 && p.b == 32) {
+      launch_stream<T, 32, 32, 128, 4>(g, p, stream);
+    } else if (p.a == 32 && p.b == 16) {
+      launch_stream<T, 32, 16, 256, 3>(g, p, stream);
+    } else if (p.a == 64 && p.b == 48) {
+      launch_stream<T, 64, 48, 128, 4>(g, p, stream);
+    } else if (p.a == 64 && p.b == 32) {
+      launch_stream<T, 64, 32, 128, 4>(g, p, stream);
+    } else if (p.a == 64 && p.b == 16) {
+      launch_stream<T, 64, 16, 256, 3>(g, p, stream);
+    } else {
+      return fail(M3_EUNSUPPORTED, "m3_linear: no stream kernel %d/%d", p.a, p.b);
     }
+  } else if (p.wide) {
+    if (p.a != 1) return fail(M3_EUNSUPPORTED, "m3_linear: no wide kernel for %d row tiles", p.a);
+    const int rc = launch_wide_k<T, 1>(g, p, stream);
     if (rc != M3_OK) return rc;
   } else if (p.gemv) {
     if (p.a == 2 && p.b == 4) {

@@ -216,7 +216,8 @@ class _Mamba3Mixer(nn.Module):
         self._check_inference(hidden_states)
         rows = hidden_states[:, 0]
         small = rows.shape[0] <= ops.DECODE_LINEAR_ROWS
-        if small and ops.linear_supported(rows, self.in_proj.weight):
+        supported = ops.linear_norm_supported if norm is not None else ops.linear_supported
+        if small and supported(rows, self.in_proj.weight):
             proj = ops.linear(rows, self.in_proj.weight,
                               norm_weight=norm.weight if norm is not None else None,
                               norm_eps=norm.eps if norm is not None else ops.NORM_EPS)

@@ -486,12 +486,13 @@ def step_projection(proj: torch.Tensor, mixer, cache, *, inplace: bool = False):
 # --------------------------------------------------------------------------- decode GEMMs
 
 LINEAR_MAX_ROWS = 256
-LINEAR_NORM_MAX_ROWS = 32
+# The fused RMSNorm takes up to 32 rows, or up to 64 when K is a multiple of 256.
+LINEAR_NORM_MAX_ROWS = 64
 # Decode steps run in_proj (with the block's RMSNorm fused) on ``linear`` up to
 # DECODE_LINEAR_ROWS rows, and out_proj (with the residual add fused) up to
 # DECODE_LINEAR_OUT_ROWS. Measured on the decode shapes with cold weights: above these, hipBLASLt
-# (plus the separate norm or add) is as fast.
-DECODE_LINEAR_ROWS = 16
+# (plus the separate norm or add) is faster.
+DECODE_LINEAR_ROWS = 64
 DECODE_LINEAR_OUT_ROWS = 64
 
 
@@ -518,6 +519,15 @@ def linear_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
     return True
 
 
+def linear_norm_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether ``linear(x, weight, norm_weight=...)`` takes these operands: ``linear_supported``
+    and at most 32 rows, or at most ``LINEAR_NORM_MAX_ROWS`` with K a multiple of 256."""
+    if not linear_supported(x, weight):
+        return False
+    m, k = x.shape
+    return m <= 32 or (m <= LINEAR_NORM_MAX_ROWS and k % 256 == 0)
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor | None = None, *,
            out: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None,
            norm_eps: float = NORM_EPS) -> torch.Tensor:
@@ -526,8 +536,9 @@ def linear(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor | None 
     ``x`` is ``[M, K]`` (``M <= 256``), ``weight`` the ``[N, K]`` weight of an ``nn.Linear``
     without bias, both bfloat16 or both float16 (``linear_supported``); ``residual`` and
     ``out`` are ``[M, N]`` of that dtype. Products accumulate in FP32; the residual is added
-    to the FP32 sum, which is rounded once. With ``norm_weight`` (``[K]``, ``M <= 32``) ``x``
-    is first RMS-normalised, as ``F.rms_norm(x, (K,), norm_weight, norm_eps)``. This replaces
+    to the FP32 sum, which is rounded once. With ``norm_weight`` (``[K]``; ``M <= 32``, or
+    ``M <= 64`` with K a multiple of 256) ``x`` is first RMS-normalised, as
+    ``F.rms_norm(x, (K,), norm_weight, norm_eps)``. This replaces
     the decode step's RMSNorm, ``in_proj`` / ``out_proj`` calls and the block's residual add
     (reference ``model.py:441-458, 514-520``).
     """
@@ -543,8 +554,9 @@ def linear(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor | None 
             raise ValueError(f"linear: {name} must be [{m}, {n}] {x.dtype}, got "
                              f"{tuple(t.shape)} {t.dtype}")
     if norm_weight is not None:
-        if x.shape[0] > LINEAR_NORM_MAX_ROWS:
-            raise ValueError(f"linear: norm_weight needs at most {LINEAR_NORM_MAX_ROWS} rows")
+        if not linear_norm_supported(x, weight):
+            raise ValueError(f"linear: norm_weight needs at most 32 rows, or at most "
+                             f"{LINEAR_NORM_MAX_ROWS} with K a multiple of 256")
         norm_weight = norm_weight.detach().to(x.dtype).contiguous()
         if norm_weight.shape != (x.shape[1],):
             raise ValueError(f"linear: norm_weight must be [{x.shape[1]}]")

@@ -165,11 +165,14 @@ def test_linear_validation_and_workspace_on_the_host(lib):
     args = _linear_args(1, 512, 4064)
     assert lib.m3_linear(ctypes.byref(args), None) == 4
     assert b"workspace" in lib.m3_last_error()
-    args = _linear_args(33, 64, 2048)
-    args.norm_weight.ptr, args.norm_weight.dtype = 0x40000, _hip.BF16
-    args.norm_weight.stride[0] = 1
-    assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == 2
-    assert b"M <= 32" in lib.m3_last_error()
+    # the fused norm: up to 64 rows with K a multiple of 256, else up to 32
+    for m, k, code in ((64, 2048, 0), (65, 2048, 2), (33, 2080, 2), (32, 2080, 0)):
+        args = _linear_args(m, 64, k)
+        args.norm_weight.ptr, args.norm_weight.dtype = 0x40000, _hip.BF16
+        args.norm_weight.stride[0] = 1
+        assert lib.m3_linear_workspace_size(ctypes.byref(args), ctypes.byref(size)) == code, (m, k)
+        if code:
+            assert b"M <= 32" in lib.m3_last_error()
     for field, value, code, text in (("m", 257, 2, b"M = 257"), ("k", 2040, 2, b"K % 32"),
                                      ("dtype", _hip.F32, 2, b"dtype")):
         args = _linear_args(4, 64, 2048)

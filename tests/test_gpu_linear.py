@@ -40,13 +40,18 @@ SHAPES = [
     (5, 2048, 2048),    # five rows: the wide kernel, one 16-row tile, four waves
     (7, 2048, 4096),    # out_proj, ragged rows (wide, eight waves)
     (16, 1000, 2048),   # N not a multiple of the wide kernel's 16 rows
-    (17, 8672, 2048),   # wide, two row tiles, the second one row
-    (32, 2048, 4096),   # wide, two full row tiles, eight waves
     (9, 37, 512),       # wide, one wave, fewer weight rows than a workgroup
-    (24, 3000, 1536),   # wide, three waves
-    (5, 100, 800),      # K not a multiple of 512: the rows kernel
-    (33, 8672, 2048),   # the 64-row tile, ragged
-    (64, 2048, 4096),
+    (5, 8672, 2048),    # decode B = 5 in_proj: the stream kernel, 32-row tile, 48 weight rows
+    (17, 8672, 2048),   # stream, 32-row tile, 17 rows
+    (32, 2048, 4096),   # decode B = 32 out_proj: stream, 32-row tile, 16 weight rows
+    (24, 3000, 1536),   # stream, 16 weight rows, N ragged
+    (20, 4100, 1280),   # stream, 32 weight rows (N / 16 just past the 256 CUs)
+    (33, 8672, 2048),   # stream, 64-row tile, ragged rows
+    (64, 8672, 2048),   # decode B = 64 in_proj (64-row tile, 48 weight rows)
+    (64, 2048, 4096),   # decode B = 64 out_proj (64-row tile, 16 weight rows)
+    (40, 5000, 768),    # stream, 64-row tile, 32 weight rows, ragged N
+    (48, 12289, 256),   # stream, one stage of K, more workgroups than CUs, one row past N / 16
+    (5, 100, 800),      # K not a multiple of 256: the rows kernel
     (200, 4144, 1024),  # the 128-row tile, ragged rows and columns
     (256, 8672, 2048),  # decode B = 256 in_proj (config 4)
     (256, 2048, 4096),  # decode B = 256 out_proj (K split)
@@ -73,7 +78,8 @@ def test_linear_matches_fp32_reference(shape, dtype):
 @pytest.mark.parametrize("shape", [(1, 8672, 2048), (2, 8672, 2048), (3, 1001, 4096),
                                    (4, 13, 512), (5, 2048, 4096), (16, 1000, 2048),
                                    (32, 4144, 1024), (17, 8672, 2048), (30, 77, 4096),
-                                   (12, 500, 1536)])
+                                   (12, 500, 1536), (5, 8672, 2048), (64, 8672, 2048),
+                                   (48, 300, 4096), (40, 5000, 768), (20, 100, 800)])
 def test_linear_fused_rms_norm_matches_fp32_reference(shape, dtype):
     """norm_weight: x is RMS-normalised first. The kernel rounds x * norm_weight (not the
     normalised value) to the operand dtype, one rounding per element either way, so the bound
@@ -126,15 +132,16 @@ def test_linear_gemv_strided_rows_and_in_place_residual():
     _check(out, x, w, keep)
 
 
-def test_linear_wide_strided_rows_and_in_place_residual():
-    """The wide kernel (4 < M <= 32) with strided x / weight rows and out aliasing the
-    residual, with and without the fused RMSNorm."""
-    g = torch.Generator(device="cpu").manual_seed(7)
-    big_x = torch.randn(41, 4096 + 64, generator=g).to(torch.bfloat16).to(DEV)
+@pytest.mark.parametrize("rows", [6, 20, 40])
+def test_linear_wide_and_stream_strided_rows_and_in_place_residual(rows):
+    """The wide kernel (6 rows) and the stream kernel (20 and 40 rows) with strided x /
+    weight rows and out aliasing the residual, with and without the fused RMSNorm."""
+    g = torch.Generator(device="cpu").manual_seed(7 + rows)
+    big_x = torch.randn(2 * rows + 1, 4096 + 64, generator=g).to(torch.bfloat16).to(DEV)
     big_w = (torch.randn(700, 4096 + 32, generator=g) / 64).to(torch.bfloat16).to(DEV)
-    x, w = big_x[1:41:2, :4096], big_w[:, 32:]  # 20 rows of stride 8320, weight stride 4128
-    assert x.stride(0) == 8320 and w.stride(0) == 4128
-    res = torch.randn(20, 700, generator=g).to(torch.bfloat16).to(DEV)
+    x, w = big_x[1::2, :4096], big_w[:, 32:]  # rows of stride 8320, weight stride 4128
+    assert x.shape[0] == rows and x.stride(0) == 8320 and w.stride(0) == 4128
+    res = torch.randn(rows, 700, generator=g).to(torch.bfloat16).to(DEV)
     keep = res.clone()
     with torch.inference_mode():
         out = ops.linear(x, w, res, out=res)
