@@ -365,12 +365,26 @@ class Mamba3(nn.Module):
         if cache is not None and len(cache) != depth:
             raise ValueError(f"expected cache for {depth} layers")
         updated: list[_LayerCache] = []
+        if x.shape[0] <= ops.DECODE_LINEAR_ROWS:
+            # few rows: each block's RMSNorm and residual add run inside its two projections
+            for i, layer in enumerate(self.layers):
+                layer_cache = None if cache is None else cache[i]
+                x, layer_cache = layer.step(x, layer_cache,
+                                            inplace=inplace and layer_cache is not None)
+                updated.append(layer_cache)
+            return self.norm_f(x), updated
+        # more rows (general GEMM projections): each residual add runs fused with the RMSNorm
+        # after it, as in the forward's layer loop
+        h, mixed = x, None
         for i, layer in enumerate(self.layers):
             layer_cache = None if cache is None else cache[i]
-            x, layer_cache = layer.step(x, layer_cache,
-                                        inplace=inplace and layer_cache is not None)
+            normed, h = self._add_norm(h, mixed, layer.norm, self._norm_dtype(h), keep_sum=True)
+            mixed, layer_cache = layer.mixer.step(normed, layer_cache,
+                                                  inplace=inplace and layer_cache is not None)
             updated.append(layer_cache)
-        return self.norm_f(x), updated
+        out, _ = self._add_norm(h, mixed, self.norm_f, torch.promote_types(h.dtype, mixed.dtype),
+                                keep_sum=False)
+        return out, updated
 
     def set_chunk_sizes(self, *, training: int | None = None,
                         inference: int | None = None) -> Mamba3:
