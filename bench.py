@@ -534,10 +534,10 @@ def main() -> None:
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the default extra lines (configs 3 and 5, decode R=4 B=256 and "
-                         "R=1 B=1)")
+                    help="skip the default extra lines (configs 3 and 5, decode R=4 B=256, "
+                         "R=1 B=64 and R=1 B=1)")
     ap.add_argument("--extra", action="store_true",
-                    help="also measure config 5 long, config 4 at every B and R, the chunk-state "
+                    help="also measure config 5 long, config 4 at more B and R, the chunk-state "
                          "update and the hook boundaries")
     ap.add_argument("--extra-only", choices=("config3", "config5", "config5_long", "decode",
                                              "chunk_state", "hook", "hook_step"),
@@ -556,7 +556,7 @@ def main() -> None:
         print(msg, file=sys.stderr, flush=True)
 
     # The headline call is prepared first. The default extra lines (BASELINE configs 3 and 5
-    # and two more decode points) run next, and the headline call is timed right after them:
+    # and three more decode points) run next, and the headline call is timed right after them:
     # its kernels then run at the clocks of sustained load, as in a serving or prefill loop,
     # not in the clock ramp of the first tens of launches after an idle GPU.
     prep = prepare_prefill()
@@ -565,6 +565,7 @@ def main() -> None:
         # the sustained prefill load (config 3) last, right before the headline
         if not args.no_decode:
             extra["config4_decode_r4_b256"] = bench_decode(256, args.decode_steps, log, rank=4)
+            extra["config4_decode_r1_b64"] = bench_decode(64, args.decode_steps, log, rank=1)
             extra["config4_decode_r1_b1"] = bench_decode(1, args.decode_steps, log, rank=1)
         extra["config5_bidir_16x2048"] = bench_prefill_config(
             "config 5", 768, 12, 1, False, (16, 2048, 768), 4, log)
@@ -586,7 +587,7 @@ def main() -> None:
                 "config 5 long", 768, 12, 1, False, (1, 65536, 768), 4, log, iters=2)),
             "config4_decode": ("decode", lambda: [
                 bench_decode(b, args.decode_steps, log, rank=r)
-                for b, r in ((1, 1), (64, 1), (256, 4), (64, 4), (1, 4))]),
+                for b, r in ((64, 4), (1, 4), (32, 1), (16, 1))]),
             "chunk_state_config2": ("chunk_state", lambda: bench_chunk_state(log)),
             "hook_scan_config2": ("hook", lambda: bench_hook_scan(log)),
             "hook_step_b256": ("hook_step", lambda: [bench_hook_step(log, rank=r) for r in (1, 4)]),
