@@ -19,13 +19,13 @@
 // Every workgroup reads all of x, so it takes the shapes whose workgroups fit one pass over the
 // CUs: the out_proj shape (N 2048, K 4096) in 6.4 us at M = 5 and 8.2 us at M = 16.
 //
-// stream kernel (M <= 64, K a multiple of 256): all the x rows and 16-48 weight rows per
-// workgroup, x and weight tiles loaded straight into an LDS ring (no registers held in flight),
-// the K steps of a stage split over the waves. Fewer workgroups than the wide kernel read x.
-// Timed in a graph of 24 calls with distinct weights: in_proj (N 8672, K 2048) 9.4-10.5 us at
-// M = 5-32 and 13.5 us at M = 64, 9.6-11.0 / 14.7 us with the RMSNorm fused, against about
-// 14-15.4 us for hipBLASLt and 5 us more for a separate norm; out_proj 8.4-9.0 us at M = 17-32
-// and 12.1 us at M = 64.
+// stream kernel (M <= 64, K a multiple of 256): a block of 32 or 64 x rows and 16-48 weight
+// rows per workgroup, x and weight tiles loaded straight into an LDS ring (no registers held in
+// flight), the K steps of a stage split over the waves. Fewer workgroups than the wide kernel
+// read x. Timed in a graph of 24 calls with distinct weights: in_proj (N 8672, K 2048)
+// 9.4-10.5 us at M = 5-32 and 13.5 us at M = 64, 9.6-11.0 / 14.7 us with the RMSNorm fused,
+// against about 14-15.4 us for hipBLASLt and 5 us more for a separate norm; out_proj (N 2048,
+// K 4096) 8.4-9.0 us at M = 17-64.
 //
 // rows kernel (M <= 32 where the kernels above do not apply): a weight stream. The B operand of
 // a 16x16x32 MFMA is, per lane, 16 contiguous bytes of one weight row (lane l16 + 16 lg holds
@@ -937,14 +937,26 @@ LinPlan plan(int64_t m, int64_t n, int64_t k, bool norm) {
     return p;
   }
   if (m <= 64 && k % 256 == 0) {
-    // stream kernel: all the rows in one tile of 32 or 64, and the fewest weight rows per
-    // workgroup (16, 32 or 48) that keep the workgroups within one pass over the CUs (each
-    // workgroup reads all of x, so fewer of them read less of it)
+    // stream kernel: the smallest workgroup tile (x rows MT + weight rows NT, the bytes each
+    // workgroup streams per K step) whose workgroups fit one pass over the CUs; above 32 rows a
+    // 32-row tile runs as two row blocks (out_proj at M = 64: 9.0 against 12.1 us with one
+    // 64-row block)
+    static constexpr int kFew[][2] = {{32, 16}, {32, 32}, {32, 48}};
+    static constexpr int kMore[][2] = {{32, 16}, {32, 32}, {64, 16}, {64, 32}, {64, 48}};
+    const auto& tiles = m <= 32 ? kFew : kMore;
+    const int count = m <= 32 ? 3 : 5;
     p.stream = true;
-    p.a = m <= 32 ? 32 : 64;
-    p.b = cdiv(n, 16) <= kCUs ? 16 : cdiv(n, 32) <= kCUs ? 32 : 48;
+    p.a = tiles[count - 1][0];  // (the largest, when none fits one pass)
+    p.b = tiles[count - 1][1];
+    for (int i = 0; i < count; ++i) {
+      if (cdiv(m, tiles[i][0]) * cdiv(n, tiles[i][1]) <= kCUs) {
+        p.a = tiles[i][0];
+        p.b = tiles[i][1];
+        break;
+      }
+    }
     p.gx = static_cast<int>(cdiv(n, p.b));
-    p.gy = 1;
+    p.gy = static_cast<int>(cdiv(m, p.a));
     p.splits = 1;
     p.k_split = static_cast<int>(k);
     return p;

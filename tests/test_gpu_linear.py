@@ -48,7 +48,7 @@ SHAPES = [
     (20, 4100, 1280),   # stream, 32 weight rows (N / 16 just past the 256 CUs)
     (33, 8672, 2048),   # stream, 64-row tile, ragged rows
     (64, 8672, 2048),   # decode B = 64 in_proj (64-row tile, 48 weight rows)
-    (64, 2048, 4096),   # decode B = 64 out_proj (64-row tile, 16 weight rows)
+    (64, 2048, 4096),   # decode B = 64 out_proj (two 32-row blocks, 16 weight rows)
     (40, 5000, 768),    # stream, 64-row tile, 32 weight rows, ragged N
     (48, 12289, 256),   # stream, one stage of K, more workgroups than CUs, one row past N / 16
     (5, 100, 800),      # K not a multiple of 256: the rows kernel
