@@ -379,8 +379,9 @@ __device__ __forceinline__ void st4(void* base, int64_t i, const float (&x)[4]) 
 // PIN (few (batch, head) pairs, where each workgroup's latency chain is the step's time): the
 // state loads are issued as soon as their own addresses are known, ahead of the other kernel
 // arguments' round trips (the compiler otherwise places them after about six of those). With
-// many pairs the launch streams and the default order is the faster one (B = 1: 2,058 against
-// 2,012 tokens/s for config 4; B = 256: 46.3K against 46.8K).
+// many pairs the launch streams and the default order is the faster one (config 4, tokens/s:
+// B = 1 2,058 against 2,012 and B = 32 27.25K against 27.04K; B = 64 36.1K either way; B = 256
+// 46.3K against 46.8K), so the launch takes it below 2048 (batch, head) pairs.
 template <typename T, int R, int RPT, bool FULL, bool PIN = false>
 __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_args a) {
   constexpr int N = 128, P = 64, S = 32;
@@ -1074,9 +1075,9 @@ static bool step_full(const m3_step_args& a) {
 
 template <typename T, int R, int RPT>
 static void launch128(const m3_step_args& a, dim3 grid, dim3 block, hipStream_t stream,
-                      bool few) {
+                      bool pin) {
   if (step_full(a)) {
-    if (few) {
+    if (pin) {
       hipLaunchKernelGGL((step128_kernel<T, R, RPT, true, true>), grid, block, 0, stream, a);
     } else {
       hipLaunchKernelGGL((step128_kernel<T, R, RPT, true>), grid, block, 0, stream, a);
@@ -1115,14 +1116,15 @@ static int launch_step(const m3_step_args& a, hipStream_t stream) {
   // The 256-thread form at every batch: at B = 1 its 4 waves start together, where a 1024-
   // thread form's 16 waves start in four groups about 1400 cycles apart and its barrier waits
   // for the last (13.1k against 18.1k cycles per workgroup, measured).
-  const bool few = static_cast<int64_t>(a.batch) * a.heads < 1024;
+  const int64_t pairs = static_cast<int64_t>(a.batch) * a.heads;
+  const bool few = pairs < 1024, pin = pairs < 2048;
   if ((a.rank <= 2 || (a.rank == 4 && few)) && step128_ok(a)) {
     if (a.rank == 1) {
-      launch128<T, 1, 8>(a, grid, block, stream, few);
+      launch128<T, 1, 8>(a, grid, block, stream, pin);
     } else if (a.rank == 2) {
-      launch128<T, 2, 8>(a, grid, block, stream, few);
+      launch128<T, 2, 8>(a, grid, block, stream, pin);
     } else {
-      launch128<T, 4, 8>(a, grid, block, stream, few);
+      launch128<T, 4, 8>(a, grid, block, stream, pin);
     }
     return check_launch("m3_step");
   }
