@@ -677,9 +677,9 @@ __device__ __forceinline__ void lin_load_lds(__amdgpu_buffer_rsrc_t r, char* dst
 #endif
 }
 
-// 4 < M <= 64: every x row (MT = 32 or 64) and NT weight rows per 512-thread workgroup over
-// the whole K range (one rounding, no reduce launch). Stages of KB elements of K hold the MT x
-// rows and NT weight rows in LDS, S stages in a ring, loaded straight into LDS (buffer loads
+// 4 < M <= 64: a block of MT = 32 or 64 x rows (blockIdx.y) and NT weight rows (blockIdx.x) per
+// 512-thread workgroup over the whole K range (one rounding, no reduce launch). Stages of KB
+// elements of K hold the MT x rows and NT weight rows in LDS, S stages in a ring, loaded straight into LDS (buffer loads
 // with the LDS destination): a load unit is one instruction, 64 lanes x 16 bytes = RPU whole
 // row pieces, contiguous in memory and in LDS, and the ring keeps S - 1 stages in flight with no
 // registers held. Within a row piece the 16-byte chunk c sits at position c ^ (row & 15), so the
