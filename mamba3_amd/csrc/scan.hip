@@ -238,6 +238,8 @@ __device__ __forceinline__ void load_words(uint32_t (&w)[NW], const T* p, int n,
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Two values rounded to a 16-bit type (round to nearest even) and packed into one word, a
@@ -1063,6 +1065,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // over each 16-row tile, so the carry's and the intra product's 16-byte reads of 16 rows hit
   // 16 distinct bank groups (8- and 16-byte LDS accesses see 64 banks)
   constexpr int KSH = F32 ? 3 : 4, VSH = F32 ? 2 : 4;
+  // 16-bit: the carry reads K~^T straight from the row-major Ks through transposing LDS reads,
+  // with each token's scale * end decay on a scaled copy of V^T (VS, in KT's place)
+  constexpr bool KTR = !F32;
   // FULL: the model's shape (N = 128, P = 64, S = 32) in projection form with vector loads
   constexpr bool FIX = FULL || SHAPE;  // the model's shape, fixed at compile time
   const int N = FIX ? kNPad : a.d_state;
@@ -1093,7 +1098,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   extern __shared__ __attribute__((aligned(16))) char smem[];
   T* Qs = lds_t<T>(smem, Lay::QS);
   T* Ks = lds_t<T>(smem, Lay::KS);
-  T* KT = lds_t<T>(smem, Lay::KT);
+  T* KT = lds_t<T>(smem, Lay::KT);  // FP32: [n][row] K~, transposed and scaled (carry)
+  T* VS = KT;                        // 16-bit: [p][row] rank values scaled per token (carry)
   T* VT = lds_t<T>(smem, Lay::VT);  // [p][row] rank values v mx_r, transposed (intra, carry)
   T* VR = lds_t<T>(smem, Lay::VR);  // [row][p] the same, row-major (epilogue D v)
   T* ZR = lds_t<T>(smem, Lay::ZR);  // [row][p] rank gates z mz_r, row-major (epilogue)
@@ -1482,17 +1488,19 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
         for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
       }
-      // K^T for the carry, each row scaled by its token's scale * end decay (the carry's
-      // K~ e^{cum_last - cum}, ops.py:806-816)
-      const int r0 = (2 * rp) / R, r1 = (2 * rp + 1) / R;
-      const float cl = SC[SB_::CL];
-      const float e0 = SC[SB_::SCL + r0] * __expf(cl - SC[SB_::CUM + r0]);
-      const float e1 = SC[SB_::SCL + r1] * __expf(cl - SC[SB_::CUM + r1]);
+      // (FP32) K^T for the carry, each row scaled by its token's scale * end decay (the
+      // carry's K~ e^{cum_last - cum}, ops.py:806-816)
+      if constexpr (!KTR) {
+        const int r0 = (2 * rp) / R, r1 = (2 * rp + 1) / R;
+        const float cl = SC[SB_::CL];
+        const float e0 = SC[SB_::SCL + r0] * __expf(cl - SC[SB_::CUM + r0]);
+        const float e1 = SC[SB_::SCL + r1] * __expf(cl - SC[SB_::CUM + r1]);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int n = col_of(i);
-        if (FIX || n < N) {
-          st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> KSH), kt[0][i] * e0, kt[1][i] * e1);
+        for (int i = 0; i < 8; ++i) {
+          const int n = col_of(i);
+          if (FIX || n < N) {
+            st_pair<T>(KT + n * LR + swz<ROWS>(2 * rp, n >> KSH), kt[0][i] * e0, kt[1][i] * e1);
+          }
         }
       }
     };
@@ -1518,6 +1526,15 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           z[j][i] = raw_get<T>(rz[j], i);
         }
       }
+      // (16-bit) rows 2vp, 2vp+1 of VS: the token's scale * end decay (the carry's
+      // e^{cum_last - cum} K~ factor, ops.py:806-816, moved onto V)
+      float ev0 = 0.f, ev1 = 0.f;
+      if constexpr (KTR) {
+        const int u0 = (2 * vp) / R, u1 = (2 * vp + 1) / R;
+        const float cl = SC[SB_::CL];
+        ev0 = SC[SB_::SCL + u0] * __expf(cl - SC[SB_::CUM + u0]);
+        ev1 = SC[SB_::SCL + u1] * __expf(cl - SC[SB_::CUM + u1]);
+      }
       if (R == 1 && !F32) {
         // the loaded 16-bit words go to LDS unchanged: VR / ZR rows as they are, VT pairs
         // (token 2vp, token 2vp+1) of one column by a byte permute
@@ -1526,7 +1543,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           const int p = p0 + i;
           const uint32_t pr = __builtin_amdgcn_perm(rv[1][i >> 1], rv[0][i >> 1],
                                                     (i & 1) ? 0x07060302u : 0x05040100u);
-          if (FIX || p < P) *reinterpret_cast<uint32_t*>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH)) = pr;
+          if (FIX || p < P) {
+            *reinterpret_cast<uint32_t*>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH)) = pr;
+            st_pair<T>(VS + p * LR + swz<ROWS>(2 * vp, p >> VSH), v[0][i] * ev0, v[1][i] * ev1);
+          }
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -1575,6 +1595,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           const int p = p0 + i;
           if (FIX || p < P) {
             st_pair<T>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH), vq[0][i], vq[1][i]);
+            if constexpr (KTR) {
+              st_pair<T>(VS + p * LR + swz<ROWS>(2 * vp, p >> VSH), vq[0][i] * ev0, vq[1][i] * ev1);
+            }
           }
         }
       }
@@ -1673,13 +1696,22 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       if (!all_tiles && u >= n_tiles) continue;
       const int ni = u / kPT, pj = u - ni * kPT;
       const int nrow = 16 * ni + l16, prow = 16 * pj + l16;
-      if constexpr (!F32) {
+      if constexpr (KTR) {
+        // A: 8 tokens of column nrow from the row-major Ks, two transposing reads of 4 tokens
+        // (in each 16-lane group, lane 4a + b receives element b of the 8-byte vectors of lanes
+        // a, a + 4, a + 8, a + 12: lane x addresses token x / 4, columns 4 (x % 4) ..)
+        const T* kc = Ks + (l16 >> 2) * LQ + 16 * ni + 4 * (l16 & 3);
 #pragma unroll
         for (int kk = 0; kk < ROWS; kk += 32) {
-          const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
-              KT + nrow * LR + swz<ROWS>(kk + 8 * lg, nrow >> KSH));
+          const T* k0 = kc + (kk + 8 * lg) * LQ;
+          const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(k0));
+          const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(k0 + 4 * LQ));
+          const typename M::v8 av = __builtin_bit_cast(
+              typename M::v8, (i16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
           const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
-              VT + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> VSH));
+              VS + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> VSH));
           st[k] = M::mma(av, bv, st[k]);
         }
       } else {
