@@ -1536,21 +1536,14 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         ev1 = SC[SB_::SCL + u1] * __expf(cl - SC[SB_::CUM + u1]);
       }
       if (R == 1 && !F32) {
-        // the loaded 16-bit words go to LDS unchanged: VR / ZR rows as they are, VT pairs
-        // (token 2vp, token 2vp+1) of one column by a byte permute
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int p = p0 + i;
-          const uint32_t pr = __builtin_amdgcn_perm(rv[1][i >> 1], rv[0][i >> 1],
-                                                    (i & 1) ? 0x07060302u : 0x05040100u);
-          if (FIX || p < P) {
-            *reinterpret_cast<uint32_t*>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH)) = pr;
-            st_pair<T>(VS + p * LR + swz<ROWS>(2 * vp, p >> VSH), v[0][i] * ev0, v[1][i] * ev1);
-          }
-        }
+        // the loaded 16-bit words go to LDS unchanged as VR / ZR rows; VS rows scaled
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          if constexpr (SO) break;
+          f4 sv;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sv[i] = v[j][i] * (j ? ev1 : ev0);
+          st_quad<T>(VS + (2 * vp + j) * LP + p0, sv);
+          if constexpr (SO) continue;
           *reinterpret_cast<u32x2*>(VR + (2 * vp + j) * LP + p0) = (u32x2){rv[j][0], rv[j][1]};
           *reinterpret_cast<u32x2*>(ZR + (2 * vp + j) * LP + p0) = (u32x2){rz[j][0], rz[j][1]};
         }
@@ -1590,14 +1583,19 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
             st_quad<T>(ZR + row * LP + p0, zq);
           }
         }
+        if constexpr (KTR) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int p = p0 + i;
-          if (FIX || p < P) {
-            st_pair<T>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH), vq[0][i], vq[1][i]);
-            if constexpr (KTR) {
-              st_pair<T>(VS + p * LR + swz<ROWS>(2 * vp, p >> VSH), vq[0][i] * ev0, vq[1][i] * ev1);
-            }
+          for (int jr = 0; jr < 2; ++jr) {
+            f4 sv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[i] = vq[jr][i] * (jr ? ev1 : ev0);
+            st_quad<T>(VS + (2 * vp + jr) * LP + p0, sv);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int p = p0 + i;
+            if (FIX || p < P) st_pair<T>(VT + p * LR + swz<ROWS>(2 * vp, p >> VSH), vq[0][i], vq[1][i]);
           }
         }
       }
@@ -1701,6 +1699,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         // (in each 16-lane group, lane 4a + b receives element b of the 8-byte vectors of lanes
         // a, a + 4, a + 8, a + 12: lane x addresses token x / 4, columns 4 (x % 4) ..)
         const T* kc = Ks + (l16 >> 2) * LQ + 16 * ni + 4 * (l16 & 3);
+        const T* vc = VS + (l16 >> 2) * LP + 16 * pj + 4 * (l16 & 3);  // B: the same from VS
 #pragma unroll
         for (int kk = 0; kk < ROWS; kk += 32) {
           const T* k0 = kc + (kk + 8 * lg) * LQ;
@@ -1710,8 +1709,13 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
               (__attribute__((address_space(3))) i16x4*)(k0 + 4 * LQ));
           const typename M::v8 av = __builtin_bit_cast(
               typename M::v8, (i16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-          const typename M::v8 bv = *reinterpret_cast<const typename M::v8*>(
-              VS + prow * LR + swz<ROWS>(kk + 8 * lg, prow >> VSH));
+          const T* v0 = vc + (kk + 8 * lg) * LP;
+          const i16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(v0));
+          const i16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(v0 + 4 * LP));
+          const typename M::v8 bv = __builtin_bit_cast(
+              typename M::v8, (i16x8){vlo[0], vlo[1], vlo[2], vlo[3], vhi[0], vhi[1], vhi[2], vhi[3]});
           st[k] = M::mma(av, bv, st[k]);
         }
       } else {
@@ -1800,10 +1804,14 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         for (int m = 0; m < (RT + 1) / 2; ++m) {
           if (2 * m > it) continue;
           typename M::v8 av, bv;
-          const typename M::v4 b0 = *reinterpret_cast<const typename M::v4*>(
-              VT + pcol * LR + swz<ROWS>(32 * m + 4 * lg, key));
-          const typename M::v4 b1 = *reinterpret_cast<const typename M::v4*>(
-              VT + pcol * LR + swz<ROWS>(32 * m + 16 + 4 * lg, key));
+          // 4 tokens of column pcol from the row-major VR by a transposing read each
+          const T* vr0 = VR + (32 * m + 4 * lg + (l16 >> 2)) * LP + 16 * pj + 4 * (l16 & 3);
+          const typename M::v4 b0 = __builtin_bit_cast(
+              typename M::v4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                  (__attribute__((address_space(3))) i16x4*)(vr0)));
+          const typename M::v4 b1 = __builtin_bit_cast(
+              typename M::v4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                  (__attribute__((address_space(3))) i16x4*)(vr0 + 16 * LP)));
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             bv[i] = from_f<T>(wsc[2 * m][i]);
