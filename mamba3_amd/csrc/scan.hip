@@ -1061,12 +1061,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   constexpr bool MSPLIT = FULL && R > 1 && !F32;
   constexpr int TPL = SPLIT ? 8 : 4;   // tokens per phase lane
   constexpr int PG = TOK / TPL;        // phase lanes per angle
-  // swizzle keys of the transposed tiles, n >> KSH for KT and p >> VSH for VT. 16-bit: constant
-  // over each 16-row tile, so the carry's and the intra product's 16-byte reads of 16 rows hit
-  // 16 distinct bank groups (8- and 16-byte LDS accesses see 64 banks)
+  // swizzle keys of the FP32 transposed tiles, n >> KSH for KT and p >> VSH for VT
   constexpr int KSH = F32 ? 3 : 4, VSH = F32 ? 2 : 4;
-  // 16-bit: the carry reads K~^T straight from the row-major Ks through transposing LDS reads,
-  // with each token's scale * end decay on a scaled copy of V^T (VS, in KT's place)
+  // 16-bit: no transposed copies. The carry reads K~^T from the row-major Ks and V from the
+  // row-major VS (the rank values with each token's scale * end decay, in KT's place), the
+  // intra product V^T from VR, all through transposing LDS reads
   constexpr bool KTR = !F32;
   // FULL: the model's shape (N = 128, P = 64, S = 32) in projection form with vector loads
   constexpr bool FIX = FULL || SHAPE;  // the model's shape, fixed at compile time
@@ -1099,8 +1098,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   T* Qs = lds_t<T>(smem, Lay::QS);
   T* Ks = lds_t<T>(smem, Lay::KS);
   T* KT = lds_t<T>(smem, Lay::KT);  // FP32: [n][row] K~, transposed and scaled (carry)
-  T* VS = KT;                        // 16-bit: [p][row] rank values scaled per token (carry)
-  T* VT = lds_t<T>(smem, Lay::VT);  // [p][row] rank values v mx_r, transposed (intra, carry)
+  T* VS = KT;                        // 16-bit: [row][p] rank values scaled per token (carry)
+  T* VT = lds_t<T>(smem, Lay::VT);  // FP32: [p][row] rank values v mx_r, transposed
   T* VR = lds_t<T>(smem, Lay::VR);  // [row][p] the same, row-major (epilogue D v)
   T* ZR = lds_t<T>(smem, Lay::ZR);  // [row][p] rank gates z mz_r, row-major (epilogue)
   T* Sb = lds_t<T>(smem, Lay::SB);
@@ -1375,9 +1374,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       if (2 * tid < side_n) *reinterpret_cast<float2*>(scb(c + 1) + 2 * tid) = side;
       ang_store(ang);
     }
-    // q / k rows -> Qs, Ks (row-major), KT (transposed, swizzled); rows 2rp, 2rp+1. SPLIT: one
-    // copy of the code per column half, rotated (waves 0-3) or not, so no values merge between
-    // the two.
+    // q / k rows -> Qs, Ks (row-major), FP32 KT (transposed, swizzled); rows 2rp, 2rp+1.
+    // SPLIT: one copy of the code per column half, rotated (waves 0-3) or not, so no values
+    // merge between the two.
     auto stage_qk = [&](auto rot_tag) {
       constexpr bool ROT = decltype(rot_tag)::value;
       // (q, k) RMSNorm factors of rows 2rp, 2rp+1
@@ -1513,8 +1512,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     } else if (qk_on) {
       stage_qk(std::false_type{});
     }
-    // value / gate of tokens 2vp, 2vp+1, columns p0 .. p0+3: rank values v mx_r -> VT
-    // (transposed, swizzled) and VR (row-major), rank gates z mz_r -> ZR (row-major)
+    // value / gate of tokens 2vp, 2vp+1, columns p0 .. p0+3: rank values v mx_r -> VR
+    // (row-major; 16-bit also VS, scaled; FP32 VT, transposed and swizzled), rank gates z mz_r
+    // -> ZR (row-major)
     if (vz_on) {
       constexpr int VJ = Feed<T, R, FULL>::VJ;
       float v[VJ][4], z[VJ][4];
