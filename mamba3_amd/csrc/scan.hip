@@ -328,6 +328,18 @@ __device__ __forceinline__ int swz(int row, int key) {
   return row ^ (8 * (key & (ROWS / 8 - 1)));
 }
 
+// Column col of row row of the 16-bit Ks tile: its 16-byte chunk c sits at c ^ 2 (row & 3). The
+// scores' reads of one chunk in 16 consecutive rows (rows 272 bytes apart) still cover 16 bank
+// groups, and the carry's transposing reads of 4 rows x 32 bytes no longer overlap. FP32: as is.
+template <bool F32>
+__device__ __forceinline__ int ks_col(int row, int col) {
+  if constexpr (F32) {
+    return col;
+  } else {
+    return (((col >> 3) ^ (2 * (row & 3))) << 3) | (col & 7);
+  }
+}
+
 // Buffer resource over `bytes` bytes from `base` (raw, stride 0): loads at offsets beyond the
 // extent return zero, stores there are dropped.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
@@ -1478,11 +1490,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) { lo[i] = k[i]; hi[i] = k[i + 4]; }
-          st_quad<T>(Ks + row * LQ + n0, lo);
-          st_quad<T>(Ks + row * LQ + n0 + 64, hi);
+          st_quad<T>(Ks + row * LQ + ks_col<F32>(row, n0), lo);
+          st_quad<T>(Ks + row * LQ + ks_col<F32>(row, n0 + 64), hi);
         } else {
           if constexpr (!SO) st_row8<T>(Qs + row * LQ + n0, q);
-          st_row8<T>(Ks + row * LQ + n0, k);
+          st_row8<T>(Ks + row * LQ + ks_col<F32>(row, n0), k);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
@@ -1676,7 +1688,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
         for (int kk = 0; kk < NP / 32; ++kk) {
           const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
-              Ks + (16 * sj + l16) * LQ + 32 * kk + 8 * lg);
+              Ks + (16 * sj + l16) * LQ + ks_col<F32>(l16, 32 * kk + 8 * lg));
           acc[sj] = M::mma(av, qv[kk], acc[sj]);
         }
       } else {
@@ -1698,7 +1710,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         // A: 8 tokens of column nrow from the row-major Ks, two transposing reads of 4 tokens
         // (in each 16-lane group, lane 4a + b receives element b of the 8-byte vectors of lanes
         // a, a + 4, a + 8, a + 12: lane x addresses token x / 4, columns 4 (x % 4) ..)
-        const T* kc = Ks + (l16 >> 2) * LQ + 16 * ni + 4 * (l16 & 3);
+        const T* kc = Ks + (l16 >> 2) * LQ + ks_col<F32>(l16 >> 2, 16 * ni + 4 * (l16 & 3));
         const T* vc = VS + (l16 >> 2) * LP + 16 * pj + 4 * (l16 & 3);  // B: the same from VS
 #pragma unroll
         for (int kk = 0; kk < ROWS; kk += 32) {
@@ -1914,7 +1926,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
     for (int i = tid; i < R * N; i += kThreads) {
       const int r = i / N, n = i - r * N;
       static_cast<T*>(a.final_k.ptr)[b * a.final_k.stride[0] + h * a.final_k.stride[1] +
-                                     r * a.final_k.stride[2] + n] = Ks[(tl * R + r) * LQ + n];
+                                     r * a.final_k.stride[2] + n] =
+          Ks[(tl * R + r) * LQ + ks_col<F32>(tl * R + r, n)];
     }
   }
 
