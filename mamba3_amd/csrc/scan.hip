@@ -328,12 +328,12 @@ __device__ __forceinline__ int swz(int row, int key) {
   return row ^ (8 * (key & (ROWS / 8 - 1)));
 }
 
-// Column col of row row of the 16-bit Ks tile: its 16-byte chunk c sits at c ^ 2 (row & 3). The
-// scores' reads of one chunk in 16 consecutive rows (rows 272 bytes apart) still cover 16 bank
-// groups, and the carry's transposing reads of 4 rows x 32 bytes no longer overlap. FP32: as is.
-template <bool F32>
+// Column col of row row of the Ks tile when swizzled: its 16-byte chunk c sits at c ^ 2 (row & 3)
+// (16-bit). The scores' reads of one chunk in 16 consecutive rows (rows 272 bytes apart) still
+// cover 16 bank groups, and the carry's transposing reads of 4 rows x 32 bytes no longer overlap.
+template <bool PLAIN>
 __device__ __forceinline__ int ks_col(int row, int col) {
-  if constexpr (F32) {
+  if constexpr (PLAIN) {
     return col;
   } else {
     return (((col >> 3) ^ (2 * (row & 3))) << 3) | (col & 7);
@@ -1059,6 +1059,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   constexpr int WPR = kWaves / RT;     // waves sharing one query row tile
   constexpr int TOK = ROWS / R;        // tokens per sub-chunk
   constexpr bool F32 = sizeof(T) == 4;
+  // the swizzled Ks layout (ks_col): rank 1 in 16 bits (config 2 442 against 445 us); at rank 4
+  // it measured within the 1% spread of these comparisons, and the plain rows are kept
+  constexpr bool KSW = !F32 && R == 1;
   constexpr int ES = sizeof(T);
   constexpr int LQ = Lay::LQ, LR = Lay::LR, LP = Lay::LP, NP = kNPad, CST = Lay::CST;
   using SB_ = ScBlk<TOK>;
@@ -1490,11 +1493,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) { lo[i] = k[i]; hi[i] = k[i + 4]; }
-          st_quad<T>(Ks + row * LQ + ks_col<F32>(row, n0), lo);
-          st_quad<T>(Ks + row * LQ + ks_col<F32>(row, n0 + 64), hi);
+          st_quad<T>(Ks + row * LQ + ks_col<!KSW>(row, n0), lo);
+          st_quad<T>(Ks + row * LQ + ks_col<!KSW>(row, n0 + 64), hi);
         } else {
           if constexpr (!SO) st_row8<T>(Qs + row * LQ + n0, q);
-          st_row8<T>(Ks + row * LQ + ks_col<F32>(row, n0), k);
+          st_row8<T>(Ks + row * LQ + ks_col<!KSW>(row, n0), k);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) kt[j][i] = k[i];
@@ -1688,7 +1691,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 #pragma unroll
         for (int kk = 0; kk < NP / 32; ++kk) {
           const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
-              Ks + (16 * sj + l16) * LQ + ks_col<F32>(l16, 32 * kk + 8 * lg));
+              Ks + (16 * sj + l16) * LQ + ks_col<!KSW>(l16, 32 * kk + 8 * lg));
           acc[sj] = M::mma(av, qv[kk], acc[sj]);
         }
       } else {
@@ -1710,7 +1713,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
         // A: 8 tokens of column nrow from the row-major Ks, two transposing reads of 4 tokens
         // (in each 16-lane group, lane 4a + b receives element b of the 8-byte vectors of lanes
         // a, a + 4, a + 8, a + 12: lane x addresses token x / 4, columns 4 (x % 4) ..)
-        const T* kc = Ks + (l16 >> 2) * LQ + ks_col<F32>(l16 >> 2, 16 * ni + 4 * (l16 & 3));
+        const T* kc = Ks + (l16 >> 2) * LQ + ks_col<!KSW>(l16 >> 2, 16 * ni + 4 * (l16 & 3));
         const T* vc = VS + (l16 >> 2) * LP + 16 * pj + 4 * (l16 & 3);  // B: the same from VS
 #pragma unroll
         for (int kk = 0; kk < ROWS; kk += 32) {
@@ -1927,7 +1930,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
       const int r = i / N, n = i - r * N;
       static_cast<T*>(a.final_k.ptr)[b * a.final_k.stride[0] + h * a.final_k.stride[1] +
                                      r * a.final_k.stride[2] + n] =
-          Ks[(tl * R + r) * LQ + ks_col<F32>(tl * R + r, n)];
+          Ks[(tl * R + r) * LQ + ks_col<!KSW>(tl * R + r, n)];
     }
   }
 
