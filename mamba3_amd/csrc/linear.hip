@@ -674,6 +674,8 @@ __device__ __forceinline__ void lin_load_lds(__amdgpu_buffer_rsrc_t r, char* dst
 #if defined(__HIP_DEVICE_COMPILE__)
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
                                            voff, soff, 0, AUX);
+#else
+  (void)r, (void)dst, (void)voff, (void)soff;
 #endif
 }
 

@@ -1093,7 +1093,6 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   const bool angles = FULL || a.phase_mode == M3_PHASE_ANGLES;
   const bool raw_dt = FULL || a.raw_dt != 0;
   const bool mimo_rot = FULL ? (R > 1) : (a.mimo_rotation != 0);
-  const bool vec_qk = FIX || g.vec_qk, vec_vz = FIX || g.vec_vz;
   const int H = a.heads, L = a.length;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (wave-uniform)
@@ -1136,12 +1135,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
   // (SPLIT / MSPLIT: every lane has both roles, 512 threads covering 64 rows x 128 columns and
   // 64 rows x 64 columns)
   const bool qk_on = SPLIT || MSPLIT || (rp < ROWS / 2 && n0 < N);
-  const int qk_n = min(8, N - n0);
   // v / z: row pair vp (rows 2vp, 2vp+1; tokens 2vp, 2vp+1 for R = 1), columns p0 .. p0+3
   constexpr int P4 = kPPad / 4;
   const int vp = tid / P4, p0 = 4 * (tid % P4);
   const bool vz_on = SPLIT || (2 * vp < TOK * R && p0 < P);
-  const int vz_n = min(4, P - p0);
   // phase: angle ps, token group pg (tokens TPL pg .. TPL pg + TPL-1)
   const int pg = tid % PG, ps = tid / PG;
   const bool ph_on = rotate && ps < S;
