@@ -200,20 +200,24 @@ def test_graph_decoder_matches_forward_and_resets():
         decoder(x[:, :1].clone().requires_grad_())
 
 
+@pytest.mark.parametrize("batch", [3, 40, 70])
 @pytest.mark.parametrize("rank", [1, 4])
-def test_graph_decoder_bf16_weights_against_oracle(rank):
+def test_graph_decoder_bf16_weights_against_oracle(rank, batch):
     """bf16 weights, FP32 state: a prefill loaded into the graph decoder (``load_cache``), then
     40 replays with eager work in between. Against the eager HIP steps: outputs within 1e-2,
     states within 1e-4. Against the oracle: the bf16 parity bar (``conftest.bf16_parity``) on the
     outputs, with the oracle's chain in bf16 and in FP32 (same bf16-valued weights), and the
-    FP32 states at least as close to the FP32 chain as the oracle's bf16 chain is."""
+    FP32 states at least as close to the FP32 chain as the oracle's bf16 chain is. Batch 3 runs
+    the block's norm and residual inside ``m3_linear`` (gemv), batch 40 its out_proj on the
+    stream kernel in two row blocks, batch 70 the general-GEMM loop with each residual add fused
+    into the next RMSNorm."""
     model, params, dims = _model(128, 128, 2, rank, seed=6)
     model = model.to(torch.bfloat16)
     torch.manual_seed(6)
-    x_cpu = torch.randn(3, 70, 128).to(torch.bfloat16)
+    x_cpu = torch.randn(batch, 70, 128).to(torch.bfloat16)
     x = x_cpu.to(DEV)
     split = 30
-    decoder = model.cuda_graph(batch_size=3)
+    decoder = model.cuda_graph(batch_size=batch)
     with torch.inference_mode():
         _, cache = model.prefill(x[:, :split])
     decoder.load_cache(cache)
