@@ -267,6 +267,35 @@ def test_chunk_state_matches_oracle(dtype, rank):
     torch.testing.assert_close(out.cpu(), want, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("shape", [(3, 7, 50, 2, torch.bfloat16), (32, 32, 9, 1, torch.float16)])
+def test_chunk_state_in_place(shape):
+    """state_out aliasing state_in: each workgroup rewrites only the state elements it read.
+    21 (b, h) pairs take the column-split MFMA form with a grid padded to 32 blocks; 1024 pairs
+    take one workgroup per pair."""
+    batch, heads, width, rank, dtype = shape
+    g = torch.Generator().manual_seed(11)
+    p, n = 64, 128
+    k = torch.randn(batch, heads, width, rank, n, generator=g).to(dtype)
+    v = torch.randn(batch, heads, width, rank, p, generator=g).to(dtype)
+    cum = torch.cumsum(-torch.rand(batch, heads, width, generator=g) * 0.05, -1)
+    scale = torch.rand(batch, heads, width, generator=g) * 0.1
+    state = torch.randn(batch, heads, p, n, generator=g)
+    ks = k * scale.to(dtype)[..., None, None]
+    ke = ks * torch.exp(cum[..., -1:] - cum).to(dtype)[..., None, None]
+    upd = torch.bmm(v.flatten(2, 3).float().transpose(-1, -2).flatten(0, 1),
+                    ke.flatten(2, 3).float().flatten(0, 1)).unflatten(0, (batch, heads))
+    want = torch.exp(cum[..., -1])[..., None, None] * state + upd
+    st = state.to(DEV)
+    out = torch.empty_like(st)
+    with torch.inference_mode():
+        ops.chunk_state(k.to(DEV), v.to(DEV), cum.to(DEV), scale.to(DEV), st, out,
+                        width=width, rank=rank)
+        ops.chunk_state(k.to(DEV), v.to(DEV), cum.to(DEV), scale.to(DEV), st, st,
+                        width=width, rank=rank)
+    torch.testing.assert_close(out.cpu(), want, rtol=1e-4, atol=1e-4)
+    assert torch.equal(st, out)
+
+
 # Shapes outside the MFMA kernel's tiles (d_state not a power of 2 or above 128, head_dim above
 # 64, ranks 3, 5, 6, 7): the recurrent scan. FP32 within 1e-4 of the oracle's chunked scan (the
 # same recurrence, summed in another order); 16-bit at the 16-bit parity bar.
