@@ -334,6 +334,8 @@ def bench_chunk_state(log, batch=8, heads=32, width=256, rank=1, n=128, p=64):
     log(f"chunk_state B={batch} H={heads} W={width}: {t * 1e6:.2f} us, {gbs:.0f} GB/s")
     return dict(us=round(t * 1e6, 2), bytes=nbytes, bound="hbm", achieved=round(gbs, 1),
                 peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
+                traffic=_traffic_from_profile(
+                    os.path.join(ROOT, "profiles", "chunk_state_config2_pmc.txt")),
                 kernel="m3::chunk_state_mma_kernel<__bf16>",
                 shape=f"[{batch}, {heads}] x {width} tokens, R={rank}, N={n}, P={p}")
 

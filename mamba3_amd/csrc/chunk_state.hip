@@ -172,7 +172,9 @@ __global__ __launch_bounds__(kCsThreads) void chunk_state_mma_kernel(const m3_ch
             t2{ok0 ? vr[0][i] : from_f<T>(0.f), ok1 ? vr[1][i] : from_f<T>(0.f)};
       }
     }
-    load(r0 + kCmRows < rows ? r0 + kCmRows : 0);  // (the last pass re-reads pass 0, unused)
+    // no loads after the last pass: they would add a pass of k / v reads and hold the final
+    // state read behind them in the in-order load counter
+    if (r0 + kCmRows < rows) load(r0 + kCmRows);
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < kCmRows / 32; ++ks) {
