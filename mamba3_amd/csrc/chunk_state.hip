@@ -87,19 +87,24 @@ __global__ __launch_bounds__(kCsThreads) void chunk_state_kernel(const m3_chunk_
 }
 
 // The model's shape (N = 128, P = 64) with 16-bit activations, on MFMA: the update V^T ke of
-// (b, h) is 32 tiles of S'^T (16 columns n x 16 rows p), accumulated over passes of kCmRows
+// (b, h) is 32 tiles of S'^T (16 columns n x 16 rows p), accumulated over passes of ROWS
 // (token, rank) rows with bf16 / f16 16x16x32 MFMAs (exact products of the rounded operands,
 // FP32 sums, as the reference's bmm). Each pass stages ke (the same rounding points as above)
 // and v transposed into LDS ([n][row], [p][row]); a lane stores a row pair of 8 columns, with
-// the row pairs on consecutive lanes so a store instruction's 32 lanes hit 32 banks. The global
-// loads of pass i + 1 are issued before the MFMAs of pass i. Wave w owns
-// rows p = 16 w .. 16 w + 15, all 8 column tiles; lane l ends with S'[p][n .. n+3] of each tile
-// in the MFMA output layout, one 16-byte vector of the state row.
-constexpr int kCmRows = 64;
+// the row pairs on consecutive lanes so a store instruction's lanes hit distinct banks. The
+// global loads of pass i + 1 are issued before the MFMAs of pass i. Wave w owns rows
+// p = 16 (w & 3) .. + 15 and its share of the 8 column tiles; lane l ends with S'[p][n .. n+3]
+// of each of its tiles in the MFMA output layout, one 16-byte vector of the state row.
+//
+// ROWS rows per pass, 4 ROWS threads: 128 where the (b, h) pairs fit one workgroup per CU (2
+// passes for a 256-token chunk, 52 KB of LDS), else 64 (27 KB, so more workgroups share a CU and
+// overlap their loads with each other's MFMAs). Waves 0 .. 3 of the 128-row form take column
+// tiles 0 .. 3 and waves 4 .. 7 tiles 4 .. 7 of the same p tiles.
+constexpr long kCmCUs = 256;  // MI355X compute units
 
-template <typename T>
-__global__ __launch_bounds__(kCsThreads) void chunk_state_mma_kernel(const m3_chunk_state_args a) {
-  constexpr int N = 128, P = 64, LR = kCmRows + 8, NT = N / 16;
+template <typename T, int ROWS>
+__global__ __launch_bounds__(4 * ROWS) void chunk_state_mma_kernel(const m3_chunk_state_args a) {
+  constexpr int N = 128, P = 64, LR = ROWS + 8, NT = N / 16 / (ROWS / 64), RP = ROWS / 2;
   typedef T t8 __attribute__((ext_vector_type(8)));
   const int H = a.heads, W = a.width, R = a.rank;
   const int b = blockIdx.x / H, h = blockIdx.x - (blockIdx.x / H) * H;
@@ -117,7 +122,8 @@ __global__ __launch_bounds__(kCsThreads) void chunk_state_mma_kernel(const m3_ch
   f4 acc[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
-  const int rp = tid & 31;  // row pair of the staging tasks
+  const int rp = tid & (RP - 1), cg = tid / RP;  // row pair and column group of the staging
+  const int pt = w & 3, nt0 = NT * (w >> 2);      // this wave's p tile and first column tile
   // the raw operands of one pass: every load issues unconditionally (rows past the end re-read
   // row 0 and stage zeros), so the next pass's loads fly during this pass's MFMAs
   t8 kr[2][2], vr[2];
@@ -129,23 +135,23 @@ __global__ __launch_bounds__(kCsThreads) void chunk_state_mma_kernel(const m3_ch
       const int t = row < rows ? row / R : 0, r = row < rows ? row - t * R : 0;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int n0 = 8 * ((tid >> 5) + 8 * j);
+        const int n0 = 8 * (cg + 8 * j);
         kr[j][jr] = *reinterpret_cast<const t8*>(kb + t * a.k.stride[2] + r * a.k.stride[3] + n0);
       }
       vr[jr] = *reinterpret_cast<const t8*>(vb + t * a.value.stride[2] + r * a.value.stride[3] +
-                                             8 * (tid >> 5));
+                                             8 * cg);
       sr[jr] = scl[t * a.scale.stride[2]];
       cr[jr] = cum[t * a.cumulative.stride[2]];
     }
   };
   load(0);
-  for (int r0 = 0; r0 < rows; r0 += kCmRows) {
+  for (int r0 = 0; r0 < rows; r0 += ROWS) {
     __syncthreads();  // the previous pass's operands are read
     // ke rows 2 rp, 2 rp + 1, columns 8 cg .. 8 cg + 7 (two column groups per thread), then v
     typedef T t2 __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int n0 = 8 * ((tid >> 5) + 8 * j);
+      const int n0 = 8 * (cg + 8 * j);
       float ke[2][8];
 #pragma unroll
       for (int jr = 0; jr < 2; ++jr) {
@@ -164,7 +170,7 @@ __global__ __launch_bounds__(kCsThreads) void chunk_state_mma_kernel(const m3_ch
       }
     }
     {
-      const int p0 = 8 * (tid >> 5);
+      const int p0 = 8 * cg;
       const bool ok0 = r0 + 2 * rp < rows, ok1 = r0 + 2 * rp + 1 < rows;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -174,14 +180,15 @@ __global__ __launch_bounds__(kCsThreads) void chunk_state_mma_kernel(const m3_ch
     }
     // no loads after the last pass: they would add a pass of k / v reads and hold the final
     // state read behind them in the in-order load counter
-    if (r0 + kCmRows < rows) load(r0 + kCmRows);
+    if (r0 + ROWS < rows) load(r0 + ROWS);
     __syncthreads();
 #pragma unroll
-    for (int ks = 0; ks < kCmRows / 32; ++ks) {
-      const t8 bv = *reinterpret_cast<const t8*>(&VT[(16 * w + l16) * LR + 32 * ks + 8 * lg]);
+    for (int ks = 0; ks < ROWS / 32; ++ks) {
+      const t8 bv = *reinterpret_cast<const t8*>(&VT[(16 * pt + l16) * LR + 32 * ks + 8 * lg]);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const t8 av = *reinterpret_cast<const t8*>(&KeT[(16 * nt + l16) * LR + 32 * ks + 8 * lg]);
+        const t8 av =
+            *reinterpret_cast<const t8*>(&KeT[(16 * (nt0 + nt) + l16) * LR + 32 * ks + 8 * lg]);
         if constexpr (std::is_same<T, __bf16>::value) {
           acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[nt], 0, 0, 0);
         } else {
@@ -191,20 +198,22 @@ __global__ __launch_bounds__(kCsThreads) void chunk_state_mma_kernel(const m3_ch
     }
   }
   const float ecl = expf(cl);
-  const int p = 16 * w + l16;
+  const int p = 16 * pt + l16;
   const float* sin_ = static_cast<const float*>(a.state_in.ptr) + b * a.state_in.stride[0] +
                       h * a.state_in.stride[1] + p * a.state_in.stride[2];
   float* sout = static_cast<float*>(a.state_out.ptr) + b * a.state_out.stride[0] +
                 h * a.state_out.stride[1] + p * a.state_out.stride[2];
   f4 old[NT];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) old[nt] = *reinterpret_cast<const f4*>(sin_ + 16 * nt + 4 * lg);
+  for (int nt = 0; nt < NT; ++nt) {
+    old[nt] = *reinterpret_cast<const f4*>(sin_ + 16 * (nt0 + nt) + 4 * lg);
+  }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     f4 o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = ecl * old[nt][i] + acc[nt][i];
-    *reinterpret_cast<f4*>(sout + 16 * nt + 4 * lg) = o;
+    *reinterpret_cast<f4*>(sout + 16 * (nt0 + nt) + 4 * lg) = o;
   }
 }
 
@@ -257,10 +266,15 @@ extern "C" int m3_chunk_state(const m3_chunk_state_args* args, hipStream_t strea
   if (a.batch == 0) return M3_OK;
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kCsThreads);
   if (chunk_state_mma_ok(a)) {
-    if (act == M3_BF16) {
-      hipLaunchKernelGGL(chunk_state_mma_kernel<__bf16>, grid, block, 0, stream, a);
+    const bool few = static_cast<long>(a.batch) * a.heads <= kCmCUs;
+    if (act == M3_BF16 && few) {
+      hipLaunchKernelGGL((chunk_state_mma_kernel<__bf16, 128>), grid, dim3(512), 0, stream, a);
+    } else if (act == M3_BF16) {
+      hipLaunchKernelGGL((chunk_state_mma_kernel<__bf16, 64>), grid, dim3(256), 0, stream, a);
+    } else if (few) {
+      hipLaunchKernelGGL((chunk_state_mma_kernel<_Float16, 128>), grid, dim3(512), 0, stream, a);
     } else {
-      hipLaunchKernelGGL(chunk_state_mma_kernel<_Float16>, grid, block, 0, stream, a);
+      hipLaunchKernelGGL((chunk_state_mma_kernel<_Float16, 64>), grid, dim3(256), 0, stream, a);
     }
     return check_launch("m3_chunk_state");
   }
