@@ -246,7 +246,8 @@ def test_scan_continuation(rank):
 @pytest.mark.parametrize("rank", [1, 4])
 def test_chunk_state_matches_oracle(dtype, rank):
     """The standalone per-chunk state update (reference _triton.py:500-561); 16-bit operands at
-    this shape take the MFMA form (37 x rank rows: passes of 64 with a ragged last one)."""
+    this shape take the MFMA form (6 (b, h) pairs: 128-row passes over 37 x rank rows, the last
+    one ragged)."""
     g = torch.Generator().manual_seed(4)
     batch, heads, width, p, n = 2, 3, 37, 64, 128
     k = torch.randn(batch, heads, width, rank, n, generator=g).to(dtype)
@@ -269,9 +270,8 @@ def test_chunk_state_matches_oracle(dtype, rank):
 
 @pytest.mark.parametrize("shape", [(3, 7, 50, 2, torch.bfloat16), (32, 32, 9, 1, torch.float16)])
 def test_chunk_state_in_place(shape):
-    """state_out aliasing state_in: each workgroup rewrites only the state elements it read.
-    21 (b, h) pairs take the column-split MFMA form with a grid padded to 32 blocks; 1024 pairs
-    take one workgroup per pair."""
+    """state_out aliasing state_in: each lane rewrites only the state elements it read.
+    21 (b, h) pairs take the MFMA form's 128-row passes, 1024 pairs its 64-row passes."""
     batch, heads, width, rank, dtype = shape
     g = torch.Generator().manual_seed(11)
     p, n = 64, 128
