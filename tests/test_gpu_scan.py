@@ -268,10 +268,11 @@ def test_chunk_state_matches_oracle(dtype, rank):
     torch.testing.assert_close(out.cpu(), want, rtol=1e-4, atol=1e-4)
 
 
-@pytest.mark.parametrize("shape", [(3, 7, 50, 2, torch.bfloat16), (32, 32, 9, 1, torch.float16)])
+@pytest.mark.parametrize("shape", [(3, 7, 50, 2, torch.bfloat16), (32, 32, 75, 2, torch.float16)])
 def test_chunk_state_in_place(shape):
     """state_out aliasing state_in: each lane rewrites only the state elements it read.
-    21 (b, h) pairs take the MFMA form's 128-row passes, 1024 pairs its 64-row passes."""
+    21 (b, h) pairs take the MFMA form's 128-row passes (100 rows), 1024 pairs its 64-row passes
+    (150 rows: 3 passes, the last one ragged)."""
     batch, heads, width, rank, dtype = shape
     g = torch.Generator().manual_seed(11)
     p, n = 64, 128
@@ -292,8 +293,12 @@ def test_chunk_state_in_place(shape):
                         width=width, rank=rank)
         ops.chunk_state(k.to(DEV), v.to(DEV), cum.to(DEV), scale.to(DEV), st, st,
                         width=width, rank=rank)
-    torch.testing.assert_close(out.cpu(), want, rtol=1e-4, atol=1e-4)
-    assert torch.equal(st, out)
+    # 1e-3: the reference rounds exp(cl - cum) to 16 bits from the CPU's expf, the kernel from
+    # the device's; where the two straddle a rounding boundary, one token's whole contribution
+    # moves by a 16-bit ulp (about 6e-5 x |v|), which 76,800 tokens hit a few times. A missing or
+    # misplaced pass moves most elements by 1e-1 or more.
+    torch.testing.assert_close(out.cpu(), want, rtol=1e-3, atol=1e-3)
+    assert torch.equal(st, out)  # in place and out of place agree bit for bit
 
 
 # Shapes outside the MFMA kernel's tiles (d_state not a power of 2 or above 128, head_dim above
