@@ -652,18 +652,46 @@ __device__ __forceinline__ void lin_wait_vm() {
 
 __device__ __forceinline__ void lin_wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// An LDS read the compiler does not track, and the wait that makes its value usable (the "+v"
-// operand keeps every use of v after the wait). The compiler would otherwise wait for all of the
-// wave's loads into LDS still in flight before any LDS read, which undoes the ring.
-__device__ __forceinline__ u32x4 lin_ds_read(const char* p) {
-  u32x4 v;
-  asm volatile("ds_read_b128 %0, %1"
-               : "=v"(v)
-               : "v"(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-                     (__attribute__((address_space(3))) const char*)p))));
-  return v;
+// LDS reads the compiler does not track, with the wait that makes their values usable, in one
+// asm statement: no instruction the compiler places can read an output register before the
+// wait (early-clobber outputs, so no address register is overwritten while a later read in the
+// statement still needs it). The compiler would otherwise wait for all of the wave's loads into
+// LDS still in flight before any LDS read, which undoes the ring.
+template <int K>
+__device__ __forceinline__ void lin_ds_read_all(u32x4 (&v)[K], const uint32_t (&a)[K]) {
+  static_assert(K >= 1 && K <= 6, "1 to 6 reads per statement");
+  if constexpr (K == 1) {
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v[0]) : "v"(a[0]));
+  } else if constexpr (K == 2) {
+    asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]) : "v"(a[0]), "v"(a[1]));
+  } else if constexpr (K == 3) {
+    asm volatile("ds_read_b128 %0, %3\n\tds_read_b128 %1, %4\n\tds_read_b128 %2, %5\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]) : "v"(a[0]), "v"(a[1]), "v"(a[2]));
+  } else if constexpr (K == 4) {
+    asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\tds_read_b128 %2, %6\n\t"
+                 "ds_read_b128 %3, %7\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]));
+  } else if constexpr (K == 5) {
+    asm volatile("ds_read_b128 %0, %5\n\tds_read_b128 %1, %6\n\tds_read_b128 %2, %7\n\t"
+                 "ds_read_b128 %3, %8\n\tds_read_b128 %4, %9\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]));
+  } else {
+    asm volatile("ds_read_b128 %0, %6\n\tds_read_b128 %1, %7\n\tds_read_b128 %2, %8\n\t"
+                 "ds_read_b128 %3, %9\n\tds_read_b128 %4, %10\n\tds_read_b128 %5, %11\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]));
+  }
 }
-__device__ __forceinline__ void lin_ds_wait(u32x4& v) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)); }
+
+__device__ __forceinline__ uint32_t lin_lds_addr(const char* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p));
+}
 
 // A buffer load of 16 bytes per lane written straight to LDS: lane l's bytes land at
 // dst + 16 l (dst wave-uniform). The builtin exists only in the device pass of the compiler
@@ -785,24 +813,23 @@ __global__ __launch_bounds__(512) void linear_stream_kernel(const LinGeom g) {
     const char* base = ring[slot];
 #pragma unroll
     for (int q = 0; q < QS; ++q) {
-      u32x4 ra[TMW], rb[TN], rn;
+      // the step's operands: TMW x tiles, TN weight tiles, then the norm weights
+      constexpr int NR = TMW + TN + (NORM ? 1 : 0);
+      uint32_t ad[NR];
+      u32x4 rd[NR];
 #pragma unroll
-      for (int i = 0; i < TMW; ++i) ra[i] = lin_ds_read(base + (16 * (TMW * tw + i)) * RB + roff[q]);
+      for (int i = 0; i < TMW; ++i) ad[i] = lin_lds_addr(base + (16 * (TMW * tw + i)) * RB + roff[q]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) rb[j] = lin_ds_read(base + (MT + 16 * j) * RB + roff[q]);
-      if constexpr (NORM) rn = lin_ds_read(base + 1024 * U + 16 * (4 * (kw + WK * q) + lg));
-#pragma unroll
-      for (int i = 0; i < TMW; ++i) lin_ds_wait(ra[i]);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) lin_ds_wait(rb[j]);
+      for (int j = 0; j < TN; ++j) ad[TMW + j] = lin_lds_addr(base + (MT + 16 * j) * RB + roff[q]);
+      if constexpr (NORM) ad[NR - 1] = lin_lds_addr(base + 1024 * U + 16 * (4 * (kw + WK * q) + lg));
+      lin_ds_read_all<NR>(rd, ad);
       typename M::v8 av[TMW], bv[TN];
 #pragma unroll
-      for (int i = 0; i < TMW; ++i) av[i] = __builtin_bit_cast(typename M::v8, ra[i]);
+      for (int i = 0; i < TMW; ++i) av[i] = __builtin_bit_cast(typename M::v8, rd[i]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bv[j] = __builtin_bit_cast(typename M::v8, rb[j]);
+      for (int j = 0; j < TN; ++j) bv[j] = __builtin_bit_cast(typename M::v8, rd[TMW + j]);
       if constexpr (NORM) {
-        lin_ds_wait(rn);
-        const typename M::v8 nv = __builtin_bit_cast(typename M::v8, rn);
+        const typename M::v8 nv = __builtin_bit_cast(typename M::v8, rd[NR - 1]);
 #pragma unroll
         for (int i = 0; i < TMW; ++i) {
 #pragma unroll

@@ -15,7 +15,9 @@ reference's dispatch contract:
   ``None``;
 * ``_HIP_LAST_DISPATCH`` / ``_HIP_LAST_SCAN_DISPATCH`` tell whether the last call ran on the
   GPU (the reference's ``_TRITON_LAST_DISPATCH`` / ``_TRITON_LAST_SCAN_DISPATCH``,
-  ``ops.py:14, 18``).
+  ``ops.py:14, 18``). ``bind`` installs both hooks into the reference's modules and makes every
+  call also set those two flags there, so the reference's dispatch assertions
+  (``tests/test_scan.py:423``, ``tests/test_model.py:465``) hold with the hooks bound.
 
 The call keys are the reference's: device, the dtypes of every tensor argument and the shape
 parameters (``ops.py:110-126``, ``ops.py:288-302``). Everything else (validation and its
@@ -40,6 +42,40 @@ _STEP_FAILURES: set[tuple[object, ...]] = set()
 _SCAN_FAILURES: set[tuple[object, ...]] = set()
 _HIP_LAST_DISPATCH = False
 _HIP_LAST_SCAN_DISPATCH = False
+# modules whose `_TRITON_LAST_DISPATCH` / `_TRITON_LAST_SCAN_DISPATCH` mirror the flags above
+_FLAG_TARGETS: list[object] = []
+
+
+def _set_step_flag(value: bool) -> None:
+    global _HIP_LAST_DISPATCH
+    _HIP_LAST_DISPATCH = value
+    for module in _FLAG_TARGETS:
+        module._TRITON_LAST_DISPATCH = value
+
+
+def _set_scan_flag(value: bool) -> None:
+    global _HIP_LAST_SCAN_DISPATCH
+    _HIP_LAST_SCAN_DISPATCH = value
+    for module in _FLAG_TARGETS:
+        module._TRITON_LAST_SCAN_DISPATCH = value
+
+
+def bind(ops_module, model_module=None) -> None:
+    """Serve the reference's two hooks from this module.
+
+    ``ops_module`` is the reference's ``mamba3.ops``: its ``_fused_chunk_scan`` (called by name
+    from ``mamba3_scan``, ``ops.py:635``) and ``fused_step`` become the bodies here, and every
+    call sets its ``_TRITON_LAST_DISPATCH`` / ``_TRITON_LAST_SCAN_DISPATCH`` as the reference's
+    own bodies do (``ops.py:109, 181, 285, 358``). ``model_module`` is ``mamba3.model``, which
+    imports ``fused_step`` by name (``model.py:11``, called at ``441``), so its binding is
+    replaced too.
+    """
+    ops_module._fused_chunk_scan = fused_chunk_scan
+    ops_module.fused_step = fused_step
+    if model_module is not None:
+        model_module.fused_step = fused_step
+    if not any(m is ops_module for m in _FLAG_TARGETS):
+        _FLAG_TARGETS.append(ops_module)
 
 
 def disabled() -> bool:
@@ -72,8 +108,7 @@ def fused_step(q, k, value, gate, adt, dt, trap_logits, angle_rate, D, cache, *,
     [B, S]``, ``cache = (phase, state, prev_k, prev_value)``; returns ``(output [B, H, P],
     (phase', state', k_rot, value))``.
     """
-    global _HIP_LAST_DISPATCH
-    _HIP_LAST_DISPATCH = False
+    _set_step_flag(False)
     key = (q.device, q.dtype, k.dtype, value.dtype, gate.dtype, adt.dtype, dt.dtype,
            trap_logits.dtype, angle_rate.dtype, D.dtype, tuple(t.dtype for t in cache),
            q.shape[-1], value.shape[-1], q.shape[2], cache[0].shape[-1])
@@ -84,7 +119,7 @@ def fused_step(q, k, value, gate, adt, dt, trap_logits, angle_rate, D, cache, *,
                                          cache, mimo_x=mimo_x, mimo_z=mimo_z,
                                          mimo_out=mimo_out),
                   key, _STEP_FAILURES, "fused Mamba-3 decoding")
-    _HIP_LAST_DISPATCH = result is not None
+    _set_step_flag(result is not None)
     return result
 
 
@@ -93,8 +128,7 @@ def fused_chunk_scan(q, k, value, gate, adt, dt, trap_logits, D, *, mimo_x, mimo
                      q_bias, k_bias):
     """The chunked SSD on the GPU, or ``None`` (reference ``ops._fused_chunk_scan``,
     ``ops.py:253-367``): ``(output [B, L, H, P], state [B, H, P, N] FP32)``."""
-    global _HIP_LAST_SCAN_DISPATCH
-    _HIP_LAST_SCAN_DISPATCH = False
+    _set_scan_flag(False)
     key = (q.device, q.dtype, k.dtype, value.dtype, gate.dtype, adt.dtype, dt.dtype,
            trap_logits.dtype, D.dtype, q.shape[-1], value.shape[-1], q.shape[3], chunk_size)
     if (torch.is_grad_enabled() or disabled() or key in _SCAN_FAILURES
@@ -108,7 +142,7 @@ def fused_chunk_scan(q, k, value, gate, adt, dt, trap_logits, D, *, mimo_x, mimo
         initial_k=initial_k, initial_value=initial_value, phase=phase,
         mimo_rotation=mimo_rotation, q_bias=q_bias, k_bias=k_bias),
         key, _SCAN_FAILURES, "fused Mamba-3 chunked scan")
-    _HIP_LAST_SCAN_DISPATCH = result is not None
+    _set_scan_flag(result is not None)
     return result
 
 
@@ -118,4 +152,4 @@ def reset_failures() -> None:
     _SCAN_FAILURES.clear()
 
 
-__all__ = ["fused_step", "fused_chunk_scan", "disabled", "reset_failures", "DISABLE_ENV"]
+__all__ = ["fused_step", "fused_chunk_scan", "bind", "disabled", "reset_failures", "DISABLE_ENV"]

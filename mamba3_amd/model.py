@@ -414,6 +414,13 @@ class Mamba3(nn.Module):
         return _HipGraphDecoder(self, batch_size)
 
 
+def _storage_signature(w: torch.Tensor) -> tuple[object, ...]:
+    """What a captured graph depends on for one parameter: the same checks as the reference's
+    ``_parameter_signature`` (``model.py:763-774``: identity, version, data pointer, device,
+    dtype, shape), with the object itself kept instead of its ``id``."""
+    return (w, w._version, w.data_ptr(), w.device, w.dtype, tuple(w.shape))
+
+
 class _HipGraphDecoder:
     """A decode step of the whole stack, captured once in a hipGraph and replayed.
 
@@ -435,8 +442,10 @@ class _HipGraphDecoder:
         if model.training:
             raise ValueError("cuda_graph requires model.eval()")
         self.model = model
-        # the captured tensors themselves and their version counters at capture time
-        self._captured = [(w, w._version) for w in weights]
+        # what the graph holds of each parameter: the object, its version counter, and the
+        # storage it read (address, device, dtype, shape): `Module.to`, `.half()` or
+        # `p.data = ...` keep the object and its version but move the storage
+        self._captured = [_storage_signature(w) for w in weights]
         self.input = torch.zeros(batch_size, 1, model.d_model, device=device, dtype=dtype)
         self.cache = [layer.mixer.allocate_cache(batch_size, device=device, dtype=dtype)
                       for layer in model.layers]
@@ -475,10 +484,10 @@ class _HipGraphDecoder:
         return self.output
 
     def validate(self) -> None:
-        current = list(self.model.parameters())
+        current = [_storage_signature(w) for w in self.model.parameters()]
         same = len(current) == len(self._captured) and all(
-            now is then and now._version == version
-            for now, (then, version) in zip(current, self._captured))
+            now[0] is then[0] and now[1:] == then[1:]
+            for now, then in zip(current, self._captured))
         if not same:
             raise RuntimeError("model state changed; recreate the CUDA graph decoder")
 

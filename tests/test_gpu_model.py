@@ -198,6 +198,17 @@ def test_graph_decoder_matches_forward_and_resets():
         decoder.validate()
     with pytest.raises(ValueError, match="gradient"):
         decoder(x[:, :1].clone().requires_grad_())
+    # storage moved under the same Parameter object and version: `p.data = ...`, `Module.to`
+    fresh = model.cuda_graph(batch_size=2)
+    fresh.validate()
+    weight = model.layers[0].mixer.in_proj.weight
+    weight.data = weight.data.clone()
+    with pytest.raises(RuntimeError, match="recreate"):
+        fresh(x[:, :1], validate=True)
+    fresh = model.cuda_graph(batch_size=2)
+    model.to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="recreate"):
+        fresh.validate()
 
 
 @pytest.mark.parametrize("batch", [3, 40, 70])

@@ -104,3 +104,35 @@ def test_scan_gates_follow_the_reference(monkeypatch):
         inp = _scan_inputs()
         inp["value"] = inp["value"].half()  # one activation dtype
         assert hooks.fused_chunk_scan(**inp) is None
+
+
+def test_bind_installs_the_hooks_and_sets_the_reference_flags(monkeypatch):
+    """``hooks.bind`` replaces the reference's hook bindings (``ops._fused_chunk_scan``,
+    ``ops.fused_step`` and the name ``model.fused_step`` imported at ``model.py:11``) and mirrors
+    every dispatch into the reference's ``_TRITON_LAST_DISPATCH`` / ``_TRITON_LAST_SCAN_DISPATCH``,
+    which its tests assert (``tests/test_scan.py:423``, ``tests/test_model.py:465``). Stub modules
+    stand for ``mamba3.ops`` and ``mamba3.model``."""
+    import types
+    ref_ops = types.ModuleType("stub_ops")
+    ref_ops._TRITON_LAST_DISPATCH = False
+    ref_ops._TRITON_LAST_SCAN_DISPATCH = False
+    ref_model = types.ModuleType("stub_model")
+    monkeypatch.setattr(hooks, "_FLAG_TARGETS", [])
+    hooks.bind(ref_ops, ref_model)
+    hooks.bind(ref_ops, ref_model)  # binding twice keeps one flag target
+    assert hooks._FLAG_TARGETS == [ref_ops]
+    assert ref_ops._fused_chunk_scan is hooks.fused_chunk_scan
+    assert ref_ops.fused_step is hooks.fused_step and ref_model.fused_step is hooks.fused_step
+
+    monkeypatch.setattr(hooks, "_on_rocm", lambda *t: True)
+    monkeypatch.setattr(ops, "mamba3_scan", lambda *a, **k: ("y", "s"))
+    monkeypatch.setattr(ops, "fused_step", lambda *a, **k: ("o", "c"))
+    with torch.inference_mode():
+        assert ref_ops._fused_chunk_scan(**_scan_inputs()) == ("y", "s")
+        assert ref_ops._TRITON_LAST_SCAN_DISPATCH and not ref_ops._TRITON_LAST_DISPATCH
+        assert ref_model.fused_step(**_step_inputs()) == ("o", "c")
+        assert ref_ops._TRITON_LAST_DISPATCH
+        monkeypatch.setenv("MAMBA3_DISABLE_TRITON", "1")
+        assert ref_ops._fused_chunk_scan(**_scan_inputs()) is None
+        assert ref_model.fused_step(**_step_inputs()) is None
+    assert not ref_ops._TRITON_LAST_SCAN_DISPATCH and not ref_ops._TRITON_LAST_DISPATCH

@@ -188,3 +188,42 @@ def test_set_chunk_sizes_and_compile_are_accepted():
         model.set_chunk_sizes(inference=0)
     assert model.compile() is model
     assert model.compile_layers() is model
+
+
+def test_graph_decoder_validate_sees_moved_storage():
+    """The graph decoder's staleness check compares what the reference's
+    ``_parameter_signature`` compares (``model.py:763-774``): identity, version, data pointer,
+    device, dtype and shape. ``p.data = ...`` and ``Module.to(dtype)`` keep the Parameter object
+    and its version, so a check of those two alone passes a graph that reads freed weights.
+    The decoder's capture needs a GPU; its check does not, so it runs here on a decoder whose
+    capture record is taken from a CPU model."""
+    from mamba3_amd.model import _HipGraphDecoder, _storage_signature
+
+    def decoder_for(model):
+        dec = object.__new__(_HipGraphDecoder)
+        dec.model = model
+        dec._captured = [_storage_signature(w) for w in model.parameters()]
+        return dec
+
+    model = Mamba3(16, d_state=8, depth=1)
+    dec = decoder_for(model)
+    dec.validate()
+    weight = model.layers[0].mixer.in_proj.weight
+    version = weight._version
+    weight.data = weight.data.clone()
+    assert weight._version == version
+    with pytest.raises(RuntimeError, match="recreate"):
+        dec.validate()
+
+    dec = decoder_for(model)
+    before = list(model.parameters())
+    model.to(torch.bfloat16)
+    assert all(a is b for a, b in zip(before, model.parameters()))
+    with pytest.raises(RuntimeError, match="recreate"):
+        dec.validate()
+
+    dec = decoder_for(model)
+    with torch.no_grad():
+        model.layers[0].mixer.D.add_(1)
+    with pytest.raises(RuntimeError, match="recreate"):
+        dec.validate()

@@ -59,12 +59,17 @@ def test_noalloc_scan_equals_the_workspace_scan(case):
             gc.disable()
             try:
                 before = torch.cuda.memory_allocated(DEV)
+                free_before = torch.cuda.mem_get_info(DEV)[0]
                 _noalloc(call)
                 torch.cuda.synchronize()
                 after = torch.cuda.memory_allocated(DEV)
+                free_after = torch.cuda.mem_get_info(DEV)[0]
             finally:
                 gc.enable()
+            # torch's allocator count, and the driver's free memory, which also sees a
+            # hipMalloc made outside torch
             assert after == before
+            assert free_after == free_before
             got = _outputs(call)
         print(f"noalloc d={d_model} R={rank} {dtype} B={batch} L={length}: workspace "
               f"{0 if call._keep[-1] is None else call._keep[-1].numel()} bytes", flush=True)
