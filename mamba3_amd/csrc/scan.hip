@@ -141,6 +141,11 @@ struct ScanGeom {
   int64_t ws_norm, ws_ang, ws_sc;
   int L4, tok, nsub, scw;
   int ws_bytes;  // workspace bytes when below 2^31 (the projection form addresses it in 32 bits)
+  // the model's SISO 16-bit shape (scan16_kernel): the RMS-normalized q / k rows [B][L][2][N]
+  // in the activation dtype, after the regions above (byte offset, -1: absent) and their bytes
+  // when below 2^31 (read through a buffer resource of their own)
+  int64_t ws_qk;
+  int qk_bytes;
   // projection form (the full-shape kernel): q, k, value, gate, dt, a, trap are slices of one
   // projection row; byte offsets of each slice from `proj`, the batch / token strides and the
   // group / rank / head strides of the slices, in bytes
@@ -908,8 +913,8 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
              gi * x.stride[2] + r * x.stride[3] + (in ? 8 * l16 : 0);
     };
     float ss[kNormRows];
+    uint32_t w8[kNormRows][Words<T>::W8];
     if (g.vec_qk) {
-      uint32_t w8[kNormRows][Words<T>::W8];
 #pragma unroll
       for (int k = 0; k < kNormRows; ++k) {
         // rows past the end re-read the last row; their sums are not stored
@@ -954,6 +959,31 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
       if (l16 == 0 && row < nrows) {
         ws[g.ws_norm + static_cast<int64_t>(row)] =
             1.f / sqrtf(ss[k] / static_cast<float>(N) + a.norm_eps);
+      }
+    }
+    if constexpr (sizeof(T) == 2) {
+      if (g.ws_qk >= 0 && g.vec_qk) {
+        // the model's SISO shape (N = 128, one group and rank, vector rows): the normalized rows
+        // themselves, rnd(x * factor * rnd(w)) (model.py:48-55: F.rms_norm with the weight in the
+        // activation dtype, the result in it), rows (token, q | k) at N elements each
+        float wn[2][8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          wn[0][i] = rnd<T>(ldx(a.q_norm_w.ptr, a.q_norm_w.dtype, (8 * l16 + i) * a.q_norm_w.stride[0]));
+          wn[1][i] = rnd<T>(ldx(a.k_norm_w.ptr, a.k_norm_w.dtype, (8 * l16 + i) * a.k_norm_w.stride[0]));
+        }
+        char* qk = reinterpret_cast<char*>(ws) + g.ws_qk;
+#pragma unroll
+        for (int k = 0; k < kNormRows; ++k) {
+          const int row = row0 + 16 * k;
+          if (row >= nrows) continue;
+          const float f = 1.f / sqrtf(ss[k] / static_cast<float>(N) + a.norm_eps);
+          const int which = row & 1;
+          float x[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[i] = raw_get<T>(w8[k], i) * f * wn[which][i];
+          st_row8<T>(reinterpret_cast<T*>(qk + (static_cast<int64_t>(row) * N + 8 * l16) * 2), x);
+        }
       }
     }
   } else if (blk < nb_norm + nb_ang) {
@@ -1966,6 +1996,527 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 }
 
 
+// ------------------------------------------------------------ 16-wave SISO scan
+
+// scan16_kernel<T, SO>: the model's SISO shape in projection form (rank 1, N = 128, P = 64,
+// 32 angles, one group, 16-bit activations; forwards or backwards) with 1024 threads, so that
+// four waves share each SIMD to hide one another's LDS, MFMA and transcendental latency. Per
+// 64-token sub-chunk, three intervals between workgroup barriers:
+//   A  staging (every wave): token qt's q / k (RMSNorm, bias, rotation; waves 0-7 the rotated
+//      columns 0-63, waves 8-15 columns 64-127) -> Qs, Ks; token vt's value / gate -> VR, ZR
+//      and the carry's scaled values -> VS; the state, rounded -> Sb; the side block and angle
+//      tile of the next sub-chunk -> LDS;
+//   B  waves 0-9 one causal score tile each (Sc^T = K Q^T) and its decay weights W -> WS;
+//      every wave the carry products of its two state tiles; the next sub-chunk's global loads
+//      are issued here;
+//   C  wave w the output tile (row tile w / 4, P tile w % 4): intra V^T W^T from WS, inter
+//      rnd(S) Q^T, epilogue, store; waves 0-7, whose row tiles 0 and 1 have the shortest intra
+//      products, also the phases of the next sub-chunk (a long dependent chain per wave).
+// Same mathematics and rounding points as scan_kernel<T, 1, true> (whose header lists them).
+
+constexpr int k16Threads = 1024;
+
+// LDS layout, 16-bit elements unless noted. The strides and swizzles make every access pattern
+// of the kernel conflict-free under the measured gfx950 LDS behaviour: 16-byte reads of 16 rows
+// at one 16-byte chunk (the MFMA operands) with 288-byte rows or an XOR swizzle of 256-byte rows;
+// 8-byte accesses (stores, transposing reads) 32 lanes at a time over 64 banks of 4 bytes, so
+// the 32 lanes' 8-byte pieces must cover 256 distinct bytes.
+//   Qs, Ks  [64 tokens][144]: 288-byte rows
+//   Sb      [64 p][128]: 256-byte rows, 16-byte chunk c of row p at c ^ (p % 16) (sb_off)
+//   VR, ZR, VS [64 tokens][64]: 128-byte rows, 32-byte pair and chunk half swizzled (v_off)
+//   WS      [64 t][80]: 160-byte rows
+struct Lay16 {
+  static constexpr int ROWS = 64, LQ = kNPad + 16, LS = kNPad, LV = kPPad, LW = kPPad + 16, ES = 2;
+  static constexpr int QS = 0;
+  static constexpr int KS = QS + ROWS * LQ * ES;
+  static constexpr int VR = KS + ROWS * LQ * ES;
+  static constexpr int ZR = VR + ROWS * LV * ES;
+  static constexpr int VS = ZR + ROWS * LV * ES;
+  static constexpr int SB = VS + ROWS * LV * ES;
+  static constexpr int WS = SB + kPPad * LS * ES;  // decay weights [t][s'] (s' permuted, below)
+  static constexpr int FB = WS + ROWS * LW * ES;
+  // floats from FB: two side blocks (scalar blocks), the angle tile, two cos / sin tables, the
+  // phase block sum and carry per angle
+  static constexpr int SCB = 5 * ROWS + 8, SC0 = 0;
+  static constexpr int ANG = SC0 + 2 * SCB;
+  static constexpr int CST = 2 * kSMax + 4, CSB = ROWS * CST;
+  static constexpr int CS0 = ANG + ROWS * kSMax, PBASE = CS0 + 2 * CSB, POFF = PBASE + kSMax;
+  static constexpr int BYTES = FB + 4 * (POFF + kSMax);
+};
+static_assert(Lay16::BYTES <= 160 * 1024, "scan16 LDS layout exceeds 160 KiB");
+static_assert(Lay16::FB % 16 == 0 && Lay16::WS % 16 == 0 && Lay16::SB % 16 == 0 &&
+              (Lay16::ANG * 4) % 16 == 0 && (Lay16::CS0 * 4) % 16 == 0, "alignment");
+
+// Element offset of column `col` of state row p in Sb (16-byte chunks XOR-swizzled by row).
+__device__ __forceinline__ int sb_off(int p, int col) {
+  return p * Lay16::LS + 8 * ((col >> 3) ^ (p & 15)) + (col & 7);
+}
+
+// Element offset of column `col` of token row r in VR, ZR, VS: the row's 32-byte pair
+// (col / 16) XOR (r / 2) % 4 and the chunk within it flipped by (r / 8) % 2. Eight consecutive
+// rows then place one pair in eight distinct 32-byte bank groups (the transposing reads), and
+// sixteen consecutive rows one chunk in sixteen distinct 16-byte groups (the epilogue reads).
+__device__ __forceinline__ int v_off(int r, int col) {
+  const int c = col >> 3;
+  const int pc = 2 * ((c >> 1) ^ ((r >> 1) & 3)) + ((c & 1) ^ ((r >> 3) & 1));
+  return r * Lay16::LV + 8 * pc + (col & 7);
+}
+
+// The causal score tiles (row tile it, column tile sj <= it) of waves 0-9: the diagonal tiles,
+// whose decay weights take the most arithmetic, on waves 0-3 (one per SIMD).
+__device__ __forceinline__ void score_tile16(int w, int& it, int& sj) {
+  // w: 0 1 2 3 | 4 5 6 7 8 9  ->  (0,0) (1,1) (2,2) (3,3) | (1,0) (2,0) (2,1) (3,0) (3,1) (3,2)
+  const int k = w - 4;
+  it = w < 4 ? w : (k < 1 ? 1 : (k < 3 ? 2 : 3));
+  sj = w < 4 ? w : (k < 1 ? 0 : (k < 3 ? k - 1 : k - 3));
+}
+
+template <typename T, bool SO>
+__global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a,
+                                                            const ScanGeom g,
+                                                            const float* __restrict__ prep) {
+  using M = Mma<T>;
+  using Ly = Lay16;
+  using SB_ = ScBlk<64>;
+  constexpr int TOK = 64, LQ = Ly::LQ, LW = Ly::LW, CST = Ly::CST, ES = 2, S = kSMax;
+  constexpr int PG = 16, TPL = 4;  // phase: 16 lanes per angle, 4 tokens per lane (waves 0-7)
+  const int H = a.heads, L = a.length;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+
+  int bid = blockIdx.x;
+  if (g.xcd_map) {
+    const int per = gridDim.x >> 3;
+    bid = (bid & 7) * per + (bid >> 3);
+  }
+  const int b = bid / H, h = bid - b * H;
+
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  T* Qs = lds_t<T>(smem, Ly::QS);
+  T* Ks = lds_t<T>(smem, Ly::KS);
+  T* VR = lds_t<T>(smem, Ly::VR);
+  T* ZR = lds_t<T>(smem, Ly::ZR);
+  T* VS = lds_t<T>(smem, Ly::VS);
+  T* Sb = lds_t<T>(smem, Ly::SB);
+  T* WS = lds_t<T>(smem, Ly::WS);
+  float* F = lds_t<float>(smem, Ly::FB);
+  const float Dh = ldx(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
+
+  // ---- lane roles
+  // q / k: tokens qt and qt + 32, columns n0 .. n0+3 (waves 0-7: the rotated columns 0-63)
+  const bool rot = w < 8;
+  const int qt = (tid & 511) >> 4;
+  const int n0 = 64 * (tid >> 9) + 4 * (tid & 15);
+  // value / gate: token vt, columns p0 .. p0+3
+  const int vt = tid >> 4, p0 = 4 * (tid & 15);
+  // phase (waves 0-7): angle ps, tokens TPL pg .. TPL pg + 3
+  const int ps = tid >> 4, pg = tid & 15;
+  const bool ph_wave = w < 8;
+  // state tiles (ni, pj), k = 0, 1: ni = w / 2, pj = 2 (w % 2) + k; lane holds
+  // n = 16 ni + 4 lg + i, p = 16 pj + l16 (S^T in MFMA accumulator layout)
+  const int sni = w >> 1, spj0 = 2 * (w & 1);
+
+  for (int s = tid; s < S; s += k16Threads) {
+    F[Ly::PBASE + s] = 0.f;
+    F[Ly::POFF + s] = a.initial_phase.ptr != nullptr
+                          ? static_cast<const float*>(a.initial_phase.ptr)
+                                [b * a.initial_phase.stride[0] + h * a.initial_phase.stride[1] +
+                                 s * a.initial_phase.stride[2]]
+                          : 0.f;
+  }
+
+  // rounded biases of the lane's 4 columns (the rows come normalized from prep)
+  float bq[4], bk[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = n0 + i;
+    bq[i] = rnd<T>(ldx(a.q_bias.ptr, a.q_bias.dtype, h * a.q_bias.stride[0] + n));
+    bk[i] = rnd<T>(ldx(a.k_bias.ptr, a.k_bias.dtype, h * a.k_bias.stride[0] + n));
+  }
+
+  f4 st[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    st[k] = zero4();
+    if (a.initial_state.ptr != nullptr) {
+      const int p = 16 * (spj0 + k) + l16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = 16 * sni + 4 * lg + i;
+        st[k][i] = static_cast<const float*>(a.initial_state.ptr)
+            [b * a.initial_state.stride[0] + h * a.initial_state.stride[1] +
+             p * a.initial_state.stride[2] + n];
+      }
+    }
+  }
+  // Endpoint continuation (ops.py:681-686): S += dt_0 (1 - trap_0) v_prev k_prev^T.
+  if (a.initial_k.ptr != nullptr && L > 0) {
+    float dt0, adt0;
+    dt_adt(true, ldx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + h * a.dt.stride[2]),
+           ldx(a.a.ptr, a.a.dtype, b * a.a.stride[0] + h * a.a.stride[2]),
+           ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]), dt0, adt0);
+    const float tr0 = sigmoidf(ldx(a.trap.ptr, a.trap.dtype,
+                                   b * a.trap.stride[0] + h * a.trap.stride[2]));
+    const float c0 = dt0 * (1.f - tr0);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int p = 16 * (spj0 + k) + l16;
+      const float v0 = to_f(static_cast<const T*>(a.initial_value.ptr)
+                                [b * a.initial_value.stride[0] + h * a.initial_value.stride[1] + p]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = 16 * sni + 4 * lg + i;
+        const float k0 = to_f(static_cast<const T*>(a.initial_k.ptr)
+                                  [b * a.initial_k.stride[0] + h * a.initial_k.stride[1] + n]);
+        st[k][i] += c0 * (v0 * k0);
+      }
+    }
+  }
+
+  // ---- global reads: one buffer resource over the batch row of the projection (its extent
+  // ends at token L: rows past it read zero, stores past it are dropped) and one over the
+  // workspace; per-lane byte offsets at token 0
+  const int tok_b = g.tok_b;
+  const __amdgpu_buffer_rsrc_t rs_p =
+      make_rsrc(g.proj + b * g.proj_b, L * (tok_b < 0 ? -tok_b : tok_b));
+  const __amdgpu_buffer_rsrc_t rs_w = make_rsrc(prep, g.ws_bytes);
+  // the normalized q / k rows of batch row b (token stride 2 N elements, k after q; rows past
+  // token L read zero)
+  const __amdgpu_buffer_rsrc_t rs_qk =
+      make_rsrc(reinterpret_cast<const char*>(prep) + g.ws_qk + static_cast<int64_t>(b) * L * 4 * kNPad,
+                L * 4 * kNPad);
+  const int o_qk = qt * 4 * kNPad + n0 * ES;  // token qt (forward order), column n0 of q
+  const int o_vz = g.o_v + h * g.vz_h + vt * tok_b + p0 * ES, d_z = g.o_z - g.o_v;
+  const int nsub = g.nsub, scw = g.scw;
+  // side words (waves 0-3, one float pair per lane): the scalar block
+  const int q2 = 2 * tid;
+  const bool side_on = q2 < scw;
+  const int side_o =
+      side_on ? static_cast<int>(g.ws_sc + static_cast<int64_t>(b * H + h) * nsub * scw + q2) * 4
+              : 0;
+  const int side_s = scw * 4;
+  // angle words (waves 0-7): 4 tokens of one angle each, in the tile order [TOK / 4][S][4]
+  const int ang_o = static_cast<int>(g.ws_ang + static_cast<int64_t>(b) * g.L4 * S * 4 + 4 * tid) * 4;
+  const int ang_s = (TOK / 4) * S * 16;
+  const bool ang_on = tid < TOK * S / 4;
+
+  float* fph = a.final_phase.ptr != nullptr && ph_wave
+                   ? static_cast<float*>(a.final_phase.ptr) + b * a.final_phase.stride[0] +
+                         h * a.final_phase.stride[1] + ps * a.final_phase.stride[2]
+                   : nullptr;
+  float* fblk = a.block_phase.ptr != nullptr && ph_wave
+                    ? static_cast<float*>(a.block_phase.ptr) + b * a.block_phase.stride[0] +
+                          h * a.block_phase.stride[1] + ps * a.block_phase.stride[3]
+                    : nullptr;
+  const int64_t blk_stride = a.block_phase.stride[2];
+  const __amdgpu_buffer_rsrc_t rs_o =
+      make_rsrc(const_cast<char*>(g.out_base) + b * g.out_b, L * (g.out_t < 0 ? -g.out_t : g.out_t));
+  const int out_t = g.out_t, o_out = h * g.out_h + g.out_o0;
+
+  // q / k words: [token qt, qt + 32][q, k] 4 elements each
+  uint32_t rq[2][2], rk[2][2], rv[2], rz[2];
+  float2 side = make_float2(0.f, 0.f);
+  float4 ang = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto load_qk = [&](int t0) {
+    // the rows are stored in the call's token order: logical token t at row t
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int o = o_qk + (t0 + 32 * j) * 4 * kNPad;
+      bload_words<2>(rq[j], rs_qk, o);
+      bload_words<2>(rk[j], rs_qk, o + 2 * kNPad);
+    }
+  };
+  auto load_vz = [&](int t0) {
+    bload_words<2>(rv, rs_p, o_vz + t0 * tok_b);
+    bload_words<2>(rz, rs_p, o_vz + t0 * tok_b + d_z);
+  };
+  auto load_side = [&](int c) {
+    if (w < 4) {
+      const u32x2 v = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_w, side_o + c * side_s, 0, 0));
+      side = make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+    }
+    if (w < 8) {
+      const u32x4 v = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_w, ang_o + c * ang_s, 0, 0));
+      ang = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                        __uint_as_float(v[3]));
+    }
+  };
+  float* ANG = F + Ly::ANG;
+  // angle tile slot of 4-token group gq and angle s (XOR-keyed by the group's phase lane)
+  auto ang_slot = [&](int gq, int s) { return gq * kSMax + (s ^ gq); };
+  auto put_side = [&](int c) {
+    if (w < 4 && side_on) *reinterpret_cast<float2*>(F + Ly::SC0 + (c & 1) * Ly::SCB + q2) = side;
+    if (w < 8 && ang_on) {
+      const int gq = tid / S;
+      *reinterpret_cast<float4*>(ANG + 4 * ang_slot(gq, tid - gq * S)) = ang;
+    }
+  };
+  auto scb = [&](int c) { return F + Ly::SC0 + (c & 1) * Ly::SCB; };
+  auto csb = [&](int c) { return F + Ly::CS0 + (c & 1) * Ly::CSB; };
+  auto phases = [&](int c) {
+    // phases of sub-chunk c (waves 0-7), from the angle tile and the dt of its side block
+    if (ph_wave && c < nsub) {
+      float pa[TPL];
+      const float4 v = *reinterpret_cast<const float4*>(ANG + 4 * ang_slot(pg, ps));
+      pa[0] = v.x;
+      pa[1] = v.y;
+      pa[2] = v.z;
+      pa[3] = v.w;
+      phase_stage<PG, TPL, CST, true, false>(csb(c), ps, F + Ly::PBASE + ps, F + Ly::POFF + ps,
+                                             scb(c) + SB_::DTV, c * TOK, L, pg, lane, true, pa,
+                                             fph, fblk, blk_stride);
+    }
+  };
+
+  // prologue: side block and angle tile of sub-chunk 0, its phases; the loads of 0 and 1
+  load_side(0);
+  load_qk(0);
+  load_vz(0);
+  put_side(0);
+  load_side(1);
+  __syncthreads();
+  phases(0);
+  __syncthreads();
+
+  float log_decay = 0.f;
+  for (int c = 0; c < nsub; ++c) {
+    const int t0 = c * TOK;
+    const float* SC = scb(c);
+    const float* CSt = csb(c);
+
+    // ---- A: staging
+    if (c + 1 < nsub) put_side(c + 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      // token tt: q = q^ + bias, k = k^ + bias, rotated (pairs (n0, n0+1), (n0+2, n0+3), angles
+      // n0 / 2 and n0 / 2 + 1, adjacent in the cos / sin table row)
+      const int tt = qt + 32 * j;
+      f4 q, k;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        q[i] = raw_get<T>(rq[j], i) + bq[i];
+        k[i] = raw_get<T>(rk[j], i) + bk[i];
+      }
+      if (rot) {
+        const f4 cv = *reinterpret_cast<const f4*>(CSt + tt * CST + 2 * cs_col<true>(n0 >> 1, tt));
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          const float cc = cv[2 * pp], ss = cv[2 * pp + 1];
+          const float q0 = q[2 * pp], q1 = q[2 * pp + 1];
+          const float k0 = k[2 * pp], k1 = k[2 * pp + 1];
+          q[2 * pp] = fmaf(q0, cc, -(q1 * ss));
+          q[2 * pp + 1] = fmaf(q0, ss, q1 * cc);
+          k[2 * pp] = fmaf(k0, cc, -(k1 * ss));
+          k[2 * pp + 1] = fmaf(k0, ss, k1 * cc);
+        }
+      }
+      if constexpr (!SO) st_quad<T>(Qs + tt * LQ + n0, q);
+      st_quad<T>(Ks + tt * LQ + n0, k);
+    }
+    {
+      // value / gate of token vt: VR / ZR as loaded, VS = v * scale * exp(cum_last - cum)
+      const float ev = SC[SB_::SCL + vt] * __expf(SC[SB_::CL] - SC[SB_::CUM + vt]);
+      f4 sv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = raw_get<T>(rv, i) * ev;
+      st_quad<T>(VS + v_off(vt, p0), sv);
+      if constexpr (!SO) {
+        *reinterpret_cast<u32x2*>(VR + v_off(vt, p0)) = (u32x2){rv[0], rv[1]};
+        *reinterpret_cast<u32x2*>(ZR + v_off(vt, p0)) = (u32x2){rz[0], rz[1]};
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      if constexpr (!SO) st_quad<T>(Sb + sb_off(16 * (spj0 + k) + l16, 16 * sni + 4 * lg), st[k]);
+    }
+    {
+      const float ecl = SC[SB_::ECL];
+      log_decay += SC[SB_::CL];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[k][i] *= ecl;
+      }
+    }
+    __syncthreads();
+
+    // ---- B: score tiles and decay weights, carry products, phases of c + 1; loads of c + 1
+    __builtin_amdgcn_sched_barrier(0);
+    load_qk(t0 + TOK);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!SO && w < 10) {
+      int it, sj;
+      score_tile16(w, it, sj);
+      const int tq = 16 * it + l16;
+      f4 acc = zero4();
+      // (four waves per SIMD hide the operand latency: one k-step's operands in registers at a
+      // time keeps the kernel within 128 VGPRs)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
+            Ks + (16 * sj + l16) * LQ + 32 * kk + 8 * lg);
+        const typename M::v8 bv =
+            *reinterpret_cast<const typename M::v8*>(Qs + tq * LQ + 32 * kk + 8 * lg);
+        acc = M::mma(av, bv, acc);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const float cum_t = SC[SB_::CUM + tq];
+      f4 wv;
+      if (sj < it) {
+        // d = exp(cum_t - cend) * (scale_s exp(cend - cum_s)), both factors <= 1
+        const float at = __expf(cum_t - SC[SB_::CEND + sj]);
+        const f4 bs = *reinterpret_cast<const f4*>(SC + SB_::BSC + 16 * sj + 4 * lg);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wv[i] = acc[i] * (at * bs[i]);
+      } else {
+        const float gam_t = SC[SB_::GAM + tq];
+        int tq_m = tq;
+        __asm__ volatile("" : "+v"(tq_m));
+        const f4 c4 = *reinterpret_cast<const f4*>(SC + SB_::CUM + 16 * sj + 4 * lg);
+        const f4 s4 = *reinterpret_cast<const f4*>(SC + SB_::SCL + 16 * sj + 4 * lg);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int ts = 16 * sj + 4 * lg + i;
+          const float lower = s4[i] * __expf(cum_t - c4[i]);
+          const float d = tq_m > ts ? lower : (tq_m == ts ? gam_t : 0.f);
+          wv[i] = acc[i] * d;
+        }
+      }
+      // W[t][s], s = 16 sj + 4 lg + i, at s' = 32 (sj / 2) + 8 lg + 4 (sj % 2) + i: the order of
+      // the intra product's K axis (below)
+      st_quad<T>(WS + tq * LW + 32 * (sj >> 1) + 8 * lg + 4 * (sj & 1), wv);
+    }
+    {
+      // carry: S^T(ni, pj) += K~^T V~ over the 64 tokens. A: 8 tokens of column n from the
+      // row-major Ks by two transposing reads (in each 16-lane group, lane 4a + b receives
+      // element b of the 8-byte vectors of lanes a, a + 4, a + 8, a + 12); B: the same from VS.
+      // The K axis of k-step kk, lane group lg: tokens kk + 4 lg + j (slots j) and
+      // kk + 16 + 4 lg + j (slots 4 + j), so the 32 lanes of each read take 8 consecutive tokens
+      const int xr = l16 >> 2, xc = 4 * (l16 & 3);
+#pragma unroll
+      for (int kk = 0; kk < TOK; kk += 32) {
+        const int r0 = kk + 4 * lg + xr;
+        const T* k0 = Ks + r0 * LQ + 16 * sni + xc;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(k0));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(k0 + 16 * LQ));
+        const typename M::v8 av = __builtin_bit_cast(
+            typename M::v8, (i16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const int vc = 16 * (spj0 + k) + xc;
+          const i16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(VS + v_off(r0, vc)));
+          const i16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(VS + v_off(r0 + 16, vc)));
+          const typename M::v8 bv = __builtin_bit_cast(
+              typename M::v8,
+              (i16x8){vlo[0], vlo[1], vlo[2], vlo[3], vhi[0], vhi[1], vhi[2], vhi[3]});
+          st[k] = M::mma(av, bv, st[k]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_vz(t0 + TOK);
+    __builtin_amdgcn_sched_barrier(0);
+    load_side(c + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+
+    // ---- C: output tile (row tile it, P tile pj)
+    if constexpr (!SO) {
+      const int it = w >> 2, pj = w & 3;
+      const int tq = 16 * it + l16;
+      f4 yi = zero4(), ye = zero4();
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        if (2 * m > it) continue;
+        // intra: V^T W^T over tokens s = 32 m + 4 lg + i and 32 m + 16 + 4 lg + i
+        const int vrow = 32 * m + 4 * lg + (l16 >> 2), vcol = 16 * pj + 4 * (l16 & 3);
+        const typename M::v4 b0 = __builtin_bit_cast(
+            typename M::v4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                (__attribute__((address_space(3))) i16x4*)(VR + v_off(vrow, vcol))));
+        const typename M::v4 b1 = __builtin_bit_cast(
+            typename M::v4,
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4*)(VR + v_off(vrow + 16, vcol))));
+        typename M::v8 av, bv = *reinterpret_cast<const typename M::v8*>(WS + tq * LW + 32 * m + 8 * lg);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          av[i] = b0[i];
+          av[4 + i] = b1[i];
+          if (2 * m + 1 > it) bv[4 + i] = from_f<T>(0.f);  // column tile 2m + 1 lies above it
+        }
+        yi = M::mma(av, bv, yi);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        // inter: rnd(S) Q^T
+        const typename M::v8 av = *reinterpret_cast<const typename M::v8*>(
+            Sb + sb_off(16 * pj + l16, 32 * kk + 8 * lg));
+        const typename M::v8 bv =
+            *reinterpret_cast<const typename M::v8*>(Qs + tq * LQ + 32 * kk + 8 * lg);
+        ye = M::mma(av, bv, ye);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // epilogue: token tq, columns pb .. pb+3
+      const int pb = 16 * pj + 4 * lg;
+      const float ecum_t = __expf(SC[SB_::CUM + tq]);
+      const typename M::v4 v4 = *reinterpret_cast<const typename M::v4*>(VR + v_off(tq, pb));
+      const typename M::v4 z4 = *reinterpret_cast<const typename M::v4*>(ZR + v_off(tq, pb));
+      f4 y;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        y[i] = (fmaf(ye[i], ecum_t, yi[i]) + Dh * to_f(v4[i])) * silu_fast(to_f(z4[i]));
+      }
+      bstore_quad<T>(y, rs_o, (tq * out_t + o_out + pb * ES) +
+                                  __builtin_amdgcn_readfirstlane(t0 * out_t));
+    }
+    // phases of c + 1: its angle tile and side block came to LDS in A; its cos / sin table is
+    // the other buffer than the one A read
+    phases(c + 1);
+    __syncthreads();
+  }
+
+  // ---- final k: the biased, rotated k of token L-1, still in Ks from the last sub-chunk
+  if (a.final_k.ptr != nullptr && L > 0) {
+    const int tl = (L - 1) - (nsub - 1) * TOK;
+    for (int n = tid; n < kNPad; n += k16Threads) {
+      static_cast<T*>(a.final_k.ptr)[b * a.final_k.stride[0] + h * a.final_k.stride[1] + n] =
+          Ks[tl * LQ + n];
+    }
+  }
+  if (a.final_decay.ptr != nullptr && tid == 0) {
+    static_cast<float*>(a.final_decay.ptr)[b * a.final_decay.stride[0] +
+                                           h * a.final_decay.stride[1]] = log_decay;
+  }
+  if (a.block_phase.ptr != nullptr && L > 0) {
+    for (int i = tid; i < S; i += k16Threads) {
+      static_cast<float*>(a.block_phase.ptr)[b * a.block_phase.stride[0] +
+                                             h * a.block_phase.stride[1] +
+                                             ((L - 1) >> 6) * a.block_phase.stride[2] +
+                                             i * a.block_phase.stride[3]] = F[Ly::PBASE + i];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int p = 16 * (spj0 + k) + l16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = 16 * sni + 4 * lg + i;
+      static_cast<float*>(a.final_state.ptr)[b * a.final_state.stride[0] +
+                                             h * a.final_state.stride[1] +
+                                             p * a.final_state.stride[2] + n] = st[k][i];
+    }
+  }
+}
+
 // ------------------------------------------------------------ segmented scan (composition)
 
 // A sequence split into G equal segments is scanned twice (pass 1: every segment from a zero
@@ -2320,6 +2871,16 @@ __global__ __launch_bounds__(kCompThreads) void gather_kernel(const m3_scan_args
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// A call scan16_kernel may serve (the projection form is checked later, at launch): the model's
+// SISO shape in a 16-bit activation dtype with RMSNorm, head biases, raw dt and angle phases.
+static bool siso16_candidate(const m3_scan_args& a) {
+  return (a.act_dtype == M3_BF16 || a.act_dtype == M3_F16) && a.rank == 1 && a.groups == 1 &&
+         a.d_state == kNPad && a.head_dim == kPPad && a.num_angles == kSMax &&
+         a.q_norm_w.ptr != nullptr && a.k_norm_w.ptr != nullptr && a.q_bias.ptr != nullptr &&
+         a.k_bias.ptr != nullptr && a.raw_dt != 0 && a.phase_mode == M3_PHASE_ANGLES &&
+         a.mimo_rotation == 0;
+}
+
 // Prep workspace regions (floats, each 16-byte aligned) and the sub-chunk geometry; returns the
 // workspace size in bytes.
 static size_t ws_layout(const m3_scan_args& a, ScanGeom& g) {
@@ -2345,6 +2906,15 @@ static size_t ws_layout(const m3_scan_args& a, ScanGeom& g) {
   const int64_t bytes = off * static_cast<int64_t>(sizeof(float));
   // the projection form's 32-bit offsets run up to two sub-chunk strides past the end
   g.ws_bytes = bytes < (int64_t{1} << 30) ? static_cast<int>(bytes) : -1;
+  g.ws_qk = -1;
+  g.qk_bytes = -1;
+  if (siso16_candidate(a)) {
+    // 256-byte aligned; the rows' 32-bit offsets run up to two sub-chunks past the end
+    const int64_t qk = batch * len * 2 * a.d_state * 2;
+    g.ws_qk = (bytes + 255) / 256 * 256;
+    g.qk_bytes = qk < (int64_t{1} << 30) ? static_cast<int>(qk) : -1;
+    return static_cast<size_t>(g.ws_qk + qk);
+  }
   return static_cast<size_t>(bytes);
 }
 
@@ -2511,6 +3081,23 @@ static int launch_kernel(const m3_scan_args& a, const ScanGeom& g, const float* 
   return check_launch("m3_scan_fwd");
 }
 
+template <typename T, bool SO>
+static int launch_kernel16(const m3_scan_args& a, const ScanGeom& g, const float* prep,
+                           dim3 grid, hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan16_kernel<T, SO>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Lay16::BYTES);
+    if (e != hipSuccess) {
+      return fail(M3_ELAUNCH, "m3_scan_fwd: hipFuncSetAttribute: %s", hipGetErrorString(e));
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((scan16_kernel<T, SO>), grid, dim3(k16Threads), Lay16::BYTES, stream, a, g,
+                     prep);
+  return check_launch("m3_scan_fwd");
+}
+
 // One pass: the prep kernel (unless `run_prep` is false: its workspace already holds this
 // geometry's results) and the scan kernel.
 // `state_only`: the caller needs only the end state, decay, last k and phase block sums (the
@@ -2548,6 +3135,15 @@ static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep,
   }
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kThreads);
   if (full_shape(a, g, R) && prep != nullptr) {
+    if constexpr (sizeof(T) == 2 && R == 1) {
+      // the model's SISO shape: the 16-wave kernel (prep wrote the normalized rows: vector rows)
+      if (g.ws_qk < 0 || g.qk_bytes <= 0) {
+        return fail(M3_EUNSUPPORTED, "m3_scan_fwd: %lld normalized q / k rows exceed 2^30 bytes",
+                    static_cast<long long>(a.batch) * a.length);
+      }
+      if (state_only) return launch_kernel16<T, true>(a, g, prep, grid, stream);
+      return launch_kernel16<T, false>(a, g, prep, grid, stream);
+    }
     if constexpr (sizeof(T) == 2) {
       if (state_only) return launch_kernel<T, R, true, true>(a, g, prep, grid, block, stream);
     }
