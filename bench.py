@@ -2,11 +2,13 @@
 
 Headline workload: the SISO prefill scan of
 ``Mamba3(d_model=1024, d_state=128, depth=1, mimo_rank=1)`` on ``x [8, 8192, 1024]`` under
-bf16 autocast, seed 1. A step is one ``m3_scan_fwd`` call (its per-token prep kernel: B/C
-RMSNorm factors and pi tanh(angle); then the scan kernel: dt / A, bounded phase, bias,
-rotation, chunked SSD, D skip, SiLU gate) over the whole batch, with its input, the
-``in_proj`` output, already resident in HBM, timed with HIP events on the launch stream.
-``value`` is prefill tokens/s of that call. Also reported, in the same JSON line:
+bf16 autocast, seed 1. A step is one ``m3_scan_fwd`` call (its prep kernel: the RMS-normalized
+B/C rows, pi tanh(angle), the per-(head, sub-chunk) dt / A / trapezoid scalars; then the
+16-wave scan kernel: bounded phase, bias, rotation, chunked SSD, D skip, SiLU gate) over the
+whole batch, with its input, the ``in_proj`` output, already resident in HBM, timed with HIP
+events on the launch stream. The timed calls follow the forward line's 30 passes, which run
+the same kernels, so they are timed at the GPU's sustained-load clock. ``value`` is prefill
+tokens/s of that call. Also reported, in the same JSON line:
 
 * ``roofline``: the call against the HBM roof (its binding roof: arithmetic intensity
   ~201 flop/B at the reference chunk is below the MI355X ridge of ~315 flop/B), ``traffic``
@@ -41,6 +43,7 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 METRIC = "prefill tok/s (B=8,L=8K) + decode tok/s (B=256) on 1 GPU; % MFMA/HBM roofline"
+FWD_ITERS = 30  # timed config-2 forward passes (run before the headline scan calls)
 
 
 def prefill_bytes(batch, length, d_model, proj):
@@ -113,18 +116,21 @@ def bench_prefill(prep, steps, warmup, log, copy_probe=False):
     model, x, mixer, call = prep["model"], prep["x"], prep["mixer"], prep["call"]
     batch, length = x.shape[:2]
     with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        # The forward line first: its passes run the same scan kernels (and the projection
+        # GEMMs) for ~40 ms, so the timed scan calls below find the GPU at the clocks of
+        # sustained prefill load. Right after a change of workload the shader clock runs at
+        # 1.8-2.2 GHz for the first tens of dispatches before it settles at 2.4 GHz (per-dispatch
+        # GRBM_GUI_ACTIVE / duration), and a 5-call warmup alone would time that ramp.
+        def forward():
+            model(x)
+
+        for _ in range(2):
+            forward()
+        t_fwd = _events_time(forward, FWD_ITERS)
         for _ in range(warmup):
             call.launch()
         assert ops._HIP_LAST_SCAN_DISPATCH
         t_scan = _events_time(call.launch, steps)
-
-        def forward():
-            model(x)
-
-        for _ in range(max(1, warmup // 2)):
-            forward()
-        fwd_iters = max(3, steps // 4)
-        t_fwd = _events_time(forward, fwd_iters)
     if copy_probe:
         # a plain 1 GiB device copy: the reference reading for the PMC byte counters
         src_buf = torch.ones(256 * 1024 * 1024, device=dev)
@@ -148,14 +154,14 @@ def bench_prefill(prep, steps, warmup, log, copy_probe=False):
         roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                       frac=round(gbs / HBM_PEAK_GBS, 4), traffic=traffic,
                       kernel="m3_scan_fwd: m3::prep_kernel<__bf16> + "
-                             "m3::scan_kernel<__bf16, 1, true>",
+                             "m3::scan16_kernel<__bf16, false>",
                       us_per_launch=round(per_launch * 1e6, 2), bytes_per_launch=nbytes),
         roofline_mfma=dict(bound="mfma", achieved=round(tflops, 1), peak=MFMA_BF16_PEAK_TFLOPS,
                            unit="TFLOP/s", frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                            flops_per_launch_at_c256=flops_ref,
                            flops_per_launch_at_kernel_chunk64=flops_own),
-        forward=dict(tok_s=round(tokens / (t_fwd / fwd_iters), 1),
-                     ms_per_forward=round(t_fwd / fwd_iters * 1e3, 3)),
+        forward=dict(tok_s=round(tokens / (t_fwd / FWD_ITERS), 1),
+                     ms_per_forward=round(t_fwd / FWD_ITERS * 1e3, 3), iters=FWD_ITERS),
         proj=proj_size)
 
 
@@ -199,33 +205,39 @@ def bench_decode(batch, steps, log, rank=1, prefix=2048):
         end.record()
         torch.cuda.synchronize()
         t = start.elapsed_time(end) / 1000.0
-        # the step kernel alone, layer-0 shapes, in place on the decoder's cache
-        proj = mixer.in_proj(model.layers[0].norm(nxt[0]))
-        layer_cache = decoder.cache[0]
+        # the step kernel alone, in place on the decoder's caches: step i updates layer
+        # i % depth with that layer's projection, so the timed steps stream every layer's state
+        # in turn, as the decoder does (24 distinct caches; at B = 64 they are 24 x 134 MB,
+        # beyond the 256 MB Infinity Cache, so the bytes come from HBM)
+        depth = len(model.layers)
+        projs = [layer.mixer.in_proj(layer.norm(nxt[0])) for layer in model.layers]
+        mixers = [layer.mixer for layer in model.layers]
+        iters = 2 * depth
 
-        def step_kernel():
-            ops.step_projection(proj, mixer, layer_cache, inplace=True)
+        def step_kernel(i):
+            ops.step_projection(projs[i % depth], mixers[i % depth], decoder.cache[i % depth],
+                                inplace=True)
 
-        iters = 20
         if batch * mixer.nheads >= 8192:
             # eager calls: the launch is GPU-bound at this size (at 1024 pairs a 10 us kernel
             # would time the host's launch rate instead)
-            for _ in range(3):
-                step_kernel()
-            t_k = _events_time(step_kernel, iters) / iters
+            for i in range(3):
+                step_kernel(i)
+            count = iter(range(10 ** 9))
+            t_k = _events_time(lambda: step_kernel(next(count)), iters) / iters
         else:
             # small batches: eager calls would time the host, so a captured graph of
             # back-to-back steps, as the decoder runs them
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
-                for _ in range(3):
-                    step_kernel()
+                for i in range(3):
+                    step_kernel(i)
             torch.cuda.current_stream().wait_stream(side)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                for _ in range(iters):
-                    step_kernel()
+                for i in range(iters):
+                    step_kernel(i)
             graph.replay()
             torch.cuda.synchronize()
             t_k = _events_time(graph.replay, 5) / (5 * iters)
@@ -303,7 +315,9 @@ def bench_prefill_config(name, d_model, depth, rank, causal, shape, seed, log, i
 
 def bench_chunk_state(log, batch=8, heads=32, width=256, rank=1, n=128, p=64):
     """The standalone per-chunk state update (``m3_chunk_state``) at config 2's chunk shape:
-    one chunk of ``width`` tokens for every (batch, head), bf16 k / values, FP32 state."""
+    one chunk of ``width`` tokens for every (batch, head), bf16 k / values, FP32 state. The
+    timed calls replay one ~42 MB input set, which stays in the 256 MB Infinity Cache: the
+    line reports cache-resident bandwidth (``resident``), not an HBM roof."""
     from mamba3_amd import ops
 
     dev = torch.device("cuda:0")
@@ -332,8 +346,8 @@ def bench_chunk_state(log, batch=8, heads=32, width=256, rank=1, n=128, p=64):
               + 2 * batch * heads * p * n * 4)
     gbs = nbytes / t / 1e9
     log(f"chunk_state B={batch} H={heads} W={width}: {t * 1e6:.2f} us, {gbs:.0f} GB/s")
-    return dict(us=round(t * 1e6, 2), bytes=nbytes, bound="hbm", achieved=round(gbs, 1),
-                peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
+    return dict(us=round(t * 1e6, 2), bytes=nbytes, achieved=round(gbs, 1), unit="GB/s",
+                resident="infinity cache (one 42 MB input set replayed)",
                 traffic=_traffic_from_profile(
                     os.path.join(ROOT, "profiles", "chunk_state_config2_pmc.txt")),
                 kernel="m3::chunk_state_mma_kernel<__bf16>",
@@ -529,8 +543,8 @@ def bench_cpu_decode(log, batch=256, steps=3):
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # 50 warmup calls: a kernel trace shows the scan's clock-bound duration settling only after
-    # about 50 back-to-back calls (490-570 us over the first 10, 436-450 us from call 50 on)
+    # The headline call's timed steps follow the forward line's 30 passes (same kernels), so a
+    # few warmup calls suffice; 50 are the default
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--decode-batch", type=int, default=256)
@@ -542,12 +556,12 @@ def main() -> None:
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the default extra lines (configs 3 and 5, decode R=4 B=256, "
-                         "R=1 B=64 and R=1 B=1)")
+                    help="skip the default extra lines (configs 3, 5 and 5 long, decode R=4 "
+                         "B=256, R=1 B=64 and R=1 B=1)")
     ap.add_argument("--extra", action="store_true",
-                    help="also measure config 5 long, config 4 at more B and R, the chunk-state "
-                         "update and the hook boundaries")
-    ap.add_argument("--extra-only", choices=("config3", "config5", "config5_long", "decode",
+                    help="also measure config 4 at more B and R, the chunk-state update and "
+                         "the hook boundaries")
+    ap.add_argument("--extra-only", choices=("config3", "config5", "decode",
                                              "chunk_state", "hook", "hook_step"),
                     help="with --extra: measure only this one of the extra configurations")
     ap.add_argument("--copy-probe", action="store_true",
@@ -563,20 +577,22 @@ def main() -> None:
     def log(msg):
         print(msg, file=sys.stderr, flush=True)
 
-    # The headline call is prepared first. The default extra lines (BASELINE configs 3 and 5
-    # and three more decode points) run next, and the headline call is timed right after them:
-    # its kernels then run at the clocks of sustained load, as in a serving or prefill loop,
-    # not in the clock ramp of the first tens of launches after an idle GPU.
+    # The headline call is prepared first. The default extra lines (5 and 5
+    # long and three more decode points) run next, then the config-2 forward line, and the
+    # headline scan calls are timed right after it: they then run at the clocks of sustained
+    # load of the same kernels, as in a prefill loop, not in the clock ramp that follows a
+    # change of workload.
     prep = prepare_prefill()
     extra = {}
     if not args.no_extra:
-        # the sustained prefill load (config 3) last, right before the headline
         if not args.no_decode:
             extra["config4_decode_r4_b256"] = bench_decode(256, args.decode_steps, log, rank=4)
             extra["config4_decode_r1_b64"] = bench_decode(64, args.decode_steps, log, rank=1)
             extra["config4_decode_r1_b1"] = bench_decode(1, args.decode_steps, log, rank=1)
         extra["config5_bidir_16x2048"] = bench_prefill_config(
             "config 5", 768, 12, 1, False, (16, 2048, 768), 4, log)
+        extra["config5_bidir_1x65536"] = bench_prefill_config(
+            "config 5 long", 768, 12, 1, False, (1, 65536, 768), 4, log, iters=2)
         extra["config3_mimo_prefill"] = bench_prefill_config(
             "config 3", 1024, 4, 4, True, (8, 4096, 1024), 2, log)
     pre = bench_prefill(prep, args.steps, args.warmup, log, copy_probe=args.copy_probe)
@@ -591,8 +607,6 @@ def main() -> None:
                 "config 3", 1024, 4, 4, True, (8, 4096, 1024), 2, log)),
             "config5_bidir_16x2048": ("config5", lambda: bench_prefill_config(
                 "config 5", 768, 12, 1, False, (16, 2048, 768), 4, log)),
-            "config5_bidir_1x65536": ("config5_long", lambda: bench_prefill_config(
-                "config 5 long", 768, 12, 1, False, (1, 65536, 768), 4, log, iters=2)),
             "config4_decode": ("decode", lambda: [
                 bench_decode(b, args.decode_steps, log, rank=r)
                 for b, r in ((64, 4), (1, 4), (32, 1), (16, 1))]),
