@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "../../include/mamba3_hip.h"
+#include "m3_math.h"
 
 namespace m3 {
 
@@ -166,9 +167,10 @@ __device__ __forceinline__ void dt_adt(bool raw, float dt_in, float a_in, float 
   }
 }
 
-// fmod(pi * tanh(angle) * dt, 2 pi) (model.py:225-230).
+// fmod(pi * tanh(angle) * dt, 2 pi) (model.py:225-230); m3_fmod_2pi is fmodf's exact result
+// without its general reduction loop.
 __device__ __forceinline__ float phase_inc(float angle, float dt) {
-  return fmodf(__fmul_rn(__fmul_rn(kPi, tanhf(angle)), dt), kTwoPi);
+  return m3_fmod_2pi(__fmul_rn(__fmul_rn(kPi, tanhf(angle)), dt));
 }
 
 // ---------------------------------------------------------------- error reporting (host)

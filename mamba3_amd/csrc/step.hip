@@ -531,9 +531,11 @@ __global__ __launch_bounds__(32 * 64 / RPT) void step128_kernel(const m3_step_ar
 
   // per-(b, h) scalars
   float dt, adt;
-  dt_adt(raw_dt, dt_in, a_in, dtb_in, dt, adt);
-  const float trap = sigmoidf(trap_in);
-  const float alpha = expf(adt);
+  // the scan's forms (hardware exp / log / reciprocal, a few ulp): the per-(b, h) scalars head
+  // the prologue's dependent chain
+  dt_adt_fast(raw_dt, dt_in, a_in, dtb_in, dt, adt);
+  const float trap = sigmoid_fast(trap_in);
+  const float alpha = __expf(adt);
   const float beta = (1.f - trap) * dt * alpha;
   const float gamma = trap * dt;
 
@@ -859,9 +861,11 @@ __global__ __launch_bounds__(256) void step_mma_kernel(const m3_step_args a) {
 
   // per-(b, h) scalars
   float dt, adt;
-  dt_adt(raw_dt, dt_in, a_in, dtb_in, dt, adt);
-  const float trap = sigmoidf(trap_in);
-  const float alpha = expf(adt);
+  // the scan's forms (hardware exp / log / reciprocal, a few ulp): the per-(b, h) scalars head
+  // the prologue's dependent chain
+  dt_adt_fast(raw_dt, dt_in, a_in, dtb_in, dt, adt);
+  const float trap = sigmoid_fast(trap_in);
+  const float alpha = __expf(adt);
   const float beta = (1.f - trap) * dt * alpha;
   const float gamma = trap * dt;
 
