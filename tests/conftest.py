@@ -23,7 +23,7 @@ def golden(name: str) -> dict[str, np.ndarray]:
 
 
 def bf16_parity(tag: str, got, want16, want32, *, slack: float = 1.25,
-                max_slack: float | None = None, min_inside: float = 0.98, rtol: float = 2e-2,
+                max_slack: float | None = None, min_inside: float = 0.985, rtol: float = 2e-2,
                 atol: float = 2e-2, elementwise: bool = True) -> None:
     """The 16-bit parity bar, for results the reference's own 16-bit path cannot itself
     reproduce to an elementwise 2e-2 of FP32.
@@ -36,14 +36,17 @@ def bf16_parity(tag: str, got, want16, want32, *, slack: float = 1.25,
 
     * in norm and in max abs error against the FP32 result;
     * elementwise: it misses the bar ``atol + rtol |x|`` of the FP32 result on at most
-      ``slack`` times as many elements as the reference's 16-bit path does (plus 0.1% of the
-      elements, for small samples);
+      ``slack`` times as many elements as the reference's 16-bit path does, plus the counting
+      noise of a small count (4 sqrt(count) + 8: 6 reference misses allow 25, 166k allow 209k);
 
     and, with ``elementwise`` (single passes, where two 16-bit paths stay close), that it
     agrees with the reference's 16-bit result to the same bar on at least ``min_inside`` of the
     elements, with no element further from it than the reference's own largest 16-bit error
-    plus the bar. (Long 16-bit chains such as a 24-layer decode drift from FP32 and from each
-    other by more than the bar; there only the accuracy checks apply.)
+    plus the bar. Callers set ``min_inside`` a little below the fraction the HIP path reaches on
+    their inputs (the default, 98.5%, covers the small random-input scans, which reach 98.8% and
+    more); a regression that doubles the disagreement then fails. (Long 16-bit chains such as a
+    24-layer decode drift from FP32 and from each other by more than the bar; there only the
+    accuracy checks apply.)
     """
     import torch
 
@@ -63,7 +66,7 @@ def bf16_parity(tag: str, got, want16, want32, *, slack: float = 1.25,
     assert n_got <= slack * n_ref + 1e-30, f"{tag}: norm error {n_got:.3e} > {slack} x {n_ref:.3e}"
     ms = slack if max_slack is None else max_slack
     assert m_got <= ms * m_ref + 1e-30, f"{tag}: max error {m_got:.3e} > {ms} x {m_ref:.3e}"
-    assert out_got <= slack * out_ref + 1e-3 * got.numel(), (
+    assert out_got <= slack * out_ref + 4.0 * out_ref ** 0.5 + 8, (
         f"{tag}: {out_got} elements outside the bar of FP32, the reference {out_ref}")
     if elementwise:
         assert inside >= min_inside, f"{tag}: only {inside:.4f} of elements within the bar"

@@ -115,9 +115,12 @@ def test_config2_bf16_scan_full():
         want32, want32_cache = op.mixer_scan(params, "layers.0.mixer.", proj_cpu.float(), dims)
         want32_forward = op.model_forward(params, x[[0, 7]], dims)
     print(f"config 2 bf16 oracle: {time.time() - t0:.1f} s", flush=True)
-    bf16_parity("config 2 bf16 scan output", mixed, want, want32)
-    bf16_parity("config 2 bf16 final state", state, want_cache[1], want32_cache[1])
-    bf16_parity("config 2 bf16 forward rows 0, 7", got_forward, want_forward, want32_forward)
+    # min_inside: measured 99.785%, 100% and 100% within 2e-2 of the 16-bit oracle
+    bf16_parity("config 2 bf16 scan output", mixed, want, want32, min_inside=0.997)
+    bf16_parity("config 2 bf16 final state", state, want_cache[1], want32_cache[1],
+                min_inside=0.9995)
+    bf16_parity("config 2 bf16 forward rows 0, 7", got_forward, want_forward, want32_forward,
+                min_inside=0.999)
 
 
 # ------------------------------------------------------------------------------- config 3
@@ -139,7 +142,8 @@ def test_config3_forward_rows(bf16):
                 want = op.model_forward(params, x[[0, 7]], dims)
     print(f"config 3 oracle (bf16={bf16}): {time.time() - t0:.1f} s", flush=True)
     if bf16:
-        bf16_parity("config 3 bf16 forward rows 0, 7", got, want, want32)
+        bf16_parity("config 3 bf16 forward rows 0, 7", got, want, want32,
+                    min_inside=0.999)  # measured 99.963%
     else:
         _close("config 3 fp32 forward rows 0, 7", got, want32, F32)
 
@@ -166,8 +170,10 @@ def test_config3_bf16_scan_full_and_batch_independent(monkeypatch):
         want, want_cache = op.mixer_scan(params, "layers.0.mixer.", proj_cpu, dims)
     with torch.inference_mode():
         want32, want32_cache = op.mixer_scan(params, "layers.0.mixer.", proj_cpu.float(), dims)
-    bf16_parity("config 3 bf16 scan output", mixed, want, want32)
-    bf16_parity("config 3 bf16 final state", state, want_cache[1], want32_cache[1])
+    # min_inside: measured 99.916% and 100%
+    bf16_parity("config 3 bf16 scan output", mixed, want, want32, min_inside=0.9985)
+    bf16_parity("config 3 bf16 final state", state, want_cache[1], want32_cache[1],
+                min_inside=0.9995)
 
 
 # ------------------------------------------------------------------------------- config 4
@@ -306,11 +312,35 @@ def test_config5_bidirectional_full_batch(bf16):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
+def test_config5_full_depth(bf16):
+    """Config 5 at full depth: all 12 layers of ``Mamba3(768, 128, 12, causal=False)`` on
+    x[16, 2048, 768] on the GPU (the bench's workload); rows 0 and 15 against the oracle (rows
+    are independent), FP32 to 1e-4, 16-bit under the 16-bit bar against the FP32 oracle."""
+    model, params, dims = _build(768, 128, 12, 1, seed=4, causal=False)
+    x = torch.randn(16, 2048, 768)
+    with torch.inference_mode(), _ctx("cuda", bf16):
+        got = model.to(DEV)(x.to(DEV))[[0, 15]].cpu()
+    rows = x[[0, 15]]
+    t0 = time.time()
+    with torch.inference_mode():
+        want32 = op.model_forward(params, rows, dims, causal=False)
+        if bf16:
+            with _ctx("cpu", True):
+                want = op.model_forward(params, rows, dims, causal=False)
+    print(f"config 5 12-layer oracle (bf16={bf16}): {time.time() - t0:.1f} s", flush=True)
+    if bf16:
+        bf16_parity("config 5 12 layers bf16 rows 0, 15", got, want, want32,
+                    min_inside=0.993)  # measured 99.478%
+    else:
+        _close("config 5 12 layers fp32 rows 0, 15", got, want32, F32)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
 def test_config5_long_single_sequence(bf16):
-    """Config 5 long: the first layer of ``Mamba3(768, 128, 12, causal=False)`` on
+    """Config 5 long: the first two layers of ``Mamba3(768, 128, 12, causal=False)`` on
     x[1, 65536, 768]: 24 (b, h) pairs, so each direction's scan is split into segments
     (pass 1, composition, pass 2) over about 1000 64-token blocks; against the oracle."""
-    model, params, dims = _build(768, 128, 12, 1, seed=4, causal=False, keep_layers=1)
+    model, params, dims = _build(768, 128, 12, 1, seed=4, causal=False, keep_layers=2)
     x = torch.randn(1, 65536, 768)
     with torch.inference_mode(), _ctx("cuda", bf16):
         got = model.to(DEV)(x.to(DEV)).cpu()

@@ -255,7 +255,8 @@ def test_graph_decoder_bf16_weights_against_oracle(rank, batch):
                 outs.append(o)
         chains[dtype] = (torch.cat(outs, 1), c)
     (w16, c16), (w32, c32) = chains[torch.bfloat16], chains[torch.float32]
-    bf16_parity(f"graph bf16 R={rank} outputs", got, w16, w32)
+    bf16_parity(f"graph bf16 R={rank} outputs", got, w16, w32,
+                min_inside=0.999)  # measured 99.993% and more
     bf16_parity(f"graph bf16 R={rank} states", torch.stack([c[1] for c in decoder.cache]),
                 torch.stack([c[1] for c in c16]), torch.stack([c[1] for c in c32]),
                 elementwise=False, max_slack=1.5)
