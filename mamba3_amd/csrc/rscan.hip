@@ -14,9 +14,13 @@
 // bounded phase is the reference's: increments summed within 64-token blocks counted from the
 // call's first token, fmod-reduced, on an fmod-reduced carry (model.py:215-256).
 //
-// The FP32 state lives in LDS; each token costs a few barriers, so this path runs at a fraction
-// of the MFMA kernel's speed: it exists for coverage of the shapes, not for the BASELINE
-// workloads (all of which take the MFMA kernel).
+// The FP32 state lives in LDS when it fits there with the per-token vectors (160 KiB); a larger
+// one (d_state 1024 at head_dim 64 is 256 KiB) is updated in place in final_state, where each
+// element has one owning thread for the whole call, so it needs no barrier: the first token reads
+// initial_state, every later one the row it wrote (through L2). Ranks above 8 add readout passes
+// over the updated rows in groups of 8. Each token costs a few barriers, so this path runs at a
+// fraction of the MFMA kernel's speed: it exists for coverage of the shapes, not for the
+// BASELINE workloads (all of which take the MFMA kernel).
 #include <algorithm>
 
 #include "m3_common.hpp"
@@ -26,11 +30,12 @@
 namespace m3 {
 
 constexpr int kRThreads = 256;
-constexpr int kRMaxR = 8;  // ranks up to 8
+constexpr int kRGroup = 8;  // ranks per readout pass (accumulators per thread)
+constexpr size_t kRMaxLds = 160 * 1024;
 
-// LDS floats the kernel needs for a shape.
-static size_t rscan_lds_floats(int R, int N, int P, int S) {
-  return static_cast<size_t>(P) * N            // state
+// LDS floats the kernel needs for a shape (with the state, or with the state in final_state).
+static size_t rscan_lds_floats(int R, int N, int P, int S, bool state_in_lds = true) {
+  return (state_in_lds ? static_cast<size_t>(P) * N : 0)  // state
          + 7 * static_cast<size_t>(R) * N      // q, k, previous k, biases, two scratch copies
          + 2 * static_cast<size_t>(N)          // norm weights
          + 7 * static_cast<size_t>(R) * P      // v, previous v, z, mimo x / z / out, readout
@@ -39,7 +44,14 @@ static size_t rscan_lds_floats(int R, int N, int P, int S) {
          + 2 * static_cast<size_t>(R) + 8;     // RMSNorm factors, per-token scalars
 }
 
-size_t rscan_lds_bytes(int R, int N, int P, int S) { return 4 * rscan_lds_floats(R, N, P, S); }
+size_t rscan_lds_bytes(int R, int N, int P, int S, bool state_in_lds = true) {
+  return 4 * rscan_lds_floats(R, N, P, S, state_in_lds);
+}
+
+// Whether the state stays in LDS (else it is updated in final_state).
+static bool rscan_state_in_lds(const m3_scan_args& a) {
+  return rscan_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles) <= kRMaxLds;
+}
 
 template <typename T>
 __device__ __forceinline__ float ld_el(const m3_tensor& t, int64_t i) {
@@ -48,7 +60,8 @@ __device__ __forceinline__ float ld_el(const m3_tensor& t, int64_t i) {
 
 template <typename T>
 __global__ __launch_bounds__(kRThreads) void rscan_kernel(const m3_scan_args a, int tpr,
-                                                          const m3_tensor value_out) {
+                                                          const m3_tensor value_out,
+                                                          int state_in_lds) {
   const int H = a.heads, N = a.d_state, P = a.head_dim, S = a.num_angles, R = a.rank;
   const int L = a.length;
   const int bh = blockIdx.x;
@@ -63,8 +76,16 @@ __global__ __launch_bounds__(kRThreads) void rscan_kernel(const m3_scan_args a, 
   const int RN = R * N, RP = R * P;
 
   extern __shared__ float lds[];
-  float* st = lds;           // [P][N] FP32 state
-  float* qx = st + P * N;    // [R][N] this token's q (normed, biased, then rotated)
+  // [P][N] FP32 state, row stride sps: in LDS, or this (b, h)'s rows of final_state
+  float* st = state_in_lds ? lds
+                           : static_cast<float*>(a.final_state.ptr) + b * a.final_state.stride[0] +
+                                 h * a.final_state.stride[1];
+  const int64_t sps = state_in_lds ? N : a.final_state.stride[2];
+  const float* st0 = a.initial_state.ptr == nullptr
+                         ? nullptr
+                         : static_cast<const float*>(a.initial_state.ptr) +
+                               b * a.initial_state.stride[0] + h * a.initial_state.stride[1];
+  float* qx = state_in_lds ? lds + P * N : lds;  // [R][N] this token's q (normed, biased, rotated)
   float* kx = qx + RN;       // [R][N] this token's k
   float* pk = kx + RN;       // [R][N] the previous token's rotated k
   float* bq = pk + RN;       // [R][N] C_bias of this head (rounded), 0 without biases
@@ -130,13 +151,11 @@ __global__ __launch_bounds__(kRThreads) void rscan_kernel(const m3_scan_args a, 
                                                 h * a.initial_value.stride[1] + p)
                 : 0.f;
   }
-  for (int i = tid; i < P * N; i += kRThreads) {
-    const int p = i / N, n = i - p * N;
-    st[i] = a.initial_state.ptr != nullptr
-                ? static_cast<const float*>(a.initial_state.ptr)
-                      [b * a.initial_state.stride[0] + h * a.initial_state.stride[1] +
-                       p * a.initial_state.stride[2] + n]
-                : 0.f;
+  if (state_in_lds) {
+    for (int i = tid; i < P * N; i += kRThreads) {
+      const int p = i / N, n = i - p * N;
+      st[i] = st0 != nullptr ? st0[p * a.initial_state.stride[2] + n] : 0.f;
+    }
   }
   for (int s = tid; s < S; s += kRThreads) {
     blk[s] = 0.f;
@@ -279,42 +298,72 @@ __global__ __launch_bounds__(kRThreads) void rscan_kernel(const m3_scan_args a, 
     }
     __syncthreads();
 
-    // ---- (4) state update and readout: tpr consecutive lanes share a row p
+    // ---- (4) state update and readout: tpr consecutive lanes share a row p. The thread that
+    // updates element (p, n) is the same at every token (the state in final_state relies on it).
     const float alpha = expf(adt);
     const float beta = (1.f - trap) * dt * alpha;
     const float gamma = trap * dt;
     const int rows_per_pass = kRThreads / tpr;
     const int lane_in_row = tid & (tpr - 1);
+    const bool first = !state_in_lds && t == 0;  // the state's previous value is initial_state
     for (int p0 = 0; p0 < P; p0 += rows_per_pass) {
       const int p = p0 + tid / tpr;
-      float part[kRMaxR];
+      float part[kRGroup];
 #pragma unroll
-      for (int r = 0; r < kRMaxR; ++r) part[r] = 0.f;
+      for (int r = 0; r < kRGroup; ++r) part[r] = 0.f;
       if (p < P) {
         for (int n = lane_in_row; n < N; n += tpr) {
           float po = 0.f, co = 0.f;
 #pragma unroll
-          for (int r = 0; r < kRMaxR; ++r) {
+          for (int r = 0; r < kRGroup; ++r) {
             if (r < R) {
               po = fmaf(pvr[r * P + p], pk[r * N + n], po);
               co = fmaf(vr[r * P + p], kx[r * N + n], co);
             }
           }
-          const float ns = alpha * st[p * N + n] + beta * po + gamma * co;
-          st[p * N + n] = ns;
+          for (int r = kRGroup; r < R; ++r) {
+            po = fmaf(pvr[r * P + p], pk[r * N + n], po);
+            co = fmaf(vr[r * P + p], kx[r * N + n], co);
+          }
+          const float old = first ? (st0 != nullptr ? st0[p * a.initial_state.stride[2] + n] : 0.f)
+                                  : st[p * sps + n];
+          const float ns = alpha * old + beta * po + gamma * co;
+          st[p * sps + n] = ns;
           const float nr = rnd<T>(ns);
 #pragma unroll
-          for (int r = 0; r < kRMaxR; ++r) {
+          for (int r = 0; r < kRGroup; ++r) {
             if (r < R) part[r] = fmaf(nr, qx[r * N + n], part[r]);
           }
         }
       }
 #pragma unroll
-      for (int r = 0; r < kRMaxR; ++r) {
+      for (int r = 0; r < kRGroup; ++r) {
         if (r < R) {
           float v = part[r];
           for (int o = tpr >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o);
           if (p < P && lane_in_row == 0) yp[r * P + p] = v;
+        }
+      }
+      // ranks beyond the first 8: further readout passes over the row this thread just wrote
+      for (int r0 = kRGroup; r0 < R; r0 += kRGroup) {
+#pragma unroll
+        for (int r = 0; r < kRGroup; ++r) part[r] = 0.f;
+        if (p < P) {
+          for (int n = lane_in_row; n < N; n += tpr) {
+            const float nr = rnd<T>(st[p * sps + n]);
+#pragma unroll
+            for (int r = 0; r < kRGroup; ++r) {
+              if (r0 + r < R) part[r] = fmaf(nr, qx[(r0 + r) * N + n], part[r]);
+            }
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < kRGroup; ++r) {
+          if (r0 + r < R) {
+            float v = part[r];
+            for (int o = tpr >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o);
+            if (p < P && lane_in_row == 0) yp[(r0 + r) * P + p] = v;
+          }
         }
       }
     }
@@ -335,12 +384,16 @@ __global__ __launch_bounds__(kRThreads) void rscan_kernel(const m3_scan_args a, 
     __syncthreads();
   }
 
-  // ---- final state, phase, k, decay
-  for (int i = tid; i < P * N; i += kRThreads) {
-    const int p = i / N, n = i - p * N;
-    static_cast<float*>(a.final_state.ptr)[b * a.final_state.stride[0] +
-                                           h * a.final_state.stride[1] +
-                                           p * a.final_state.stride[2] + n] = st[i];
+  // ---- final state (already in place when it lives in final_state, unless L = 0), phase, k,
+  // decay
+  if (state_in_lds || L == 0) {
+    for (int i = tid; i < P * N; i += kRThreads) {
+      const int p = i / N, n = i - p * N;
+      static_cast<float*>(a.final_state.ptr)[b * a.final_state.stride[0] +
+                                             h * a.final_state.stride[1] +
+                                             p * a.final_state.stride[2] + n] =
+          state_in_lds ? st[i] : (st0 != nullptr ? st0[p * a.initial_state.stride[2] + n] : 0.f);
+    }
   }
   if (a.final_phase.ptr != nullptr) {
     for (int s = tid; s < S; s += kRThreads) {
@@ -370,16 +423,18 @@ __global__ __launch_bounds__(kRThreads) void rscan_kernel(const m3_scan_args a, 
 }
 
 bool rscan_fits(const m3_scan_args& a) {
-  return a.rank <= kRMaxR && rscan_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles) <= 160 * 1024;
+  return a.rank >= 1 &&
+         rscan_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles, false) <= kRMaxLds;
 }
 
 template <typename T>
 static int launch_rscan_t(const m3_scan_args& a, const m3_tensor& value_out, hipStream_t stream) {
-  const size_t lds = rscan_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles);
+  const bool in_lds = rscan_state_in_lds(a);
+  const size_t lds = rscan_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles, in_lds);
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&rscan_kernel<T>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kRMaxLds);
     if (e != hipSuccess) {
       return fail(M3_ELAUNCH, "recurrent scan: hipFuncSetAttribute: %s", hipGetErrorString(e));
     }
@@ -389,7 +444,7 @@ static int launch_rscan_t(const m3_scan_args& a, const m3_tensor& value_out, hip
   int tpr = 64;
   while (tpr > 1 && kRThreads / tpr < std::min(a.head_dim, kRThreads)) tpr >>= 1;
   hipLaunchKernelGGL((rscan_kernel<T>), dim3(static_cast<unsigned>(a.batch) * a.heads),
-                     dim3(kRThreads), lds, stream, a, tpr, value_out);
+                     dim3(kRThreads), lds, stream, a, tpr, value_out, in_lds ? 1 : 0);
   return check_launch("recurrent scan");
 }
 

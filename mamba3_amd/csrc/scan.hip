@@ -3394,8 +3394,8 @@ static int validate_scan(const m3_scan_args& a) {
   if (a.d_state < 4) return fail(M3_EUNSUPPORTED, "m3_scan_fwd: d_state %d < 4", a.d_state);
   if (!tiled_shape(a) && !rscan_fits(a)) {
     return fail(M3_EUNSUPPORTED,
-                "m3_scan_fwd: rank %d, d_state %d, head_dim %d, %d angles: above 8 ranks or "
-                "160 KiB of LDS for the recurrent scan",
+                "m3_scan_fwd: rank %d, d_state %d, head_dim %d, %d angles: the recurrent scan's "
+                "per-token q / k / value vectors exceed 160 KiB of LDS",
                 a.rank, a.d_state, a.head_dim, a.num_angles);
   }
   if (!tiled_shape(a) && a.segments > 1) {

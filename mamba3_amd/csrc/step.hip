@@ -1174,8 +1174,8 @@ extern "C" int m3_step(const m3_step_args* args, hipStream_t stream) {
                       step_lds_bytes(a.rank, a.d_state, a.head_dim, a.num_angles) <= 64 * 1024;
   if (!native && !rscan_fits(step_as_scan(a))) {
     return fail(M3_EUNSUPPORTED,
-                "m3_step: rank %d, d_state %d, head_dim %d, %d angles: above 8 ranks or 160 KiB "
-                "of LDS",
+                "m3_step: rank %d, d_state %d, head_dim %d, %d angles: the recurrent step's "
+                "per-token q / k / value vectors exceed 160 KiB of LDS",
                 a.rank, a.d_state, a.head_dim, a.num_angles);
   }
   const int act = a.act_dtype;

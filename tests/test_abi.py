@@ -314,5 +314,10 @@ def test_recurrent_shapes_need_no_workspace(lib):
     assert lib.m3_scan_fwd(ctypes.byref(args(segments=4)), None) == 2
     assert b"segments" in lib.m3_last_error()
     assert lib.m3_scan_fwd(ctypes.byref(args(d_state=2, num_angles=0)), None) == 2
-    assert lib.m3_scan_fwd(ctypes.byref(args(rank=9, mimo_rotation=1)), None) == 2
+    # any rank: rank 9 passes the shape checks (and stops at the missing tensors); a per-token
+    # footprint beyond 160 KiB of LDS (7 x 64 x 96 floats of q / k rows alone) is refused
+    assert lib.m3_scan_fwd(ctypes.byref(args(rank=9, mimo_rotation=1)), None) == 1
+    assert b"required tensor is NULL" in lib.m3_last_error()
+    assert lib.m3_scan_fwd(ctypes.byref(args(rank=64, mimo_rotation=1)), None) == 2
+    assert b"160 KiB" in lib.m3_last_error()
 

@@ -319,9 +319,11 @@ def test_config1_parity():
 
 # Models whose shapes the MFMA scan does not tile (the recurrent scan), and whose decode step
 # runs on the step kernels (d_state 256) or as a one-token recurrent scan (d_state not a power
-# of 2, rank 3): forward, prefill and steps against the oracle.
+# of 2, rank 3; d_state 1024, whose 256 KiB state is updated in final_state instead of LDS;
+# rank 16, read out in two groups of 8): forward, prefill and steps against the oracle.
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("case", [(64, 256, 1, 1), (48, 96, 2, 1), (32, 8, 2, 3), (64, 64, 1, 6)])
+@pytest.mark.parametrize("case", [(64, 256, 1, 1), (48, 96, 2, 1), (32, 8, 2, 3), (64, 64, 1, 6),
+                                  (64, 1024, 1, 1), (64, 128, 1, 16)])
 def test_recurrent_shapes_match_oracle(case, bf16):
     d_model, d_state, depth, rank = case
     model, params, dims = _model(d_model, d_state, depth, rank, seed=30 + rank)
