@@ -135,6 +135,7 @@ template <int TOK> struct ScBlk {
 struct ScanGeom {
   int xcd_map;           // 1: map blocks so each XCD holds consecutive (b, h)
   int vec_qk, vec_vz;    // 1: q/k rows and v/z rows may be loaded with 16 / 8-byte vectors
+  int vec_nw;            // 1: both norm weights unit-stride and 8-byte aligned (4-element loads)
   // prep workspace, float offsets of its regions (-1: absent): RMSNorm factors [B][L][G*R][2]
   // (q, k), pi tanh(angle) [B][L4][S][4] (4 consecutive tokens of one angle together, L4 =
   // ceil(L / 4)), scalar blocks [B*H][nsub][scw] of `tok`-token sub-chunks
@@ -809,8 +810,9 @@ __device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, fl
 // within-chunk cumsum of adt by a wave scan, and the decay products the scan uses.
 template <int TOK, int TPT>
 __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __restrict__ o,
-                                             int h, int c, int lane, float dt_in, float a_in,
-                                             float tr_in, float dtn_in, float trn_in) {
+                                             int c, int lane, float dt_bias, float dt_in,
+                                             float a_in, float tr_in, float dtn_in,
+                                             float trn_in) {
   using B = ScBlk<TOK>;
   const int L = a.length;
   const int tb = c * TOK, t = tb + lane;
@@ -818,10 +820,6 @@ __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __res
   const bool tv = lane < wn;
   const bool nv = lane < TOK && t + 1 < L;
   const bool raw_dt = a.raw_dt != 0;
-  const float dt_bias =
-      raw_dt ? decode(ldraw(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]),
-                      a.dt_bias.dtype)
-             : 0.f;
   float dt = 0.f, adt = 0.f, tr = 0.f;
   if (tv) {
     dt_adt_fast(raw_dt, dt_in, a_in, dt_bias, dt, adt);
@@ -914,6 +912,17 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
     };
     float ss[kNormRows];
     uint32_t w8[kNormRows][Words<T>::W8];
+    // the normalized rows' weights for this lane's 8 columns, raw, issued with the rows (after
+    // the factor stores below they would be a second round trip)
+    const bool rows_out = sizeof(T) == 2 && g.ws_qk >= 0 && g.vec_qk;
+    const bool nw_vec = rows_out && g.vec_nw;
+    Raw4 nw_r[2][2] = {};
+    if (nw_vec) {
+      nw_r[0][0] = ldraw4(a.q_norm_w, 8 * l16);
+      nw_r[0][1] = ldraw4(a.q_norm_w, 8 * l16 + 4);
+      nw_r[1][0] = ldraw4(a.k_norm_w, 8 * l16);
+      nw_r[1][1] = ldraw4(a.k_norm_w, 8 * l16 + 4);
+    }
     if (g.vec_qk) {
 #pragma unroll
       for (int k = 0; k < kNormRows; ++k) {
@@ -962,15 +971,28 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
       }
     }
     if constexpr (sizeof(T) == 2) {
-      if (g.ws_qk >= 0 && g.vec_qk) {
+      if (rows_out) {
         // the model's SISO shape (N = 128, one group and rank, vector rows): the normalized rows
         // themselves, rnd(x * factor * rnd(w)) (model.py:48-55: F.rms_norm with the weight in the
         // activation dtype, the result in it), rows (token, q | k) at N elements each
         float wn[2][8];
+        if (nw_vec) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          wn[0][i] = rnd<T>(ldx(a.q_norm_w.ptr, a.q_norm_w.dtype, (8 * l16 + i) * a.q_norm_w.stride[0]));
-          wn[1][i] = rnd<T>(ldx(a.k_norm_w.ptr, a.k_norm_w.dtype, (8 * l16 + i) * a.k_norm_w.stride[0]));
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const f4 q4 = decode4(nw_r[0][h2], a.q_norm_w.dtype);
+            const f4 k4 = decode4(nw_r[1][h2], a.k_norm_w.dtype);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              wn[0][4 * h2 + e] = rnd<T>(q4[e]);
+              wn[1][4 * h2 + e] = rnd<T>(k4[e]);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            wn[0][i] = rnd<T>(ldx(a.q_norm_w.ptr, a.q_norm_w.dtype, (8 * l16 + i) * a.q_norm_w.stride[0]));
+            wn[1][i] = rnd<T>(ldx(a.k_norm_w.ptr, a.k_norm_w.dtype, (8 * l16 + i) * a.k_norm_w.stride[0]));
+          }
         }
         char* qk = reinterpret_cast<char*>(ws) + g.ws_qk;
 #pragma unroll
@@ -1026,6 +1048,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
     const int b = bc / g.nsub, c = bc - b * g.nsub;
     constexpr int HG = 32, NE = (TOK + 1) * HG, NIT = (NE + 255) / 256;
     __shared__ float s_in[3][TOK + 1][HG + 1];
+    __shared__ float s_db[HG];  // dt_bias of the group's heads
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const char* base_dt = static_cast<const char*>(offx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0]));
     const char* base_a = static_cast<const char*>(offx(a.a.ptr, a.a.dtype, b * a.a.stride[0]));
@@ -1038,6 +1061,12 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
       const int hn = min(HG, a.heads - h0);
       // raw loads of every element first (clamped to valid tokens / heads), then decode and store
       RawX rd[NIT], ra[NIT], rt[NIT];
+      // dt_bias with the batch (inside the per-head loop below, after its stores, each head's
+      // load would be a round trip of its own)
+      const RawX rdb = a.raw_dt != 0
+                           ? ldraw(a.dt_bias.ptr, a.dt_bias.dtype,
+                                   (h0 + min(tid & (HG - 1), hn - 1)) * a.dt_bias.stride[0])
+                           : RawX{0u, 0u};
 #pragma unroll
       for (int k = 0; k < NIT; ++k) {
         const int e = min(tid + 256 * k, NE - 1);
@@ -1057,12 +1086,13 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
           s_in[2][j][hh] = decode(rt[k], a.trap.dtype);
         }
       }
+      if (tid < HG) s_db[tid] = a.raw_dt != 0 ? decode(rdb, a.dt_bias.dtype) : 0.f;
       __syncthreads();
       for (int hh = w; hh < hn; hh += 4) {
         const int h = h0 + hh, j = min(lane, TOK - 1);
         scalar_block<TOK, TPT>(
-            a, ws + g.ws_sc + (static_cast<int64_t>(b * a.heads + h) * g.nsub + c) * g.scw, h, c,
-            lane, s_in[0][j][hh], s_in[1][j][hh], s_in[2][j][hh], s_in[0][TOK][hh],
+            a, ws + g.ws_sc + (static_cast<int64_t>(b * a.heads + h) * g.nsub + c) * g.scw, c,
+            lane, s_db[hh], s_in[0][j][hh], s_in[1][j][hh], s_in[2][j][hh], s_in[0][TOK][hh],
             s_in[2][TOK][hh]);
       }
       __syncthreads();
@@ -2933,6 +2963,10 @@ static ScanGeom make_geom(const m3_scan_args& a) {
     return true;
   };
   g.vec_qk = (a.d_state % 8 == 0) && vec_ok(a.q, 5, 16) && vec_ok(a.k, 5, 16);
+  auto nw_ok = [](const m3_tensor& t) {
+    return t.ptr != nullptr && t.stride[0] == 1 && reinterpret_cast<uintptr_t>(t.ptr) % 8 == 0;
+  };
+  g.vec_nw = (a.d_state % 8 == 0) && nw_ok(a.q_norm_w) && nw_ok(a.k_norm_w);
   const int vneed = es * 4;  // 4 elements per v / z load
   g.vec_vz = (a.head_dim % 4 == 0) && vec_ok(a.value, 4, vneed) && vec_ok(a.gate, 4, vneed);
   ws_layout(a, g);
