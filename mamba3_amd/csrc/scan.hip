@@ -142,9 +142,9 @@ struct ScanGeom {
   int64_t ws_norm, ws_ang, ws_sc;
   int L4, tok, nsub, scw;
   int ws_bytes;  // workspace bytes when below 2^31 (the projection form addresses it in 32 bits)
-  // the model's SISO 16-bit shape (scan16_kernel): the RMS-normalized q / k rows [B][L][2][N]
-  // in the activation dtype, after the regions above (byte offset, -1: absent) and their bytes
-  // when below 2^31 (read through a buffer resource of their own)
+  // the model's 16-bit shape at ranks 1 and 4 (scan16_kernel): the RMS-normalized q / k rows
+  // [B][L][R][2][N] in the activation dtype, after the regions above (byte offset, -1: absent)
+  // and their bytes when below 2^31 (read through a buffer resource of their own)
   int64_t ws_qk;
   int qk_bytes;
   // projection form (the full-shape kernel): q, k, value, gate, dt, a, trap are slices of one
@@ -972,7 +972,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
     }
     if constexpr (sizeof(T) == 2) {
       if (rows_out) {
-        // the model's SISO shape (N = 128, one group and rank, vector rows): the normalized rows
+        // the model's shape at ranks 1 and 4 (N = 128, one group, vector rows): the normalized rows
         // themselves, rnd(x * factor * rnd(w)) (model.py:48-55: F.rms_norm with the weight in the
         // activation dtype, the result in it), rows (token, q | k) at N elements each
         float wn[2][8];
@@ -2028,21 +2028,25 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const m3_scan_args a, co
 
 // ------------------------------------------------------------ 16-wave SISO scan
 
-// scan16_kernel<T, SO>: the model's SISO shape in projection form (rank 1, N = 128, P = 64,
+// scan16_kernel<T, R, SO>: the model's shape in projection form (ranks 1 and 4, N = 128, P = 64,
 // 32 angles, one group, 16-bit activations; forwards or backwards) with 1024 threads, so that
-// four waves share each SIMD to hide one another's LDS, MFMA and transcendental latency. Per
-// 64-token sub-chunk, three intervals between workgroup barriers:
-//   A  staging (every wave): token qt's q / k (RMSNorm, bias, rotation; waves 0-7 the rotated
-//      columns 0-63, waves 8-15 columns 64-127) -> Qs, Ks; token vt's value / gate -> VR, ZR
-//      and the carry's scaled values -> VS; the state, rounded -> Sb; the side block and angle
-//      tile of the next sub-chunk -> LDS;
+// four waves share each SIMD to hide one another's LDS, MFMA and transcendental latency. A
+// sub-chunk is 64 rows (token, rank), rank minor: 64 tokens at rank 1, 16 at rank 4, whose
+// decay weights, phases and scalars are per token and whose output sums the token's R rows
+// (times mimo_out). Per sub-chunk, three intervals between workgroup barriers:
+//   A  staging (every wave): row qt's q / k (bias and rotation on prep's normalized rows; waves
+//      0-7 the rotated columns, waves 8-15 the others) -> Qs, Ks; row vt's value / gate (times
+//      the rounded mimo_x / mimo_z at rank 4) -> VR, ZR and the carry's scaled values -> VS; the
+//      state, rounded -> Sb; the side block and angle tile of the next sub-chunk -> LDS;
 //   B  waves 0-9 one causal score tile each (Sc^T = K Q^T) and its decay weights W -> WS;
 //      every wave the carry products of its two state tiles; the next sub-chunk's global loads
 //      are issued here;
 //   C  wave w the output tile (row tile w / 4, P tile w % 4): intra V^T W^T from WS, inter
 //      rnd(S) Q^T, epilogue, store; waves 0-7, whose row tiles 0 and 1 have the shortest intra
 //      products, also the phases of the next sub-chunk (a long dependent chain per wave).
-// Same mathematics and rounding points as scan_kernel<T, 1, true> (whose header lists them).
+// Same mathematics and rounding points as scan_kernel<T, R, true> (whose header lists them), but
+// for q / k, which start from prep's rows rounded after the RMSNorm (the reference's rounding
+// point, model.py:48-55).
 
 constexpr int k16Threads = 1024;
 
@@ -2071,7 +2075,9 @@ struct Lay16 {
   static constexpr int ANG = SC0 + 2 * SCB;
   static constexpr int CST = 2 * kSMax + 4, CSB = ROWS * CST;
   static constexpr int CS0 = ANG + ROWS * kSMax, PBASE = CS0 + 2 * CSB, POFF = PBASE + kSMax;
-  static constexpr int BYTES = FB + 4 * (POFF + kSMax);
+  // rank 4: the rounded mimo_x, mimo_z and mimo_out [R][P]
+  static constexpr int MX = POFF + kSMax, MZ = MX + 4 * kPPad, MO = MZ + 4 * kPPad;
+  static constexpr int BYTES = FB + 4 * (MO + 4 * kPPad);
 };
 static_assert(Lay16::BYTES <= 160 * 1024, "scan16 LDS layout exceeds 160 KiB");
 static_assert(Lay16::FB % 16 == 0 && Lay16::WS % 16 == 0 && Lay16::SB % 16 == 0 &&
@@ -2101,15 +2107,18 @@ __device__ __forceinline__ void score_tile16(int w, int& it, int& sj) {
   sj = w < 4 ? w : (k < 1 ? 0 : (k < 3 ? k - 1 : k - 3));
 }
 
-template <typename T, bool SO>
+template <typename T, int R, bool SO>
 __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a,
                                                             const ScanGeom g,
                                                             const float* __restrict__ prep) {
+  static_assert(R == 1 || R == 4, "scan16_kernel: ranks 1 and 4");
   using M = Mma<T>;
   using Ly = Lay16;
-  using SB_ = ScBlk<64>;
-  constexpr int TOK = 64, LQ = Ly::LQ, LW = Ly::LW, CST = Ly::CST, ES = 2, S = kSMax;
-  constexpr int PG = 16, TPL = 4;  // phase: 16 lanes per angle, 4 tokens per lane (waves 0-7)
+  constexpr int TOK = 64 / R;  // tokens per 64-row sub-chunk (rows (token, rank), rank minor)
+  using SB_ = ScBlk<TOK>;
+  constexpr int LQ = Ly::LQ, LW = Ly::LW, CST = Ly::CST, ES = 2, S = kSMax;
+  // phase: 16 lanes per angle, TPL tokens per lane (waves 0-7)
+  constexpr int PG = 16, TPL = TOK / 16;
   const int H = a.heads, L = a.length;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2134,11 +2143,16 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
   const float Dh = ldx(a.D.ptr, a.D.dtype, h * a.D.stride[0]);
 
   // ---- lane roles
-  // q / k: tokens qt and qt + 32, columns n0 .. n0+3 (waves 0-7: the rotated columns 0-63)
+  // q / k: rows qt and qt + 32 (rank qr), four columns. Rank 1: n0 .. n0+3, waves 0-7 the
+  // rotated columns 0-63 (pairs (2j, 2j+1)). Rank 4 (the MIMO rotation pairs column n with
+  // n + 64, n < 32): waves 0-7 columns n0, n0+1, n0+64, n0+65 (n0 = 2 (tid % 16)), waves 8-15
+  // four of the unrotated columns 32-63 and 96-127.
   const bool rot = w < 8;
-  const int qt = (tid & 511) >> 4;
-  const int n0 = 64 * (tid >> 9) + 4 * (tid & 15);
-  // value / gate: token vt, columns p0 .. p0+3
+  const int qt = (tid & 511) >> 4, qr = qt & (R - 1);
+  const int n0 = R == 1 ? 64 * (tid >> 9) + 4 * (tid & 15)
+                        : (rot ? 2 * (tid & 15) : ((tid & 15) < 8 ? 32 : 64) + 4 * (tid & 15));
+  auto qcol = [&](int i) { return R > 1 && rot ? n0 + (i & 1) + 64 * (i >> 1) : n0 + i; };
+  // value / gate: row vt (token vt / R, rank vt % R), columns p0 .. p0+3
   const int vt = tid >> 4, p0 = 4 * (tid & 15);
   // phase (waves 0-7): angle ps, tokens TPL pg .. TPL pg + 3
   const int ps = tid >> 4, pg = tid & 15;
@@ -2156,13 +2170,27 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
                           : 0.f;
   }
 
-  // rounded biases of the lane's 4 columns (the rows come normalized from prep)
+  // rounded biases of the lane's 4 columns, rank qr (the rows come normalized from prep)
   float bq[4], bk[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int n = n0 + i;
-    bq[i] = rnd<T>(ldx(a.q_bias.ptr, a.q_bias.dtype, h * a.q_bias.stride[0] + n));
-    bk[i] = rnd<T>(ldx(a.k_bias.ptr, a.k_bias.dtype, h * a.k_bias.stride[0] + n));
+    const int n = qcol(i);
+    bq[i] = rnd<T>(ldx(a.q_bias.ptr, a.q_bias.dtype,
+                       h * a.q_bias.stride[0] + qr * a.q_bias.stride[1] + n));
+    bk[i] = rnd<T>(ldx(a.k_bias.ptr, a.k_bias.dtype,
+                       h * a.k_bias.stride[0] + qr * a.k_bias.stride[1] + n));
+  }
+  if constexpr (R > 1) {
+    // the rounded mimo_x / mimo_z and mimo_out of this head (ops.py:700-714, 869-877)
+    for (int i = tid; i < R * kPPad; i += k16Threads) {
+      const int r = i / kPPad, p = i - r * kPPad;
+      F[Ly::MX + i] = rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
+                                 h * a.mimo_x.stride[0] + r * a.mimo_x.stride[1] + p));
+      F[Ly::MZ + i] = rnd<T>(ldx(a.mimo_z.ptr, a.mimo_z.dtype,
+                                 h * a.mimo_z.stride[0] + r * a.mimo_z.stride[1] + p));
+      F[Ly::MO + i] = ldx(a.mimo_out.ptr, a.mimo_out.dtype,
+                          h * a.mimo_out.stride[0] + r * a.mimo_out.stride[1] + p);
+    }
   }
 
   f4 st[2];
@@ -2180,7 +2208,7 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
       }
     }
   }
-  // Endpoint continuation (ops.py:681-686): S += dt_0 (1 - trap_0) v_prev k_prev^T.
+  // Endpoint continuation (ops.py:681-686): S += dt_0 (1 - trap_0) sum_r (v_prev mx_r) k_prev_r^T.
   if (a.initial_k.ptr != nullptr && L > 0) {
     float dt0, adt0;
     dt_adt(true, ldx(a.dt.ptr, a.dt.dtype, b * a.dt.stride[0] + h * a.dt.stride[2]),
@@ -2197,9 +2225,18 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int n = 16 * sni + 4 * lg + i;
-        const float k0 = to_f(static_cast<const T*>(a.initial_k.ptr)
-                                  [b * a.initial_k.stride[0] + h * a.initial_k.stride[1] + n]);
-        st[k][i] += c0 * (v0 * k0);
+        float outer = 0.f;
+        for (int r = 0; r < R; ++r) {
+          const float pv = R > 1 ? mul_r<T>(v0, rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
+                                                             h * a.mimo_x.stride[0] +
+                                                                 r * a.mimo_x.stride[1] + p)))
+                                 : v0;
+          const float k0 = to_f(static_cast<const T*>(a.initial_k.ptr)
+                                    [b * a.initial_k.stride[0] + h * a.initial_k.stride[1] +
+                                     r * a.initial_k.stride[2] + n]);
+          outer += pv * k0;
+        }
+        st[k][i] += c0 * outer;
       }
     }
   }
@@ -2211,13 +2248,14 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
   const __amdgpu_buffer_rsrc_t rs_p =
       make_rsrc(g.proj + b * g.proj_b, L * (tok_b < 0 ? -tok_b : tok_b));
   const __amdgpu_buffer_rsrc_t rs_w = make_rsrc(prep, g.ws_bytes);
-  // the normalized q / k rows of batch row b (token stride 2 N elements, k after q; rows past
-  // token L read zero)
+  // the normalized q / k rows of batch row b: row (token, rank) at 2 N elements, k after q (rows
+  // past token L read zero)
   const __amdgpu_buffer_rsrc_t rs_qk =
-      make_rsrc(reinterpret_cast<const char*>(prep) + g.ws_qk + static_cast<int64_t>(b) * L * 4 * kNPad,
-                L * 4 * kNPad);
-  const int o_qk = qt * 4 * kNPad + n0 * ES;  // token qt (forward order), column n0 of q
-  const int o_vz = g.o_v + h * g.vz_h + vt * tok_b + p0 * ES, d_z = g.o_z - g.o_v;
+      make_rsrc(reinterpret_cast<const char*>(prep) + g.ws_qk +
+                    static_cast<int64_t>(b) * L * R * 4 * kNPad,
+                L * R * 4 * kNPad);
+  const int o_qk = qt * 4 * kNPad + n0 * ES;  // row qt (forward order), column n0 of q
+  const int o_vz = g.o_v + h * g.vz_h + (vt / R) * tok_b + p0 * ES, d_z = g.o_z - g.o_v;
   const int nsub = g.nsub, scw = g.scw;
   // side words (waves 0-3, one float pair per lane): the scalar block
   const int q2 = 2 * tid;
@@ -2249,12 +2287,20 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
   float2 side = make_float2(0.f, 0.f);
   float4 ang = make_float4(0.f, 0.f, 0.f, 0.f);
   auto load_qk = [&](int t0) {
-    // the rows are stored in the call's token order: logical token t at row t
+    // the rows are stored in the call's token order: logical token t at rows t R .. t R + R - 1
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int o = o_qk + (t0 + 32 * j) * 4 * kNPad;
-      bload_words<2>(rq[j], rs_qk, o);
-      bload_words<2>(rk[j], rs_qk, o + 2 * kNPad);
+      const int o = o_qk + (t0 * R + 32 * j) * 4 * kNPad;
+      if (R > 1 && rot) {
+        // columns n0, n0 + 1 and their rotation partners n0 + 64, n0 + 65
+        rq[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rs_qk, o, 0, 0);
+        rq[j][1] = __builtin_amdgcn_raw_buffer_load_b32(rs_qk, o + 128, 0, 0);
+        rk[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rs_qk, o + 2 * kNPad, 0, 0);
+        rk[j][1] = __builtin_amdgcn_raw_buffer_load_b32(rs_qk, o + 2 * kNPad + 128, 0, 0);
+      } else {
+        bload_words<2>(rq[j], rs_qk, o);
+        bload_words<2>(rk[j], rs_qk, o + 2 * kNPad);
+      }
     }
   };
   auto load_vz = [&](int t0) {
@@ -2290,11 +2336,15 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
     // phases of sub-chunk c (waves 0-7), from the angle tile and the dt of its side block
     if (ph_wave && c < nsub) {
       float pa[TPL];
-      const float4 v = *reinterpret_cast<const float4*>(ANG + 4 * ang_slot(pg, ps));
-      pa[0] = v.x;
-      pa[1] = v.y;
-      pa[2] = v.z;
-      pa[3] = v.w;
+      if constexpr (TPL == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(ANG + 4 * ang_slot(pg, ps));
+        pa[0] = v.x;
+        pa[1] = v.y;
+        pa[2] = v.z;
+        pa[3] = v.w;
+      } else {
+        pa[0] = ANG[4 * ang_slot(pg >> 2, ps) + (pg & 3)];  // token pg of its 4-token group
+      }
       phase_stage<PG, TPL, CST, true, false>(csb(c), ps, F + Ly::PBASE + ps, F + Ly::POFF + ps,
                                              scb(c) + SB_::DTV, c * TOK, L, pg, lane, true, pa,
                                              fph, fblk, blk_stride);
@@ -2321,9 +2371,10 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
     if (c + 1 < nsub) put_side(c + 1);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      // token tt: q = q^ + bias, k = k^ + bias, rotated (pairs (n0, n0+1), (n0+2, n0+3), angles
-      // n0 / 2 and n0 / 2 + 1, adjacent in the cos / sin table row)
-      const int tt = qt + 32 * j;
+      // row rw (token tt): q = q^ + bias, k = k^ + bias, rotated. Rank 1: pairs (n0, n0+1),
+      // (n0+2, n0+3), angles n0 / 2 and n0 / 2 + 1; rank 4: pairs (n0 + e, n0 + 64 + e), angles
+      // n0 + e (e < 2). Both angle pairs are adjacent in the cos / sin table row.
+      const int rw = qt + 32 * j, tt = rw / R;
       f4 q, k;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -2331,32 +2382,65 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
         k[i] = raw_get<T>(rk[j], i) + bk[i];
       }
       if (rot) {
-        const f4 cv = *reinterpret_cast<const f4*>(CSt + tt * CST + 2 * cs_col<true>(n0 >> 1, tt));
+        const f4 cv = *reinterpret_cast<const f4*>(
+            CSt + tt * CST + 2 * cs_col<true>(R == 1 ? n0 >> 1 : n0, tt));
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
+          // the pair's two columns: (2 pp, 2 pp + 1) for rank 1, (pp, pp + 2) for rank 4
+          const int u0 = R == 1 ? 2 * pp : pp, u1 = R == 1 ? 2 * pp + 1 : pp + 2;
           const float cc = cv[2 * pp], ss = cv[2 * pp + 1];
-          const float q0 = q[2 * pp], q1 = q[2 * pp + 1];
-          const float k0 = k[2 * pp], k1 = k[2 * pp + 1];
-          q[2 * pp] = fmaf(q0, cc, -(q1 * ss));
-          q[2 * pp + 1] = fmaf(q0, ss, q1 * cc);
-          k[2 * pp] = fmaf(k0, cc, -(k1 * ss));
-          k[2 * pp + 1] = fmaf(k0, ss, k1 * cc);
+          const float q0 = q[u0], q1 = q[u1];
+          const float k0 = k[u0], k1 = k[u1];
+          q[u0] = fmaf(q0, cc, -(q1 * ss));
+          q[u1] = fmaf(q0, ss, q1 * cc);
+          k[u0] = fmaf(k0, cc, -(k1 * ss));
+          k[u1] = fmaf(k0, ss, k1 * cc);
         }
       }
-      if constexpr (!SO) st_quad<T>(Qs + tt * LQ + n0, q);
-      st_quad<T>(Ks + tt * LQ + n0, k);
+      if (R > 1 && rot) {
+        if constexpr (!SO) {
+          st_pair<T>(Qs + rw * LQ + n0, q[0], q[1]);
+          st_pair<T>(Qs + rw * LQ + n0 + 64, q[2], q[3]);
+        }
+        st_pair<T>(Ks + rw * LQ + n0, k[0], k[1]);
+        st_pair<T>(Ks + rw * LQ + n0 + 64, k[2], k[3]);
+      } else {
+        if constexpr (!SO) st_quad<T>(Qs + rw * LQ + n0, q);
+        st_quad<T>(Ks + rw * LQ + n0, k);
+      }
     }
     {
-      // value / gate of token vt: VR / ZR as loaded, VS = v * scale * exp(cum_last - cum)
-      const float ev = SC[SB_::SCL + vt] * __expf(SC[SB_::CL] - SC[SB_::CUM + vt]);
+      // value / gate of row vt (token tv): VR / ZR = v, z (rank 1 as loaded; rank 4 times the
+      // rounded mimo_x / mimo_z of the row's rank, rounded), VS = VR * scale * exp(cum_last - cum)
+      const int tv = vt / R;
+      const float ev = SC[SB_::SCL + tv] * __expf(SC[SB_::CL] - SC[SB_::CUM + tv]);
       f4 sv;
+      if constexpr (R == 1) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sv[i] = raw_get<T>(rv, i) * ev;
-      st_quad<T>(VS + v_off(vt, p0), sv);
-      if constexpr (!SO) {
-        *reinterpret_cast<u32x2*>(VR + v_off(vt, p0)) = (u32x2){rv[0], rv[1]};
-        *reinterpret_cast<u32x2*>(ZR + v_off(vt, p0)) = (u32x2){rz[0], rz[1]};
+        for (int i = 0; i < 4; ++i) sv[i] = raw_get<T>(rv, i) * ev;
+        if constexpr (!SO) {
+          *reinterpret_cast<u32x2*>(VR + v_off(vt, p0)) = (u32x2){rv[0], rv[1]};
+          *reinterpret_cast<u32x2*>(ZR + v_off(vt, p0)) = (u32x2){rz[0], rz[1]};
+        }
+      } else {
+        const int mo = (vt & (R - 1)) * kPPad + p0;
+        const f4 mx = *reinterpret_cast<const f4*>(F + Ly::MX + mo);
+        f4 vq;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          vq[i] = mul_r<T>(raw_get<T>(rv, i), mx[i]);
+          sv[i] = vq[i] * ev;
+        }
+        if constexpr (!SO) {
+          const f4 mz = *reinterpret_cast<const f4*>(F + Ly::MZ + mo);
+          f4 zq;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) zq[i] = mul_r<T>(raw_get<T>(rz, i), mz[i]);
+          st_quad<T>(VR + v_off(vt, p0), vq);
+          st_quad<T>(ZR + v_off(vt, p0), zq);
+        }
       }
+      st_quad<T>(VS + v_off(vt, p0), sv);
     }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -2393,26 +2477,44 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
         acc = M::mma(av, bv, acc);
         __builtin_amdgcn_sched_barrier(0);
       }
-      const float cum_t = SC[SB_::CUM + tq];
+      // decay weights by token: row tq is token tq / R, column rows 16 sj + 4 lg + i are
+      // tokens (16 sj + 4 lg + i) / R (rank 4: the one token 4 sj + lg)
+      const int tqt = tq / R;
+      const float cum_t = SC[SB_::CUM + tqt];
       f4 wv;
       if (sj < it) {
         // d = exp(cum_t - cend) * (scale_s exp(cend - cum_s)), both factors <= 1
         const float at = __expf(cum_t - SC[SB_::CEND + sj]);
-        const f4 bs = *reinterpret_cast<const f4*>(SC + SB_::BSC + 16 * sj + 4 * lg);
+        if constexpr (R == 1) {
+          const f4 bs = *reinterpret_cast<const f4*>(SC + SB_::BSC + 16 * sj + 4 * lg);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) wv[i] = acc[i] * (at * bs[i]);
+          for (int i = 0; i < 4; ++i) wv[i] = acc[i] * (at * bs[i]);
+        } else {
+          const float bs = SC[SB_::BSC + 4 * sj + lg];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wv[i] = acc[i] * (at * bs);
+        }
       } else {
-        const float gam_t = SC[SB_::GAM + tq];
-        int tq_m = tq;
+        const float gam_t = SC[SB_::GAM + tqt];
+        int tq_m = tqt;
         __asm__ volatile("" : "+v"(tq_m));
-        const f4 c4 = *reinterpret_cast<const f4*>(SC + SB_::CUM + 16 * sj + 4 * lg);
-        const f4 s4 = *reinterpret_cast<const f4*>(SC + SB_::SCL + 16 * sj + 4 * lg);
+        if constexpr (R == 1) {
+          const f4 c4 = *reinterpret_cast<const f4*>(SC + SB_::CUM + 16 * sj + 4 * lg);
+          const f4 s4 = *reinterpret_cast<const f4*>(SC + SB_::SCL + 16 * sj + 4 * lg);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int ts = 16 * sj + 4 * lg + i;
-          const float lower = s4[i] * __expf(cum_t - c4[i]);
+          for (int i = 0; i < 4; ++i) {
+            const int ts = 16 * sj + 4 * lg + i;
+            const float lower = s4[i] * __expf(cum_t - c4[i]);
+            const float d = tq_m > ts ? lower : (tq_m == ts ? gam_t : 0.f);
+            wv[i] = acc[i] * d;
+          }
+        } else {
+          // same token (every rank pair): gamma; an earlier token: the decayed scale
+          const int ts = 4 * sj + lg;
+          const float lower = SC[SB_::SCL + ts] * __expf(cum_t - SC[SB_::CUM + ts]);
           const float d = tq_m > ts ? lower : (tq_m == ts ? gam_t : 0.f);
-          wv[i] = acc[i] * d;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wv[i] = acc[i] * d;
         }
       }
       // W[t][s], s = 16 sj + 4 lg + i, at s' = 32 (sj / 2) + 8 lg + 4 (sj % 2) + i: the order of
@@ -2427,7 +2529,7 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
       // kk + 16 + 4 lg + j (slots 4 + j), so the 32 lanes of each read take 8 consecutive tokens
       const int xr = l16 >> 2, xc = 4 * (l16 & 3);
 #pragma unroll
-      for (int kk = 0; kk < TOK; kk += 32) {
+      for (int kk = 0; kk < 64; kk += 32) {  // the 64 rows
         const int r0 = kk + 4 * lg + xr;
         const T* k0 = Ks + r0 * LQ + 16 * sni + xc;
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -2495,9 +2597,9 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
         ye = M::mma(av, bv, ye);
         __builtin_amdgcn_sched_barrier(0);
       }
-      // epilogue: token tq, columns pb .. pb+3
-      const int pb = 16 * pj + 4 * lg;
-      const float ecum_t = __expf(SC[SB_::CUM + tq]);
+      // epilogue: row tq (token tq / R), columns pb .. pb+3
+      const int pb = 16 * pj + 4 * lg, tqt = tq / R;
+      const float ecum_t = __expf(SC[SB_::CUM + tqt]);
       const typename M::v4 v4 = *reinterpret_cast<const typename M::v4*>(VR + v_off(tq, pb));
       const typename M::v4 z4 = *reinterpret_cast<const typename M::v4*>(ZR + v_off(tq, pb));
       f4 y;
@@ -2505,8 +2607,24 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
       for (int i = 0; i < 4; ++i) {
         y[i] = (fmaf(ye[i], ecum_t, yi[i]) + Dh * to_f(v4[i])) * silu_fast(to_f(z4[i]));
       }
-      bstore_quad<T>(y, rs_o, (tq * out_t + o_out + pb * ES) +
-                                  __builtin_amdgcn_readfirstlane(t0 * out_t));
+      if constexpr (R > 1) {
+        // times mimo_out of the row's rank, summed over the token's R rows: lanes 4m .. 4m+3
+        // of the 16-lane group (DPP quad permutes lane ^ 1 and lane ^ 2)
+        const f4 mo = *reinterpret_cast<const f4*>(F + Ly::MO + (tq & (R - 1)) * kPPad + pb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float t = y[i] * mo[i];
+          t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                             0, __builtin_bit_cast(int, t), 0xb1, 0xf, 0xf, false));
+          t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                             0, __builtin_bit_cast(int, t), 0x4e, 0xf, 0xf, false));
+          y[i] = t;
+        }
+      }
+      if (R == 1 || (tq & (R - 1)) == 0) {
+        bstore_quad<T>(y, rs_o, (tqt * out_t + o_out + pb * ES) +
+                                    __builtin_amdgcn_readfirstlane(t0 * out_t));
+      }
     }
     // phases of c + 1: its angle tile and side block came to LDS in A; its cos / sin table is
     // the other buffer than the one A read
@@ -2514,12 +2632,13 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
     __syncthreads();
   }
 
-  // ---- final k: the biased, rotated k of token L-1, still in Ks from the last sub-chunk
+  // ---- final k: the biased, rotated k rows of token L-1, still in Ks from the last sub-chunk
   if (a.final_k.ptr != nullptr && L > 0) {
     const int tl = (L - 1) - (nsub - 1) * TOK;
-    for (int n = tid; n < kNPad; n += k16Threads) {
-      static_cast<T*>(a.final_k.ptr)[b * a.final_k.stride[0] + h * a.final_k.stride[1] + n] =
-          Ks[tl * LQ + n];
+    for (int i = tid; i < R * kNPad; i += k16Threads) {
+      const int r = i / kNPad, n = i - r * kNPad;
+      static_cast<T*>(a.final_k.ptr)[b * a.final_k.stride[0] + h * a.final_k.stride[1] +
+                                     r * a.final_k.stride[2] + n] = Ks[(tl * R + r) * LQ + n];
     }
   }
   if (a.final_decay.ptr != nullptr && tid == 0) {
@@ -2903,12 +3022,13 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // A call scan16_kernel may serve (the projection form is checked later, at launch): the model's
 // SISO shape in a 16-bit activation dtype with RMSNorm, head biases, raw dt and angle phases.
-static bool siso16_candidate(const m3_scan_args& a) {
-  return (a.act_dtype == M3_BF16 || a.act_dtype == M3_F16) && a.rank == 1 && a.groups == 1 &&
+static bool scan16_candidate(const m3_scan_args& a) {
+  return (a.act_dtype == M3_BF16 || a.act_dtype == M3_F16) &&
+         (a.rank == 1 || a.rank == 4) && a.groups == 1 &&
          a.d_state == kNPad && a.head_dim == kPPad && a.num_angles == kSMax &&
          a.q_norm_w.ptr != nullptr && a.k_norm_w.ptr != nullptr && a.q_bias.ptr != nullptr &&
          a.k_bias.ptr != nullptr && a.raw_dt != 0 && a.phase_mode == M3_PHASE_ANGLES &&
-         a.mimo_rotation == 0;
+         (a.mimo_rotation != 0) == (a.rank > 1);
 }
 
 // Prep workspace regions (floats, each 16-byte aligned) and the sub-chunk geometry; returns the
@@ -2938,11 +3058,12 @@ static size_t ws_layout(const m3_scan_args& a, ScanGeom& g) {
   g.ws_bytes = bytes < (int64_t{1} << 30) ? static_cast<int>(bytes) : -1;
   g.ws_qk = -1;
   g.qk_bytes = -1;
-  if (siso16_candidate(a)) {
-    // 256-byte aligned; the rows' 32-bit offsets run up to two sub-chunks past the end
-    const int64_t qk = batch * len * 2 * a.d_state * 2;
+  const int64_t qk = batch * len * (a.rank > 0 ? a.rank : 1) * 2 * a.d_state * 2;
+  if (scan16_candidate(a) && qk < (int64_t{1} << 30)) {
+    // 256-byte aligned, addressed in 32 bits (the rows' offsets run up to two sub-chunks past
+    // the end); larger calls take scan_kernel, which reads the raw rows
     g.ws_qk = (bytes + 255) / 256 * 256;
-    g.qk_bytes = qk < (int64_t{1} << 30) ? static_cast<int>(qk) : -1;
+    g.qk_bytes = static_cast<int>(qk);
     return static_cast<size_t>(g.ws_qk + qk);
   }
   return static_cast<size_t>(bytes);
@@ -3115,19 +3236,19 @@ static int launch_kernel(const m3_scan_args& a, const ScanGeom& g, const float* 
   return check_launch("m3_scan_fwd");
 }
 
-template <typename T, bool SO>
+template <typename T, int R, bool SO>
 static int launch_kernel16(const m3_scan_args& a, const ScanGeom& g, const float* prep,
                            dim3 grid, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan16_kernel<T, SO>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan16_kernel<T, R, SO>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, Lay16::BYTES);
     if (e != hipSuccess) {
       return fail(M3_ELAUNCH, "m3_scan_fwd: hipFuncSetAttribute: %s", hipGetErrorString(e));
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((scan16_kernel<T, SO>), grid, dim3(k16Threads), Lay16::BYTES, stream, a, g,
+  hipLaunchKernelGGL((scan16_kernel<T, R, SO>), grid, dim3(k16Threads), Lay16::BYTES, stream, a, g,
                      prep);
   return check_launch("m3_scan_fwd");
 }
@@ -3169,14 +3290,13 @@ static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep,
   }
   const dim3 grid(static_cast<unsigned>(a.batch) * a.heads), block(kThreads);
   if (full_shape(a, g, R) && prep != nullptr) {
-    if constexpr (sizeof(T) == 2 && R == 1) {
-      // the model's SISO shape: the 16-wave kernel (prep wrote the normalized rows: vector rows)
-      if (g.ws_qk < 0 || g.qk_bytes <= 0) {
-        return fail(M3_EUNSUPPORTED, "m3_scan_fwd: %lld normalized q / k rows exceed 2^30 bytes",
-                    static_cast<long long>(a.batch) * a.length);
+    if constexpr (sizeof(T) == 2 && (R == 1 || R == 4)) {
+      // the model's shape at ranks 1 and 4: the 16-wave kernel, when prep wrote the normalized
+      // rows (below 2^30 bytes of them)
+      if (g.ws_qk >= 0 && g.qk_bytes > 0) {
+        if (state_only) return launch_kernel16<T, R, true>(a, g, prep, grid, stream);
+        return launch_kernel16<T, R, false>(a, g, prep, grid, stream);
       }
-      if (state_only) return launch_kernel16<T, true>(a, g, prep, grid, stream);
-      return launch_kernel16<T, false>(a, g, prep, grid, stream);
     }
     if constexpr (sizeof(T) == 2) {
       if (state_only) return launch_kernel<T, R, true, true>(a, g, prep, grid, block, stream);

@@ -46,12 +46,13 @@ def test_scan_hook_runs_the_library(rank):
 
 
 def test_scan_hook_falls_back_once_for_a_refused_shape():
-    # rank 9 exceeds what either scan kernel serves: one warning, then the cached key
+    # rank 64 at d_state 128: its per-token q / k / value rows exceed what either scan kernel
+    # holds (the recurrent scan's 160 KiB of LDS): one warning, then the cached key
     inp = _inputs(1, torch.bfloat16, seed=3, length=20, phase=False, bias=False, initial=False)
     dev = {n: (t.to(DEV) if isinstance(t, torch.Tensor) else t) for n, t in inp.items()}
-    q = dev["q"].expand(-1, -1, -1, 9, -1).contiguous()
+    q = dev["q"].expand(-1, -1, -1, 64, -1).contiguous()
     heads, p = dev["value"].shape[2], dev["value"].shape[3]
-    mimo = torch.ones(heads, 9, p, device=DEV)
+    mimo = torch.ones(heads, 64, p, device=DEV)
     args = _hook_args(dict(dev, q=q, k=q.clone(), mimo_x=mimo, mimo_z=mimo, mimo_out=mimo))
     with torch.inference_mode():
         with pytest.warns(RuntimeWarning, match="unavailable"):
