@@ -299,7 +299,8 @@ def bench_prefill_config(name, d_model, depth, rank, causal, shape, seed, log, i
         us=round(ts * 1e6, 1), tok_s=round(batch * length / ts, 1),
         hbm_frac=round(nbytes / ts / 1e12 / (HBM_PEAK_GBS / 1e3), 4),
         mfma_frac_at_cref=round(flops / ts / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-        directions=1 if causal else 2,
+        # one ScanCall is one direction; a bidirectional layer runs two of them concurrently
+        directions=1, layer_directions=1 if causal else 2,
         roofline=dict(bound="mfma" if mfma_bound else "hbm", achieved=round(achieved, 1),
                       peak=peak, unit="TFLOP/s" if mfma_bound else "GB/s",
                       frac=round(achieved / peak, 4),
