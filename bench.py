@@ -280,6 +280,25 @@ def bench_prefill_config(name, d_model, depth, rank, causal, shape, seed, log, i
         for _ in range(50):
             call.launch()
         ts = _events_time(call.launch, 10 * iters) / (10 * iters)
+        tp = None
+        if not causal:
+            # the layer's two directions as the model runs them: the reverse call on a side
+            # stream (default priority) concurrent with the forward one, joined after both
+            rcall = ops.ScanCall(proj, mixer, chunk_size=mixer.inference_chunk_size,
+                                 reverse=True)
+            main, side = torch.cuda.current_stream(dev), torch.cuda.Stream(device=dev)
+
+            def pair():
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    rcall.launch()
+                call.launch()
+                main.wait_stream(side)
+
+            for _ in range(20):
+                pair()
+            tp = _events_time(pair, 10 * iters) / (10 * iters)
+            del rcall
         del call, proj
         for _ in range(2):
             model(x)
@@ -307,8 +326,15 @@ def bench_prefill_config(name, d_model, depth, rank, causal, shape, seed, log, i
                       traffic=_traffic_from_profile(
                           os.path.join(ROOT, "profiles", f"scan_{tag}_pmc.txt")),
                       bytes_per_launch=nbytes, flops_per_launch_at_cref=flops))
+    if tp is not None:
+        # both directions of the layer, concurrent: B L tokens scanned forward and backward
+        out["scan_call"]["both_directions"] = dict(
+            us=round(tp * 1e6, 1), layer_tok_s=round(batch * length / tp, 1),
+            hbm_frac=round(2 * nbytes / tp / 1e12 / (HBM_PEAK_GBS / 1e3), 4),
+            vs_two_single_calls=round(tp / (2 * ts), 4))
     log(f"{name}: forward {t * 1e3:.2f} ms ({out['forward_tok_s']:.4e} tok/s); one layer's "
-        f"scan call {ts * 1e6:.1f} us")
+        f"scan call {ts * 1e6:.1f} us" +
+        (f", both directions concurrently {tp * 1e6:.1f} us" if tp is not None else ""))
     del model, x
     torch.cuda.empty_cache()
     return out
