@@ -79,11 +79,13 @@ def test_forward_prefill_steps_match_oracle(case, bf16):
             torch.testing.assert_close(a.float().cpu(), b.float(), **tol)
 
 
-@pytest.mark.parametrize("length", [1, 63, 64, 65, 130, 700])
-def test_model_shape_lengths_match_oracle(length):
-    """The model's SISO shape (N 128, P 64, 32 angles: the full-shape kernels) in bf16 autocast
-    over 1 to 11 sub-chunks, ragged and exact: forward output, prefill output and cache."""
-    model, params, dims = _model(128, 128, 1, 1, seed=30)
+@pytest.mark.parametrize("length", [1, 15, 16, 17, 63, 64, 65, 130, 700])
+@pytest.mark.parametrize("rank", [1, 4])
+def test_model_shape_lengths_match_oracle(length, rank):
+    """The model's shape (N 128, P 64, 32 angles: the full-shape kernels; the 16-wave scan's
+    64-row sub-chunks are 64 tokens at rank 1 and 16 at rank 4) in bf16 autocast over 1 to 44
+    sub-chunks, ragged and exact: forward output, prefill output and cache."""
+    model, params, dims = _model(128, 128, 1, rank, seed=30 + rank)
     torch.manual_seed(31)
     x = torch.randn(2, length, 128)
     with torch.inference_mode(), _oracle_ctx(True):
@@ -94,8 +96,8 @@ def test_model_shape_lengths_match_oracle(length):
         assert ops._HIP_LAST_SCAN_DISPATCH
         prefix, cache = model.prefill(x.to(DEV))
     torch.cuda.synchronize()
-    print(f"model shape L={length}: forward {(got.float().cpu() - want.float()).abs().max():.2e}",
-          flush=True)
+    print(f"model shape R={rank} L={length}: forward "
+          f"{(got.float().cpu() - want.float()).abs().max():.2e}", flush=True)
     torch.testing.assert_close(got.float().cpu(), want.float(), **BF16)
     torch.testing.assert_close(prefix.float().cpu(), want.float(), **BF16)
     for a, b in zip(cache[0], want_cache[0]):
