@@ -900,15 +900,43 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
     const int l16 = tid & 15, row0 = blk * 16 * kNormRows + (tid >> 4);
     const int N = a.d_state;
     const bool in = 8 * l16 < N;  // lanes past column N load column 0 and count zeros
-    auto row_ptr = [&](int row) {
+    // Rows (token, group, rank, q | k): a lane's rows row0 + 16 k all have row0's parity, so one
+    // tensor (q or k). When 2 gr_n divides 16 they also share its (group, rank), the token
+    // advancing by 8 / gr_n per k: the addresses follow from row0's by additions (a division
+    // per row and a select per tensor field, unrolled over the rows, were most of this range's
+    // instructions). Rows past the end re-read the last batch row's last token.
+    const int which = row0 & 1;
+    const m3_tensor& xt = which ? a.k : a.q;
+    const T* xbase = static_cast<const T*>(xt.ptr) + (in ? 8 * l16 : 0);
+    const int64_t xs0 = xt.stride[0], xs1 = xt.stride[1];
+    const bool step_rows = 16 % (2 * gr_n) == 0;
+    const int dtok = step_rows ? 8 / gr_n : 0;
+    int tk = row0 / (2 * gr_n);
+    const int gr = (row0 - tk * 2 * gr_n) >> 1;
+    const int gi = gr / a.rank, rk = gr - gi * a.rank;
+    const T* xgr = xbase + gi * xt.stride[2] + rk * xt.stride[3];
+    int bk = tk / L, tt = tk - bk * L;
+    auto row_ptr = [&](int k) -> const T* {
+      if (step_rows) {
+        if (k > 0) {
+          tt += dtok;
+          while (tt >= L) {
+            tt -= L;
+            ++bk;
+          }
+        }
+        const bool live = bk < a.batch;
+        return xgr + (live ? bk : a.batch - 1) * xs0 + (live ? tt : L - 1) * xs1;
+      }
+      const int row = min(row0 + 16 * k, nrows - 1);
       const int tok = row / (2 * gr_n);
       const int rem = row - tok * 2 * gr_n;
-      const int gr = rem >> 1, which = rem & 1;
-      const int gi = gr / a.rank, r = gr - gi * a.rank;
-      const int b = tok / L, t = tok - b * L;
-      const m3_tensor& x = which ? a.k : a.q;
-      return static_cast<const T*>(x.ptr) + b * x.stride[0] + t * x.stride[1] +
-             gi * x.stride[2] + r * x.stride[3] + (in ? 8 * l16 : 0);
+      const int g2 = rem >> 1, wh = rem & 1;
+      const int g2i = g2 / a.rank, r2 = g2 - g2i * a.rank;
+      const int b2 = tok / L, t2 = tok - b2 * L;
+      const m3_tensor& x = wh ? a.k : a.q;
+      return static_cast<const T*>(x.ptr) + b2 * x.stride[0] + t2 * x.stride[1] +
+             g2i * x.stride[2] + r2 * x.stride[3] + (in ? 8 * l16 : 0);
     };
     float ss[kNormRows];
     uint32_t w8[kNormRows][Words<T>::W8];
@@ -926,8 +954,8 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
     if (g.vec_qk) {
 #pragma unroll
       for (int k = 0; k < kNormRows; ++k) {
-        // rows past the end re-read the last row; their sums are not stored
-        const T* p = row_ptr(min(row0 + 16 * k, nrows - 1));
+        // rows past the end re-read an earlier row; their sums are not stored
+        const T* p = row_ptr(k);
 #pragma unroll
         for (int j = 0; j < Words<T>::W8; j += 4) {
           const uint4 q = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint32_t*>(p) + j);
@@ -949,7 +977,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
     } else {
 #pragma unroll
       for (int k = 0; k < kNormRows; ++k) {
-        const T* p = row_ptr(min(row0 + 16 * k, nrows - 1));
+        const T* p = row_ptr(k);
         ss[k] = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -960,15 +988,14 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
         }
       }
     }
+    float fac[kNormRows];
 #pragma unroll
     for (int k = 0; k < kNormRows; ++k) {
 #pragma unroll
       for (int o = 8; o > 0; o >>= 1) ss[k] += __shfl_xor(ss[k], o, 16);
       const int row = row0 + 16 * k;
-      if (l16 == 0 && row < nrows) {
-        ws[g.ws_norm + static_cast<int64_t>(row)] =
-            1.f / sqrtf(ss[k] / static_cast<float>(N) + a.norm_eps);
-      }
+      fac[k] = 1.f / sqrtf(ss[k] / static_cast<float>(N) + a.norm_eps);
+      if (l16 == 0 && row < nrows) ws[g.ws_norm + static_cast<int64_t>(row)] = fac[k];
     }
     if constexpr (sizeof(T) == 2) {
       if (rows_out) {
@@ -994,16 +1021,18 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
             wn[1][i] = rnd<T>(ldx(a.k_norm_w.ptr, a.k_norm_w.dtype, (8 * l16 + i) * a.k_norm_w.stride[0]));
           }
         }
+        // the lane's tensor's weights (every row of the lane is q, or every row k)
+        float wl[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wl[i] = which ? wn[1][i] : wn[0][i];
         char* qk = reinterpret_cast<char*>(ws) + g.ws_qk;
 #pragma unroll
         for (int k = 0; k < kNormRows; ++k) {
           const int row = row0 + 16 * k;
           if (row >= nrows) continue;
-          const float f = 1.f / sqrtf(ss[k] / static_cast<float>(N) + a.norm_eps);
-          const int which = row & 1;
           float x[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) x[i] = raw_get<T>(w8[k], i) * f * wn[which][i];
+          for (int i = 0; i < 8; ++i) x[i] = raw_get<T>(w8[k], i) * fac[k] * wl[i];
           st_row8<T>(reinterpret_cast<T*>(qk + (static_cast<int64_t>(row) * N + 8 * l16) * 2), x);
         }
       }
