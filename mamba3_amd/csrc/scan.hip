@@ -165,11 +165,6 @@ __device__ __forceinline__ f4 zero4() {
   return z;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
 template <typename T>
 __device__ __forceinline__ T* lds_t(char* base, int off) {
   return reinterpret_cast<T*>(base + off);
@@ -308,6 +303,19 @@ __device__ __forceinline__ float seg_incl_scan(float x, int lane) {
   if constexpr (SEG > 2) { const float u = dpp_shr<0x112>(x); x += j >= 2 ? u : 0.f; }
   if constexpr (SEG > 4) { const float u = dpp_shr<0x114>(x); x += j >= 4 ? u : 0.f; }
   if constexpr (SEG > 8) { const float u = dpp_shr<0x118>(x); x += j >= 8 ? u : 0.f; }
+  return x;
+}
+
+// Sum over each 16-lane row, in every lane of the row: DPP row rotations by 8, 4, 2 and 1.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128,
+                                                             0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x124,
+                                                             0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x122,
+                                                             0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x121,
+                                                             0xf, 0xf, false));
   return x;
 }
 
@@ -865,7 +873,7 @@ __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __res
 }
 
 // Head-independent and per-(head, sub-chunk) work ahead of the scan, three block ranges:
-//  [0, nb_norm)  one 16-lane group per kNormRows raw q / k rows (token, group, rank, q|k), 8
+//  [0, nb_norm)  one 16-lane group per norm_rows() raw q / k rows (token, group, rank, q|k), 8
 //                elements per lane: each row's RMSNorm factor 1 / sqrt(mean(x^2) + eps)
 //                (model.py:190-191);
 //  [.., +nb_ang) one lane per kAngQuads (4-token group, angle) pairs, tokens padded to a multiple
@@ -877,7 +885,13 @@ __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __res
 //                the next sub-chunk's first, every head, loaded with consecutive lanes on
 //                consecutive heads (32 heads per pass) into LDS; then one wave per head computes
 //                that head's scalar block.
-constexpr int kNormRows = 8;  // q / k rows per 16-lane group of prep_kernel
+// q / k rows per 16-lane group of prep_kernel: 16 for the 16-bit single-rank rows (their fewer,
+// longer workgroups measured faster at config 2: 37.5 -> 34.8 us per prep), else 8 (16 measured
+// slower at rank 4, and FP32 rows would not fit the registers)
+template <typename T, int R>
+constexpr int norm_rows() {
+  return sizeof(T) == 2 && R == 1 ? 16 : 8;
+}
 constexpr int kAngQuads = 4;  // (4-token group, angle) pairs per lane of prep_kernel
 
 template <typename T, int R>
@@ -886,6 +900,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
                                                    int nb_ang) {
   // every index below fits 31 bits (checked by the host)
   constexpr int TOK = Mma<T>::ROWS / R, TPT = 16 / R;
+  constexpr int kNormRows = norm_rows<T, R>();
   // the longest-running range (scalar blocks) is dispatched first: block ids [0, nb_sc) map to
   // it, the rest to the norm and angle ranges in order
   const int nb_sc = a.batch * g.nsub;
@@ -991,8 +1006,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
     float fac[kNormRows];
 #pragma unroll
     for (int k = 0; k < kNormRows; ++k) {
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) ss[k] += __shfl_xor(ss[k], o, 16);
+      ss[k] = row16_sum(ss[k]);  // the row's 16 lanes
       const int row = row0 + 16 * k;
       fac[k] = 1.f / sqrtf(ss[k] / static_cast<float>(N) + a.norm_eps);
       if (l16 == 0 && row < nrows) ws[g.ws_norm + static_cast<int64_t>(row)] = fac[k];
@@ -3306,6 +3320,7 @@ static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep,
     if (rows >= INT32_MAX || ang >= INT32_MAX || blocks >= INT32_MAX || tokens >= INT32_MAX) {
       return fail(M3_EUNSUPPORTED, "m3_scan_fwd: too many tokens for one launch");
     }
+    constexpr int kNormRows = norm_rows<T, R>();
     const int64_t nb_norm = (rows + 16 * kNormRows - 1) / (16 * kNormRows);
     const int64_t nb_ang = (ang / 4 + 256 * kAngQuads - 1) / (256 * kAngQuads), nb_sc = blocks;
     if (run_prep && nb_norm + nb_ang + nb_sc > 0) {
