@@ -872,6 +872,57 @@ __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __res
   }
 }
 
+// The same for sub-chunks of TOK <= 16 tokens, 64 / TOK heads per wave: lane = (head lane / TOK,
+// token lane % TOK), `o` the lane's head's block, `live` false for lanes past the last head
+// (they compute on a valid head's inputs and store nothing). The arithmetic and its order are
+// scalar_block's (a segment's scan is the wave scan's first row), so the blocks are identical.
+template <int TOK, int TPT>
+__device__ __forceinline__ void scalar_block_seg(const m3_scan_args& a, float* __restrict__ o,
+                                                 int c, int lane, bool live, float dt_bias,
+                                                 float dt_in, float a_in, float tr_in,
+                                                 float dtn_in, float trn_in) {
+  static_assert(TOK <= 16 && (TOK & (TOK - 1)) == 0, "segments of at most 16 lanes");
+  using B = ScBlk<TOK>;
+  const int L = a.length;
+  const int j = lane & (TOK - 1), s0 = lane - j;  // token in the sub-chunk, segment's lane 0
+  const int tb = c * TOK, t = tb + j;
+  const int wn = min(TOK, L - tb);
+  const bool tv = j < wn;
+  const bool nv = t + 1 < L;
+  const bool raw_dt = a.raw_dt != 0;
+  float dt = 0.f, adt = 0.f, tr = 0.f;
+  if (tv) {
+    dt_adt_fast(raw_dt, dt_in, a_in, dt_bias, dt, adt);
+    tr = sigmoid_fast(tr_in);
+  }
+  const float own = dt * (1.f - tr);
+  float right = __shfl_down(own, 1);
+  if (j == TOK - 1) {
+    float dn, an;
+    dt_adt_fast(raw_dt, dtn_in, 0.f, dt_bias, dn, an);
+    right = dn * (1.f - sigmoid_fast(trn_in));
+  }
+  if (!nv) right = 0.f;
+  const float gamma = dt * tr;
+  const float scale = gamma + right;
+  const float cum = seg_incl_scan<TOK>(adt, lane);
+  const float cum_last = __shfl(cum, s0 + wn - 1);
+  const float cv = tv ? cum : cum_last;
+  const float cend = __shfl(cv, s0 + min(j | (TPT - 1), wn - 1));
+  if (live) {
+    o[B::DTV + j] = dt;
+    o[B::CUM + j] = cv;
+    o[B::SCL + j] = tv ? scale : 0.f;
+    o[B::GAM + j] = gamma;
+    o[B::BSC + j] = tv ? scale * __expf(cend - cv) : 0.f;
+    if ((j & (TPT - 1)) == 0) o[B::CEND + j / TPT] = cend;
+    if (j == 0) {
+      o[B::ECL] = __expf(cum_last);
+      o[B::CL] = cum_last;
+    }
+  }
+}
+
 // Head-independent and per-(head, sub-chunk) work ahead of the scan, three block ranges:
 //  [0, nb_norm)  one 16-lane group per norm_rows() raw q / k rows (token, group, rank, q|k), 8
 //                elements per lane: each row's RMSNorm factor 1 / sqrt(mean(x^2) + eps)
@@ -884,7 +935,8 @@ __device__ __forceinline__ void scalar_block(const m3_scan_args& a, float* __res
 //  [.., +nb_sc)  one workgroup per (batch, sub-chunk): the dt / a / trap of its TOK tokens and
 //                the next sub-chunk's first, every head, loaded with consecutive lanes on
 //                consecutive heads (32 heads per pass) into LDS; then one wave per head computes
-//                that head's scalar block.
+//                that head's scalar block (sub-chunks of 16 tokens or fewer: one 16- or 8-lane
+//                segment per head, 4 or 8 heads per wave).
 // q / k rows per 16-lane group of prep_kernel: 16 for the 16-bit single-rank rows (their fewer,
 // longer workgroups measured faster at config 2: 37.5 -> 34.8 us per prep), else 8 (16 measured
 // slower at rank 4, and FP32 rows would not fit the registers)
@@ -1131,12 +1183,25 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
       }
       if (tid < HG) s_db[tid] = a.raw_dt != 0 ? decode(rdb, a.dt_bias.dtype) : 0.f;
       __syncthreads();
-      for (int hh = w; hh < hn; hh += 4) {
-        const int h = h0 + hh, j = min(lane, TOK - 1);
-        scalar_block<TOK, TPT>(
-            a, ws + g.ws_sc + (static_cast<int64_t>(b * a.heads + h) * g.nsub + c) * g.scw, c,
-            lane, s_db[hh], s_in[0][j][hh], s_in[1][j][hh], s_in[2][j][hh], s_in[0][TOK][hh],
-            s_in[2][TOK][hh]);
+      if constexpr (TOK <= 16) {
+        // 64 / TOK heads per wave (one wave per head would leave most lanes idle)
+        constexpr int HPW = 64 / TOK;
+        const int j = lane & (TOK - 1);
+        for (int hb = w * HPW; hb < hn; hb += 4 * HPW) {
+          const int hh = hb + lane / TOK, hc = min(hh, hn - 1);
+          scalar_block_seg<TOK, TPT>(
+              a, ws + g.ws_sc + (static_cast<int64_t>(b * a.heads + h0 + hc) * g.nsub + c) * g.scw,
+              c, lane, hh < hn, s_db[hc], s_in[0][j][hc], s_in[1][j][hc], s_in[2][j][hc],
+              s_in[0][TOK][hc], s_in[2][TOK][hc]);
+        }
+      } else {
+        for (int hh = w; hh < hn; hh += 4) {
+          const int h = h0 + hh, j = min(lane, TOK - 1);
+          scalar_block<TOK, TPT>(
+              a, ws + g.ws_sc + (static_cast<int64_t>(b * a.heads + h) * g.nsub + c) * g.scw, c,
+              lane, s_db[hh], s_in[0][j][hh], s_in[1][j][hh], s_in[2][j][hh], s_in[0][TOK][hh],
+              s_in[2][TOK][hh]);
+        }
       }
       __syncthreads();
     }
