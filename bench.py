@@ -284,21 +284,24 @@ def bench_prefill_config(name, d_model, depth, rank, causal, shape, seed, log, i
         if not causal:
             # the layer's two directions as the model runs them: the reverse call on a side
             # stream (default priority) concurrent with the forward one, joined after both
+            # (each call's segments sized for the two calls' combined grid, as the model's)
+            fcall = ops.ScanCall(proj, mixer, chunk_size=mixer.inference_chunk_size,
+                                 concurrent=2)
             rcall = ops.ScanCall(proj, mixer, chunk_size=mixer.inference_chunk_size,
-                                 reverse=True)
+                                 reverse=True, concurrent=2)
             main, side = torch.cuda.current_stream(dev), torch.cuda.Stream(device=dev)
 
             def pair():
                 side.wait_stream(main)
                 with torch.cuda.stream(side):
                     rcall.launch()
-                call.launch()
+                fcall.launch()
                 main.wait_stream(side)
 
             for _ in range(20):
                 pair()
             tp = _events_time(pair, 10 * iters) / (10 * iters)
-            del rcall
+            del fcall, rcall
         del call, proj
         for _ in range(2):
             model(x)

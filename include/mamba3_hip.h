@@ -119,6 +119,14 @@ typedef struct {
 
 /* Bytes of device workspace m3_scan_fwd needs for these arguments (0 is possible). */
 int m3_scan_workspace_size(const m3_scan_args* args, size_t* bytes);
+/*
+ * The segment count m3_scan_fwd uses for these arguments when `concurrent_calls` calls of this
+ * shape run on the GPU at once (1: alone); with args->segments == 0 the library picks it, else
+ * the explicit request is checked. A caller running such calls together (the two directions of
+ * a bidirectional layer) passes the result as args->segments before sizing the workspace.
+ * No counterpart in the reference, whose portable scan has no segments (ops.py:544-822).
+ */
+int m3_scan_segments(const m3_scan_args* args, int concurrent_calls, int* segments);
 int m3_scan_fwd(const m3_scan_args* args, hipStream_t stream);
 
 /*

@@ -95,7 +95,7 @@ class RmsNormArgs(ctypes.Structure):
     ]
 
 
-ENTRY_POINTS = ("m3_scan_fwd", "m3_scan_workspace_size", "m3_scan_fwd_noalloc",
+ENTRY_POINTS = ("m3_scan_fwd", "m3_scan_workspace_size", "m3_scan_segments", "m3_scan_fwd_noalloc",
                 "m3_chunk_state", "m3_step", "m3_linear", "m3_linear_workspace_size",
                 "m3_rms_norm", "m3_last_error", "m3_abi_version")
 SCRATCH_BYTES = 64 << 20  # M3_SCRATCH_BYTES: the no-alloc scan's per-GPU scratch
@@ -121,6 +121,8 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_size_t)]
+    lib.m3_scan_segments.restype = ctypes.c_int
+    lib.m3_scan_segments.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
     lib.m3_last_error.restype = ctypes.c_char_p
     lib.m3_last_error.argtypes = []
     lib.m3_abi_version.restype = ctypes.c_int
@@ -169,6 +171,17 @@ def scan_workspace(args: ctypes.Structure, device: torch.device,
     args.workspace = ws.data_ptr()
     args.workspace_bytes = nbytes.value
     return ws
+
+
+def scan_segments(args: ctypes.Structure, concurrent: int) -> int:
+    """The segment count the library picks for a scan call when ``concurrent`` calls of its
+    shape share the GPU (``m3_scan_segments``)."""
+    lib = load()
+    g = ctypes.c_int(0)
+    rc = lib.m3_scan_segments(ctypes.byref(args), concurrent, ctypes.byref(g))
+    if rc != 0:
+        raise HipError("m3_scan_segments", rc, lib.m3_last_error().decode(errors="replace"))
+    return g.value
 
 
 def call(name: str, args: ctypes.Structure, device: torch.device) -> None:

@@ -136,6 +136,8 @@ struct ScanGeom {
   int xcd_map;           // 1: map blocks so each XCD holds consecutive (b, h)
   int vec_qk, vec_vz;    // 1: q/k rows and v/z rows may be loaded with 16 / 8-byte vectors
   int vec_nw;            // 1: both norm weights unit-stride and 8-byte aligned (4-element loads)
+  int norm_factors;      // 1: prep stores the RMSNorm factors (every scan kernel but the 16-wave
+                         // one, which reads the normalized rows instead)
   // prep workspace, float offsets of its regions (-1: absent): RMSNorm factors [B][L][G*R][2]
   // (q, k), pi tanh(angle) [B][L4][S][4] (4 consecutive tokens of one angle together, L4 =
   // ceil(L / 4)), scalar blocks [B*H][nsub][scw] of `tok`-token sub-chunks
@@ -1061,36 +1063,37 @@ __global__ __launch_bounds__(256) void prep_kernel(const m3_scan_args a, const S
       ss[k] = row16_sum(ss[k]);  // the row's 16 lanes
       const int row = row0 + 16 * k;
       fac[k] = 1.f / sqrtf(ss[k] / static_cast<float>(N) + a.norm_eps);
-      if (l16 == 0 && row < nrows) ws[g.ws_norm + static_cast<int64_t>(row)] = fac[k];
+      if (l16 == 0 && row < nrows && g.norm_factors) ws[g.ws_norm + static_cast<int64_t>(row)] = fac[k];
     }
     if constexpr (sizeof(T) == 2) {
       if (rows_out) {
         // the model's shape at ranks 1 and 4 (N = 128, one group, vector rows): the normalized rows
         // themselves, rnd(x * factor * rnd(w)) (model.py:48-55: F.rms_norm with the weight in the
         // activation dtype, the result in it), rows (token, q | k) at N elements each
-        float wn[2][8];
+        // the lane's tensor's weights (every row of the lane is q, or every row k), chosen by
+        // bit masks on the raw words: a select between two weight arrays by `which` became a
+        // dynamically indexed array in scratch memory
+        float wl[8];
         if (nw_vec) {
+          const uint32_t msk = 0u - static_cast<uint32_t>(which);
+          const int wdt = which ? a.k_norm_w.dtype : a.q_norm_w.dtype;
 #pragma unroll
           for (int h2 = 0; h2 < 2; ++h2) {
-            const f4 q4 = decode4(nw_r[0][h2], a.q_norm_w.dtype);
-            const f4 k4 = decode4(nw_r[1][h2], a.k_norm_w.dtype);
+            Raw4 r;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              wn[0][4 * h2 + e] = rnd<T>(q4[e]);
-              wn[1][4 * h2 + e] = rnd<T>(k4[e]);
-            }
+            for (int j = 0; j < 4; ++j) r.w[j] = (nw_r[0][h2].w[j] & ~msk) | (nw_r[1][h2].w[j] & msk);
+            const f4 v4 = decode4(r, wdt);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wl[4 * h2 + e] = rnd<T>(v4[e]);
           }
         } else {
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            wn[0][i] = rnd<T>(ldx(a.q_norm_w.ptr, a.q_norm_w.dtype, (8 * l16 + i) * a.q_norm_w.stride[0]));
-            wn[1][i] = rnd<T>(ldx(a.k_norm_w.ptr, a.k_norm_w.dtype, (8 * l16 + i) * a.k_norm_w.stride[0]));
+            const float wq = ldx(a.q_norm_w.ptr, a.q_norm_w.dtype, (8 * l16 + i) * a.q_norm_w.stride[0]);
+            const float wk = ldx(a.k_norm_w.ptr, a.k_norm_w.dtype, (8 * l16 + i) * a.k_norm_w.stride[0]);
+            wl[i] = rnd<T>(which ? wk : wq);
           }
         }
-        // the lane's tensor's weights (every row of the lane is q, or every row k)
-        float wl[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) wl[i] = which ? wn[1][i] : wn[0][i];
         char* qk = reinterpret_cast<char*>(ws) + g.ws_qk;
 #pragma unroll
         for (int k = 0; k < kNormRows; ++k) {
@@ -3385,6 +3388,11 @@ static int launch_pass(const m3_scan_args& a, hipStream_t stream, bool run_prep,
     if (rows >= INT32_MAX || ang >= INT32_MAX || blocks >= INT32_MAX || tokens >= INT32_MAX) {
       return fail(M3_EUNSUPPORTED, "m3_scan_fwd: too many tokens for one launch");
     }
+    // the 16-wave kernel (below) reads prep's normalized rows, not the factors: their 4-byte
+    // stores, one per row, would only add partial-line writes
+    const bool k16 = sizeof(T) == 2 && (R == 1 || R == 4) && g.ws_qk >= 0 && g.qk_bytes > 0 &&
+                     full_shape(a, g, R);
+    g.norm_factors = k16 ? 0 : 1;
     constexpr int kNormRows = norm_rows<T, R>();
     const int64_t nb_norm = (rows + 16 * kNormRows - 1) / (16 * kNormRows);
     const int64_t nb_ang = (ang / 4 + 256 * kAngQuads - 1) / (256 * kAngQuads), nb_sc = blocks;
@@ -3442,11 +3450,20 @@ static bool segmentable(const m3_scan_args& a) {
 }
 
 // Segments a call's sequence is split into: 1 for none, -1 for an explicit request that cannot
-// be met. Automatic (segments == 0) when the one-workgroup-per-(b, h) grid would fill at most
-// half of the 256 CUs: the largest power of 2 G with B*H*G <= 256 that cuts L into equal
-// segments of at least 8 sub-chunks (whole 64-token phase blocks with angle phases), taken from
-// G = 4 up (the split scans the sequence twice).
+// be met. Automatic (segments == 0): the G of least estimated time among 1 and the powers of 2
+// from 4 up that cut L into equal segments of at least 8 sub-chunks (whole 64-token phase
+// blocks with angle phases). With one workgroup per (b, h, segment), G segments take
+// ceil(B H G c / 256) rounds over the 256 CUs of 1 / G of the unsplit workgroup's time (c calls
+// of this shape sharing the GPU, 1 alone), times 1.37 for a split, whose state-only first pass
+// and composition cost 0.37 of its second pass (config 5 long); ties go to the smaller G. At
+// config 5 long (24 (b, h) pairs) that is G = 32 alone (3 full rounds; 622 us per call against
+// 689 at G = 8) and G = 16 for its two concurrent directions (1,070 against 1,100 us).
 static bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+static double split_cost(int64_t bhc, int G) {
+  const double rounds = static_cast<double>((bhc * G + 255) / 256);
+  return G == 1 ? rounds : 1.37 * rounds / G;
+}
 
 // The shapes the chunked MFMA kernel tiles: d_state a power of 2 up to 128, head_dim up to 64,
 // up to 32 angles, ranks 1, 2, 4 and 8. Others take the recurrent scan (rscan.hip).
@@ -3455,7 +3472,7 @@ static bool tiled_shape(const m3_scan_args& a) {
          a.num_angles <= kSMax && (a.rank == 1 || a.rank == 2 || a.rank == 4 || a.rank == 8);
 }
 
-static int segments_for(const m3_scan_args& a) {
+static int segments_for(const m3_scan_args& a, int concurrent = 1) {
   if (!tiled_shape(a)) return a.segments > 1 ? -1 : 1;
   if (a.segments == 1 || a.length <= 0 || a.batch <= 0) return 1;
   if (a.segments < 0) return -1;
@@ -3470,12 +3487,18 @@ static int segments_for(const m3_scan_args& a) {
     return ok ? a.segments : -1;
   }
   const int tok = sub_chunk_tokens(a);
-  int G = 1;
-  while (bh * G * 2 <= 256 && a.length % (2 * G * align) == 0 &&
-         a.length / (2 * G) >= 8 * tok) {
-    G *= 2;
+  const int64_t bhc = bh * (concurrent > 1 ? concurrent : 1);
+  int best = 1;
+  double best_cost = split_cost(bhc, 1);
+  for (int G = 4; G <= kMaxSegments && bh * G <= INT32_MAX; G *= 2) {
+    if (a.length % (static_cast<int64_t>(G) * align) != 0 || a.length / G < 8 * tok) break;
+    const double c = split_cost(bhc, G);
+    if (c < best_cost * (1.0 - 1e-9)) {
+      best = G;
+      best_cost = c;
+    }
   }
-  return G >= 4 ? G : 1;
+  return best;
 }
 
 static m3_tensor contiguous(void* p, int dtype, std::initializer_list<int64_t> dims) {
@@ -3755,6 +3778,24 @@ extern "C" int m3_scan_workspace_size(const m3_scan_args* args, size_t* bytes) {
   }
   const int G = m3::segments_for(*args);
   *bytes = G > 1 ? m3::plan_segments(*args, G).total_bytes : m3::ws_layout(*args, g);
+  return M3_OK;
+}
+
+extern "C" int m3_scan_segments(const m3_scan_args* args, int concurrent_calls,
+                                int* segments) {
+  m3::clear_error();
+  if (args == nullptr || segments == nullptr) {
+    return m3::fail(M3_EINVAL, "m3_scan_segments: NULL argument");
+  }
+  if (concurrent_calls < 1) {
+    return m3::fail(M3_EINVAL, "m3_scan_segments: concurrent_calls must be at least 1");
+  }
+  const int G = m3::segments_for(*args, concurrent_calls);
+  if (G < 0) {
+    return m3::fail(M3_EUNSUPPORTED, "m3_scan_segments: the requested %d segments cannot be met",
+                    args->segments);
+  }
+  *segments = G;
   return M3_OK;
 }
 

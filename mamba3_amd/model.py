@@ -148,11 +148,11 @@ class _Mamba3Mixer(nn.Module):
             side.wait_stream(main)
             with torch.cuda.stream(side):
                 mixed_r, _, _, _ = ops.scan_projection(proj, self, chunk_size=self._chunk(),
-                                                       reverse=True)
+                                                       reverse=True, concurrent=2)
             proj.record_stream(side)
         mixed, state, final_phase, final_k = ops.scan_projection(
             proj, self, cache=cache, want_cache=return_cache and self.causal,
-            chunk_size=self._chunk())
+            chunk_size=self._chunk(), concurrent=1 if self.causal else 2)
         output = self.out_proj(mixed.flatten(-2))
         if self.causal:
             if not return_cache:

@@ -386,10 +386,14 @@ class ScanCall:
     what scanning ``flip(proj)`` and flipping the result back gives (the reverse direction of
     a bidirectional layer, reference ``model.py:330-362``, without either flip or a second
     projection).
+
+    ``concurrent``: how many calls of this shape run at once (2 for the two directions of a
+    bidirectional layer). A long sequence of few (batch, head) pairs is split into segments
+    sized for the calls' combined grid, unless ``SCAN_SEGMENTS`` fixes the split.
     """
 
     def __init__(self, proj: torch.Tensor, mixer, *, cache=None, want_cache: bool = False,
-                 chunk_size: int = 256, reverse: bool = False):
+                 chunk_size: int = 256, reverse: bool = False, concurrent: int = 1):
         self.device = _require_device(proj)
         v = split_projection(proj, mixer)
         batch, length = proj.shape[0], proj.shape[1]
@@ -433,6 +437,10 @@ class ScanCall:
             for desc in (args.q, args.k, args.value, args.gate, args.dt, args.a, args.trap,
                          args.phase, args.out):
                 _backwards(desc, length)
+        if concurrent > 1 and args.segments == 0:
+            # `concurrent` calls of this shape share the GPU (the two directions of a
+            # bidirectional layer): the library's segment choice for their combined grid
+            args.segments = _hip.scan_segments(args, concurrent)
         with torch.cuda.device(dev):
             keep.append(_hip.scan_workspace(args, dev))
         self.args = args
@@ -447,15 +455,16 @@ class ScanCall:
 
 
 def scan_projection(proj: torch.Tensor, mixer, *, cache=None, want_cache: bool = False,
-                    chunk_size: int = 256, reverse: bool = False):
+                    chunk_size: int = 256, reverse: bool = False, concurrent: int = 1):
     """The whole mixer scan from the raw ``in_proj`` output ``[B, L, proj]``.
 
     Fuses the reference mixer's ``_project`` (B/C RMSNorm, dt, adt; ``model.py:165``),
     ``_phase``, bias, rotation and the chunked SSD (reference ``model.py:282-309``). Returns ``(mixed [B,L,H,P], state, final_phase,
-    final_k)``; the last two are ``None`` unless ``want_cache``. ``reverse``: see ``ScanCall``.
+    final_k)``; the last two are ``None`` unless ``want_cache``. ``reverse``, ``concurrent``: see
+    ``ScanCall``.
     """
     call = ScanCall(proj, mixer, cache=cache, want_cache=want_cache, chunk_size=chunk_size,
-                    reverse=reverse)
+                    reverse=reverse, concurrent=concurrent)
     call.launch()
     return call.out, call.final_state, call.final_phase, call.final_k
 

@@ -236,6 +236,30 @@ def test_scan_split_decision_on_the_host(lib):
     assert b"segments" in lib.m3_last_error()
 
 
+def test_scan_segment_choice_on_the_host(lib):
+    """The automatic split minimises the estimated rounds of workgroups over the 256 CUs: 24
+    (b, h) pairs over 65,536 tokens alone take 32 segments (768 workgroups, three full rounds),
+    two such calls together 16 each; 256 pairs fill the GPU unsplit; an explicit request is
+    checked, not replaced."""
+    g = ctypes.c_int(0)
+
+    def segs(batch, length, heads, segments=0, concurrent=1):
+        args = _hook_scan_args(batch, length, heads, segments)
+        assert lib.m3_scan_segments(ctypes.byref(args), concurrent, ctypes.byref(g)) == 0
+        return g.value
+
+    assert segs(1, 65536, 24) == 32
+    assert segs(1, 65536, 24, concurrent=2) == 16
+    assert segs(8, 4096, 32) == 1
+    assert segs(1, 4096, 4) == 8
+    assert segs(1, 512, 4) == 1
+    assert segs(1, 65536, 24, segments=8, concurrent=2) == 8
+    args = _hook_scan_args(1, 4096, 4, 3)
+    assert lib.m3_scan_segments(ctypes.byref(args), 1, ctypes.byref(g)) == 2
+    assert b"segments" in lib.m3_last_error()
+    assert lib.m3_scan_segments(ctypes.byref(args), 0, ctypes.byref(g)) == 1
+
+
 def test_scan_backwards_token_strides_on_the_host(lib):
     """Per-token tensors may run backwards (the reverse scan), but all of them together."""
     args = _hook_scan_args(1, 128, 2, 1)
