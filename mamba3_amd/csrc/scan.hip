@@ -297,14 +297,17 @@ __device__ __forceinline__ float dpp_shr(float x) {
                                                                CTRL, 0xf, 0xf, true));
 }
 
-// Inclusive scan within aligned segments of SEG lanes (SEG a power of 2, <= 16).
+// Inclusive scan within aligned segments of SEG lanes (SEG a power of 2, <= 16). For SEG = 16
+// the segment is the DPP row, whose shifts already read 0 before the row's first lane (the
+// same +0 the masks add), so no mask is applied.
 template <int SEG>
 __device__ __forceinline__ float seg_incl_scan(float x, int lane) {
   const int j = lane & (SEG - 1);
-  if constexpr (SEG > 1) { const float u = dpp_shr<0x111>(x); x += j >= 1 ? u : 0.f; }
-  if constexpr (SEG > 2) { const float u = dpp_shr<0x112>(x); x += j >= 2 ? u : 0.f; }
-  if constexpr (SEG > 4) { const float u = dpp_shr<0x114>(x); x += j >= 4 ? u : 0.f; }
-  if constexpr (SEG > 8) { const float u = dpp_shr<0x118>(x); x += j >= 8 ? u : 0.f; }
+  constexpr bool ROW = SEG == 16;
+  if constexpr (SEG > 1) { const float u = dpp_shr<0x111>(x); x += (ROW || j >= 1) ? u : 0.f; }
+  if constexpr (SEG > 2) { const float u = dpp_shr<0x112>(x); x += (ROW || j >= 2) ? u : 0.f; }
+  if constexpr (SEG > 4) { const float u = dpp_shr<0x114>(x); x += (ROW || j >= 4) ? u : 0.f; }
+  if constexpr (SEG > 8) { const float u = dpp_shr<0x118>(x); x += (ROW || j >= 8) ? u : 0.f; }
   return x;
 }
 
@@ -793,7 +796,12 @@ __device__ __forceinline__ void phase_stage(float* tab, int ps, float* pbase, fl
       // hardware's range), a difference far below the 16-bit rounding of the rotated values.
       const float raw = __fadd_rn(__fadd_rn(base, __fadd_rn(excl, cpre[i])), off);
       ph[i] = EXACT ? m3_fmod_2pi_small(raw) : raw;
-      if (last && t0 + TPL * pg + i == L - 1) *fph = EXACT ? ph[i] : m3_fmod_2pi_small(raw);
+    }
+    if (last) {  // one wave-uniform branch instead of a lane test per token
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        if (t0 + TPL * pg + i == L - 1) *fph = EXACT ? ph[i] : m3_fmod_2pi_small(ph[i]);
+      }
     }
     if (pg == PG - 1) {
       *pbase = __fadd_rn(base, incl);
