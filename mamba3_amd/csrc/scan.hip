@@ -390,17 +390,6 @@ __device__ __forceinline__ float bload_f32(__amdgpu_buffer_rsrc_t r, int off) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
-// One activation element from a buffer, as FP32.
-template <typename T>
-__device__ __forceinline__ float bload_elem(__amdgpu_buffer_rsrc_t r, int off) {
-  if constexpr (sizeof(T) == 4) {
-    return bload_f32(r, off);
-  } else {
-    const uint32_t bits = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-    return bits_to_f(bits, static_cast<T*>(nullptr));
-  }
-}
-
 // Four consecutive activation values stored as one vector (8 bytes for 16-bit types).
 template <typename T>
 __device__ __forceinline__ void bstore_quad(f4 x, __amdgpu_buffer_rsrc_t r, int off) {
@@ -411,16 +400,6 @@ __device__ __forceinline__ void bstore_quad(f4 x, __amdgpu_buffer_rsrc_t r, int 
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = from_f<T>(x[i]);
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, off, 0, 0);
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ void bstore_elem(float x, __amdgpu_buffer_rsrc_t r, int off) {
-  if constexpr (sizeof(T) == 4) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, off, 0, 0);
-  } else {
-    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f<T>(x)), r, off, 0,
-                                          0);
   }
 }
 

@@ -332,17 +332,6 @@ __device__ __forceinline__ f4 ld4(const void* base, int64_t i) {
   return r;
 }
 
-// Four consecutive elements of a tensor of any supported dtype (parameters: FP32 or 16-bit).
-__device__ __forceinline__ f4 ld4x(const m3_tensor& t, int64_t i) {
-  if (t.dtype == M3_F32) return ld4<float>(t.ptr, i);
-  if (t.dtype == M3_BF16) return ld4<__bf16>(t.ptr, i);
-  return ld4<_Float16>(t.ptr, i);
-}
-
-__device__ __forceinline__ float ldx_nb(const void* p, int dtype, int64_t i) {
-  return decode(ldraw(p, dtype, i), dtype);
-}
-
 template <typename T>
 __device__ __forceinline__ void st4(void* base, int64_t i, const float (&x)[4]) {
   if constexpr (sizeof(T) == 4) {
