@@ -2680,7 +2680,14 @@ __global__ __launch_bounds__(k16Threads) void scan16_kernel(const m3_scan_args a
         for (int i = 0; i < 4; ++i) {
           av[i] = b0[i];
           av[4 + i] = b1[i];
-          if (2 * m + 1 > it) bv[4 + i] = from_f<T>(0.f);  // column tile 2m + 1 lies above it
+        }
+        if (2 * m + 1 > it) {
+          // column tile 2m + 1 lies above it: the operand's upper half (two words) is zero
+          // (element-wise 16-bit zeroing took a select and a permute per element)
+          u32x4 bw = __builtin_bit_cast(u32x4, bv);
+          bw[2] = 0u;
+          bw[3] = 0u;
+          bv = __builtin_bit_cast(typename M::v8, bw);
         }
         yi = M::mma(av, bv, yi);
         __builtin_amdgcn_sched_barrier(0);
