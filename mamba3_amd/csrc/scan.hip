@@ -2801,25 +2801,29 @@ struct SegGeom {
   void* in_v;             // [B*G][H][P]
 };
 
-constexpr int kCompThreads = 256;
+constexpr int kCompThreads = 256;                         // state-row threads (and gather_kernel's)
+constexpr int kCompBlock = 64 + kCompThreads;             // compose_kernel: phase walker + state rows
 constexpr int kCompRows = 8;                              // state rows per workgroup
 constexpr int kCompPer = kCompRows * kNPad / kCompThreads;  // state elements per thread
-constexpr int kBlkChunk = 256;                          // phase blocks staged per round trip
+constexpr int kWalkBatch = 32;                          // block sums per walker load batch
 constexpr int kMaxSegments = 256;                       // bounds compose_kernel's LDS
 
-// Dynamic LDS of compose_kernel (floats): per segment the carry, its cos and sin [3][G][S], the
-// endpoint coefficient and decay [2][G], a chunk of block sums [kBlkChunk][S], the workgroup's
-// rows of one segment's local end state [kCompRows * N].
-static size_t compose_lds_bytes(int G, int S, int N) {
-  return sizeof(float) * (static_cast<size_t>(3) * G * S + 2 * G + kBlkChunk * S +
-                          static_cast<size_t>(kCompRows) * N);
+// Dynamic LDS of compose_kernel (floats): per segment the phase carry at its start [G][S], the
+// endpoint coefficient, e^{sum adt} and sum adt [3][G].
+static size_t compose_lds_bytes(int G, int S) {
+  return sizeof(float) * (static_cast<size_t>(G) * S + static_cast<size_t>(3) * G);
 }
 
 // One workgroup per (batch, head, group of kCompRows state rows): the rows are independent in the
 // composition (rotations pair columns within a row, the endpoint term is an outer product).
+// Wave 0 walks the phase carry through every 64-token block in order; the other four waves
+// update the state rows segment by segment behind it. Everything the state update reads except
+// the carry (the local end states, last k and last values of pass 1) is loaded segments ahead,
+// so the call's critical path is the walk itself. The waves meet through s_ready in LDS, never
+// at a barrier: the walker publishes each segment's carry and moves on.
 template <typename T, int R>
-__global__ __launch_bounds__(kCompThreads) void compose_kernel(const m3_scan_args a,
-                                                               const SegGeom sg) {
+__global__ __launch_bounds__(kCompBlock) void compose_kernel(const m3_scan_args a,
+                                                             const SegGeom sg) {
   const int H = a.heads, N = a.d_state, P = a.head_dim, S = a.num_angles, G = sg.G;
   const int nrg = (P + kCompRows - 1) / kCompRows;  // row groups per (b, h)
   const int bh = blockIdx.x / nrg, rg = blockIdx.x - bh * nrg;
@@ -2827,96 +2831,22 @@ __global__ __launch_bounds__(kCompThreads) void compose_kernel(const m3_scan_arg
   const int p0 = rg * kCompRows, np = min(kCompRows, P - p0);
   const int tid = threadIdx.x;
   const bool angles = a.phase_mode == M3_PHASE_ANGLES;
+  const bool walk = angles && S > 0;
   const bool mimo = a.mimo_rotation != 0;
   const bool raw_dt = a.raw_dt != 0;
   const bool lead = rg == 0;  // writes the per-(b, h) outputs: phases, k, decay
   extern __shared__ float dyn[];
-  float* s_phig = dyn;                       // [G][S] phase carry at each segment's start
-  float* s_csg = s_phig + G * S;             // [G][S] its cos
-  float* s_sng = s_csg + G * S;              // [G][S] its sin
-  float* s_c0g = s_sng + G * S;              // [G] endpoint coefficient dt (1 - trap)
-  float* s_decg = s_c0g + G;                 // [G] e^{sum adt}
-  float* s_blk = s_decg + G;                 // [kBlkChunk][S]
-  float* s_U = s_blk + kBlkChunk * S;        // [kCompRows * N]
-  __shared__ float s_kp[R * kNPad], s_vpm[R * kCompRows], s_vp[kCompRows];
-  T* in_k = static_cast<T*>(sg.in_k);
-  T* in_v = static_cast<T*>(sg.in_v);
-  const T* seg_k = static_cast<const T*>(sg.seg_k);
-  const int lgN = 31 - __builtin_clz(N);  // d_state is a power of 2: element e = (p << lgN) | n
-  const int RN = np << lgN;               // this workgroup's state elements
+  float* s_phig = dyn;             // [G][S] phase carry at each segment's start
+  float* s_c0g = s_phig + G * S;   // [G] endpoint coefficient dt (1 - trap)
+  float* s_decg = s_c0g + G;       // [G] e^{sum adt}
+  float* s_draw = s_decg + G;      // [G] sum adt
+  __shared__ int s_ready;          // segments whose starting carry is in s_phig
   auto row = [&](int g) { return (static_cast<int64_t>(b) * G + g) * H + h; };
 
-  // rotation partner of column n (-1: not rotated), whether n is the pair's first element, and
-  // the pair's angle: SISO pairs (2j, 2j+1), j < S; MIMO pairs (j, j + 2S), j < S
-  const int S2 = 2 * S;
-  auto partner = [&](int n, bool& lo, int& j) __attribute__((always_inline)) {
-    if (!mimo) {
-      lo = (n & 1) == 0;
-      j = n >> 1;
-      return (angles && n < S2) ? (n ^ 1) : -1;
-    }
-    lo = n < S2;
-    j = lo ? n : n - S2;
-    return (angles && j < S) ? (lo ? n + S2 : j) : -1;
-  };
-  auto rot = [&](float x, float xp, int part, bool lo, float c, float sn) {
-    if (part < 0) return x;
-    return lo ? x * c - xp * sn : xp * sn + x * c;
-  };
-
-  // ---- A: the phase carry, walked through every 64-token block in order (the kernel's own
-  // recurrence off <- fmod(off + block sum)), recording each segment's starting carry. All
-  // threads stage the block sums through LDS a chunk at a time; threads s < S walk.
-  if (angles) {
-    float off = 0.f;
-    if (tid < S && a.initial_phase.ptr != nullptr) {
-      off = static_cast<const float*>(a.initial_phase.ptr)
-          [b * a.initial_phase.stride[0] + h * a.initial_phase.stride[1] +
-           tid * a.initial_phase.stride[2]];
-    }
-    for (int g = 0; g < G; ++g) {
-      if (tid < S) s_phig[g * S + tid] = off;
-      if (g == G - 1) break;  // the last segment's blocks carry into nothing pass 2 needs
-      const float* blk = sg.seg_blk + row(g) * sg.nbs * S;
-      for (int k0 = 0; k0 < sg.nbs; k0 += kBlkChunk) {
-        const int nk = min(kBlkChunk, sg.nbs - k0);
-        __syncthreads();  // the walkers are done with the previous chunk
-        if ((S & 3) == 0) {  // whole float4s (16-byte aligned: the buffer rows are S floats)
-          for (int i = 4 * tid; i < nk * S; i += 4 * kCompThreads) {
-            *reinterpret_cast<float4*>(s_blk + i) =
-                *reinterpret_cast<const float4*>(blk + k0 * S + i);
-          }
-        } else {
-          for (int i = tid; i < nk * S; i += kCompThreads) s_blk[i] = blk[k0 * S + i];
-        }
-        __syncthreads();
-        if (tid < S) {
-          // the block sums do not depend on the carry: read 8 ahead of the fmod chain
-          int k = 0;
-          for (; k + 8 <= nk; k += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = s_blk[(k + u) * S + tid];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) off = m3_fmod_2pi_small(__fadd_rn(off, v[u]));
-          }
-          for (; k < nk; ++k) off = m3_fmod_2pi_small(__fadd_rn(off, s_blk[k * S + tid]));
-        }
-      }
-    }
-  }
-  __syncthreads();
-  // per segment, in parallel: cos / sin of the carry, the endpoint coefficient, the decay
-  for (int i = tid; i < G * S; i += kCompThreads) {
-    float sv, cv;
-    __sincosf(angles ? s_phig[i] : 0.f, &sv, &cv);
-    s_csg[i] = cv;
-    s_sng[i] = sv;
-  }
-  float decay_sum = 0.f;
+  // per segment, in parallel: the endpoint coefficient and the decay
   {
     const float dtb = raw_dt ? ldx(a.dt_bias.ptr, a.dt_bias.dtype, h * a.dt_bias.stride[0]) : 0.f;
-    for (int g = tid; g < G; g += kCompThreads) {
+    for (int g = tid; g < G; g += kCompBlock) {
       const int t0 = g * sg.Ls;
       float dt0, adt0;
       dt_adt(raw_dt, ldx(a.dt.ptr, a.dt.dtype,
@@ -2926,151 +2856,250 @@ __global__ __launch_bounds__(kCompThreads) void compose_kernel(const m3_scan_arg
       s_c0g[g] = dt0 * (1.f - sigmoidf(ldx(a.trap.ptr, a.trap.dtype,
                                            b * a.trap.stride[0] + t0 * a.trap.stride[1] +
                                                h * a.trap.stride[2])));
-      s_decg[g] = expf(sg.seg_decay[row(g)]);
-    }
-    if (lead && tid == 0) {
-      for (int g = 0; g < G; ++g) decay_sum += sg.seg_decay[row(g)];
+      const float l = sg.seg_decay[row(g)];
+      s_draw[g] = l;
+      s_decg[g] = expf(l);
     }
   }
+  if (tid == 0) s_ready = walk ? 0 : G;
+  __syncthreads();
 
-  // ---- B: this workgroup's state rows, segment by segment
-  float st[kCompPer];
+  if (tid < 64) {
+    // ---- wave 0: the phase carry, the kernel's own recurrence off <- fmod(off + block sum)
+    // over the blocks of segments 0 .. G-2 in order, published at each segment's start. Lanes
+    // s < S walk angle s; block sums are loaded a batch ahead of the fmod chain.
+    if (!walk || tid >= S) return;
+    float off = 0.f;
+    if (a.initial_phase.ptr != nullptr) {
+      off = static_cast<const float*>(a.initial_phase.ptr)
+          [b * a.initial_phase.stride[0] + h * a.initial_phase.stride[1] +
+           tid * a.initial_phase.stride[2]];
+    }
+    auto publish = [&](int g) __attribute__((always_inline)) {
+      s_phig[g * S + tid] = off;
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the carry is in LDS before the count
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      if (tid == 0) __hip_atomic_store(&s_ready, g + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    };
+    publish(0);
+    const int nbs = sg.nbs, gend = G - 1;
+    const int64_t seg_stride = static_cast<int64_t>(H) * nbs * S;  // floats from segment to segment
+    const float* blk = sg.seg_blk + row(0) * nbs * S + tid;
+    // batches never cross a segment's end; every load is issued (the last one repeated past a
+    // short batch's end) so the waits stay exact
+    auto load = [&](float (&buf)[kWalkBatch], int g, int k0) __attribute__((always_inline)) {
+      const int n = min(kWalkBatch, nbs - k0);
+      const float* p = blk + g * seg_stride + static_cast<int64_t>(k0) * S;
+#pragma unroll
+      for (int u = 0; u < kWalkBatch; ++u) buf[u] = p[min(u, n - 1) * S];
+    };
+    auto advance = [&](int& g, int& k0) __attribute__((always_inline)) {
+      k0 += kWalkBatch;
+      if (k0 >= nbs) {
+        k0 = 0;
+        ++g;
+      }
+    };
+    auto walk_batch = [&](const float (&buf)[kWalkBatch], int g, int k0)
+                          __attribute__((always_inline)) {
+      const int n = min(kWalkBatch, nbs - k0);
+#pragma unroll
+      for (int u = 0; u < kWalkBatch; ++u) {
+        if (u >= n) break;
+        off = m3_fmod_2pi_small(__fadd_rn(off, buf[u]));
+      }
+      if (k0 + n == nbs) publish(g + 1);  // segment g walked: the carry at segment g + 1's start
+    };
+    if (gend > 0) {
+      float bufA[kWalkBatch], bufB[kWalkBatch];
+      int gA = 0, kA = 0;
+      load(bufA, gA, kA);
+      for (;;) {
+        int gB = gA, kB = kA;
+        advance(gB, kB);
+        const bool moreB = gB < gend;
+        load(bufB, moreB ? gB : gA, moreB ? kB : kA);
+        walk_batch(bufA, gA, kA);
+        if (!moreB) break;
+        int gC = gB, kC = kB;
+        advance(gC, kC);
+        const bool moreC = gC < gend;
+        load(bufA, moreC ? gC : gB, moreC ? kC : kB);
+        walk_batch(bufB, gB, kB);
+        if (!moreC) break;
+        gA = gC;
+        kA = kC;
+      }
+    }
+    return;
+  }
+
+  // ---- waves 1-4: this workgroup's state rows, segment by segment
+  const int tb = tid - 64;
+  const int lgN = 31 - __builtin_clz(N);  // d_state is a power of 2 dividing kCompThreads
+  const int RN = np << lgN;               // this workgroup's state elements
+  const int n = tb & (N - 1);             // the thread's column: element e = tb + kCompThreads i
+  // rotation partner of column n (-1: not rotated), whether n is the pair's first element, and
+  // the pair's angle: SISO pairs (2j, 2j+1), j < S; MIMO pairs (j, j + 2S), j < S
+  const int S2 = 2 * S;
+  bool lo;
+  int j;
+  int part;
+  if (!mimo) {
+    lo = (n & 1) == 0;
+    j = n >> 1;
+    part = (angles && n < S2) ? (n ^ 1) : -1;
+  } else {
+    lo = n < S2;
+    j = lo ? n : n - S2;
+    part = (angles && j < S) ? (lo ? n + S2 : j) : -1;
+  }
+  const int np_n = part >= 0 ? part : n;
+  auto rot = [&](float x, float xp, float c, float sn) {
+    return lo ? x * c - xp * sn : xp * sn + x * c;
+  };
+  T* in_k = static_cast<T*>(sg.in_k);
+  T* in_v = static_cast<T*>(sg.in_v);
+  const T* seg_k = static_cast<const T*>(sg.seg_k);
+  const T* value = static_cast<const T*>(a.value.ptr);
+  int pl[kCompPer];
+#pragma unroll
+  for (int i = 0; i < kCompPer; ++i) pl[i] = min(tb + kCompThreads * i, RN - 1) >> lgN;
+
+  // the start: the caller's state, k and value (zero without them)
+  float st[kCompPer], vp[kCompPer], kp[R], mxr[R][kCompPer];
 #pragma unroll
   for (int i = 0; i < kCompPer; ++i) {
-    const int e = tid + kCompThreads * i, p = p0 + (e >> lgN), n = e & (N - 1);
+    const int e = tb + kCompThreads * i;
     st[i] = (e < RN && a.initial_state.ptr != nullptr)
                 ? static_cast<const float*>(a.initial_state.ptr)
                       [b * a.initial_state.stride[0] + h * a.initial_state.stride[1] +
-                       p * a.initial_state.stride[2] + n]
+                       (p0 + pl[i]) * a.initial_state.stride[2] + n]
+                : 0.f;
+    vp[i] = a.initial_k.ptr != nullptr
+                ? to_f(static_cast<const T*>(a.initial_value.ptr)
+                           [b * a.initial_value.stride[0] + h * a.initial_value.stride[1] +
+                            p0 + pl[i]])
+                : 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      mxr[r][i] = R > 1 ? rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
+                                     h * a.mimo_x.stride[0] + r * a.mimo_x.stride[1] + p0 + pl[i]))
+                        : 1.f;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    kp[r] = a.initial_k.ptr != nullptr
+                ? to_f(static_cast<const T*>(a.initial_k.ptr)
+                           [b * a.initial_k.stride[0] + h * a.initial_k.stride[1] +
+                            r * a.initial_k.stride[2] + n])
                 : 0.f;
   }
-  for (int i = tid; i < R * N; i += kCompThreads) {
-    const int r = i >> lgN, n = i & (N - 1);
-    s_kp[i] = a.initial_k.ptr != nullptr
-                  ? to_f(static_cast<const T*>(a.initial_k.ptr)
-                             [b * a.initial_k.stride[0] + h * a.initial_k.stride[1] +
-                              r * a.initial_k.stride[2] + n])
-                  : 0.f;
-  }
-  if (tid < np) {
-    s_vp[tid] = a.initial_k.ptr != nullptr
-                    ? to_f(static_cast<const T*>(a.initial_value.ptr)
-                               [b * a.initial_value.stride[0] + h * a.initial_value.stride[1] +
-                                p0 + tid])
-                    : 0.f;
-  }
-  // registers of segment g's local end state (this workgroup's rows), last k and the value of
-  // its last token, loaded one segment ahead
-  constexpr int KQ = (R * kNPad + kCompThreads - 1) / kCompThreads;
-  float un[kCompPer], kx[KQ], kxp[KQ], vlast = 0.f;
-  auto prefetch = [&](int g) __attribute__((always_inline)) {
-    const int64_t sh = row(g);
+
+  // a ring of D segments' inputs: local end state (the element and its rotation partner), last
+  // k (column n and its partner, every rank) and the value of the last token (the thread's rows)
+  constexpr int D = R <= 4 ? 4 : 2;
+  float ru[D][kCompPer], rup[D][kCompPer], rk[D][R], rkp[D][R], rv[D][kCompPer];
+  auto fetch = [&](int d, int g) __attribute__((always_inline)) {
+    const int gc = min(g, G - 1);  // past the end: a repeat of the last segment, unused
+    const int64_t sh = row(gc);
     const float* U = sg.seg_state + (sh * P + p0) * N;
 #pragma unroll
     for (int i = 0; i < kCompPer; ++i) {
-      const int e = tid + kCompThreads * i;
-      un[i] = e < RN ? U[e] : 0.f;
+      ru[d][i] = U[(pl[i] << lgN) + n];
+      rup[d][i] = U[(pl[i] << lgN) + np_n];
     }
 #pragma unroll
-    for (int q = 0; q < KQ; ++q) {
-      const int i = min(tid + kCompThreads * q, R * N - 1);
-      const int r = i >> lgN, n = i & (N - 1);
-      bool lo;
-      int j;
-      const int part = partner(n, lo, j);
-      kx[q] = to_f(seg_k[sh * R * N + i]);
-      kxp[q] = to_f(seg_k[sh * R * N + r * N + (part >= 0 ? part : n)]);
+    for (int r = 0; r < R; ++r) {
+      rk[d][r] = to_f(seg_k[sh * R * N + r * N + n]);
+      rkp[d][r] = to_f(seg_k[sh * R * N + r * N + np_n]);
     }
-    const int tl = g * sg.Ls + sg.Ls - 1;
-    vlast = to_f(static_cast<const T*>(a.value.ptr)[b * a.value.stride[0] +
-                                                    tl * a.value.stride[1] +
-                                                    h * a.value.stride[2] + p0 +
-                                                    min(tid, np - 1)]);
-  };
-  prefetch(0);
-  __syncthreads();
-
-  for (int g = 0; g < G; ++g) {
-    const int64_t sh = row(g);
-    const float* csg = s_csg + g * S;
-    const float* sng = s_sng + g * S;
-    // (1) segment g's start for pass 2; its local state rows to LDS; the rank values of v_prev
+    const int tl = gc * sg.Ls + sg.Ls - 1;
 #pragma unroll
     for (int i = 0; i < kCompPer; ++i) {
-      const int e = tid + kCompThreads * i;
-      if (e < RN) {
-        sg.in_state[(sh * P + p0) * N + e] = st[i];
-        s_U[e] = un[i];
-      }
+      rv[d][i] = to_f(value[b * a.value.stride[0] + tl * a.value.stride[1] +
+                            h * a.value.stride[2] + p0 + pl[i]]);
     }
-    if (lead) {
-      if (angles) {
-        for (int i = tid; i < S; i += kCompThreads) sg.in_phase[sh * S + i] = s_phig[g * S + i];
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) fetch(d, d);
+
+  for (int g0 = 0; g0 < G; g0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int g = g0 + d;
+      if (g >= G) break;
+      const int64_t sh = row(g);
+      float u[kCompPer], up[kCompPer], kx[R], kxp[R], vl[kCompPer];
+#pragma unroll
+      for (int i = 0; i < kCompPer; ++i) {
+        u[i] = ru[d][i];
+        up[i] = rup[d][i];
+        vl[i] = rv[d][i];
       }
-      for (int i = tid; i < R * N; i += kCompThreads) in_k[sh * R * N + i] = from_f<T>(s_kp[i]);
-    }
-    if (tid < np) {
-      in_v[sh * P + p0 + tid] = from_f<T>(s_vp[tid]);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        s_vpm[r * kCompRows + tid] =
-            R > 1 ? mul_r<T>(s_vp[tid], rnd<T>(ldx(a.mimo_x.ptr, a.mimo_x.dtype,
-                                                   h * a.mimo_x.stride[0] +
-                                                       r * a.mimo_x.stride[1] + p0 + tid)))
-                  : s_vp[tid];
+        kx[r] = rk[d][r];
+        kxp[r] = rkp[d][r];
       }
-    }
-    float kx_c[KQ], kxp_c[KQ];
-#pragma unroll
-    for (int q = 0; q < KQ; ++q) {
-      kx_c[q] = kx[q];
-      kxp_c[q] = kxp[q];
-    }
-    const float nv = vlast;
-    __syncthreads();
-    if (g + 1 < G) prefetch(g + 1);
+      fetch(d, g + D);
 
-    // (2) the state at the segment's end: e^l (S + c0 sum_r (v_prev mx_r) k_prev_r^T) + Rot U
-    const float c0 = s_c0g[g], dec = s_decg[g];
+      // (1) segment g's start for pass 2
 #pragma unroll
-    for (int i = 0; i < kCompPer; ++i) {
-      const int e = tid + kCompThreads * i;
-      if (e >= RN) continue;
-      const int pl = e >> lgN, n = e & (N - 1);
-      float endpoint = 0.f;
+      for (int i = 0; i < kCompPer; ++i) {
+        const int e = tb + kCompThreads * i;
+        if (e < RN) sg.in_state[(sh * P + p0) * N + e] = st[i];
+      }
+      if (lead && tb < N) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) endpoint += s_vpm[r * kCompRows + pl] * s_kp[(r << lgN) + n];
-      bool lo;
-      int j;
-      const int part = partner(n, lo, j);
-      const float u = part >= 0 ? rot(s_U[e], s_U[(pl << lgN) + part], part, lo, csg[j], sng[j])
-                                : s_U[e];
-      st[i] = dec * (st[i] + c0 * endpoint) + u;
+        for (int r = 0; r < R; ++r) in_k[sh * R * N + r * N + n] = from_f<T>(kp[r]);
+      }
+      if (n == 0) {
+#pragma unroll
+        for (int i = 0; i < kCompPer; ++i) {
+          if (tb + kCompThreads * i < RN) in_v[sh * P + p0 + pl[i]] = from_f<T>(vp[i]);
+        }
+      }
+      // the carry at segment g's start, once the walker has published it
+      float cs = 1.f, sn = 0.f;
+      if (walk) {
+        for (int spin = 0;
+             __hip_atomic_load(&s_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <= g &&
+             spin < (1 << 24);
+             ++spin) {
+          __builtin_amdgcn_s_sleep(2);
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (part >= 0) __sincosf(s_phig[g * S + j], &sn, &cs);
+        if (lead && tb < S) sg.in_phase[sh * S + tb] = s_phig[g * S + tb];
+      }
+
+      // (2) the state at the segment's end: e^l (S + c0 sum_r (v_prev mx_r) k_prev_r^T) + Rot U
+      const float c0 = s_c0g[g], dec = s_decg[g];
+#pragma unroll
+      for (int i = 0; i < kCompPer; ++i) {
+        if (tb + kCompThreads * i >= RN) continue;
+        float endpoint = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) endpoint += (R > 1 ? mul_r<T>(vp[i], mxr[r][i]) : vp[i]) * kp[r];
+        const float uu = part >= 0 ? rot(u[i], up[i], cs, sn) : u[i];
+        st[i] = dec * (st[i] + c0 * endpoint) + uu;
+      }
+      // (3) the next segment's endpoint: this segment's last k, rotated by its carry, and value
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        kp[r] = part >= 0 ? rnd<T>(rot(kx[r], kxp[r], cs, sn)) : rnd<T>(kx[r]);
+      }
+#pragma unroll
+      for (int i = 0; i < kCompPer; ++i) vp[i] = vl[i];
     }
-    // (3) the next segment's endpoint: this segment's last k, rotated by its carry, and value
-    float nk[KQ];
-#pragma unroll
-    for (int q = 0; q < KQ; ++q) {
-      const int i = tid + kCompThreads * q;
-      const int n = i & (N - 1);
-      bool lo;
-      int j;
-      const int part = i < R * N ? partner(n, lo, j) : -1;
-      nk[q] = part >= 0 ? rnd<T>(rot(kx_c[q], kxp_c[q], part, lo, csg[j], sng[j]))
-                        : rnd<T>(kx_c[q]);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < KQ; ++q) {
-      const int i = tid + kCompThreads * q;
-      if (i < R * N) s_kp[i] = nk[q];
-    }
-    if (tid < np) s_vp[tid] = nv;
-    __syncthreads();
   }
 
   // the call's decay (its final state, phase and k come from pass 2: gather_kernel)
-  if (lead && a.final_decay.ptr != nullptr && tid == 0) {
+  if (lead && tb == 0 && a.final_decay.ptr != nullptr) {
+    float decay_sum = 0.f;
+    for (int g = 0; g < G; ++g) decay_sum += s_draw[g];
     static_cast<float*>(a.final_decay.ptr)[b * a.final_decay.stride[0] +
                                            h * a.final_decay.stride[1]] = decay_sum;
   }
@@ -3594,22 +3623,14 @@ static int launch_segmented(const m3_scan_args& a, int G, hipStream_t stream) {
   int rc = launch_pass<T, R>(a1, stream, true, /*state_only=*/true);
   if (rc != M3_OK) return rc;
 
-  const size_t clds = compose_lds_bytes(G, S, N);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&compose_kernel<T, R>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(compose_lds_bytes(kMaxSegments, kSMax,
-                                                                          kNPad)));
-    if (e != hipSuccess) {
-      return fail(M3_ELAUNCH, "m3_scan_fwd: hipFuncSetAttribute: %s", hipGetErrorString(e));
-    }
-    attr_set = true;
-  }
+  // at most kMaxSegments x kSMax + 3 kMaxSegments floats: within the default 64 KiB
+  const size_t clds = compose_lds_bytes(G, S);
+  static_assert(sizeof(float) * (kMaxSegments * kSMax + 3 * kMaxSegments) <= 65536,
+                "compose_kernel's LDS fits the default limit");
   const unsigned row_groups = static_cast<unsigned>((P + kCompRows - 1) / kCompRows);
   hipLaunchKernelGGL((compose_kernel<T, R>),
                      dim3(static_cast<unsigned>(a.batch) * a.heads * row_groups),
-                     dim3(kCompThreads), clds, stream, a, sg);
+                     dim3(kCompBlock), clds, stream, a, sg);
   rc = check_launch("m3_scan_fwd (compose)");
   if (rc != M3_OK) return rc;
 
