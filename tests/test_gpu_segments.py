@@ -61,6 +61,26 @@ def test_fp32_split_matches_unsplit_and_oracle(rank, phase, initial, segs, segme
     torch.testing.assert_close(s2, s_ref, **F32)
 
 
+@pytest.mark.parametrize("rank,segs,length,head_dim,d_state", [
+    (1, 32, 4096, 64, 128),  # 32 segments: the prefetch ring wraps eight times
+    (2, 2, 8192, 36, 64),    # a 4-row last row group, d_state 64
+    (8, 4, 4096, 64, 128),   # rank 8: the composition's shallower prefetch ring
+])
+def test_fp32_split_composition_shapes(rank, segs, length, head_dim, d_state, segments):
+    """The composition's state rows at the segment counts, row groups and ranks the tests above
+    leave out: split against unsplit, FP32, with given phases (no carry to walk) and an initial
+    state."""
+    inp = _inputs(rank, torch.float32, batch=1, length=length, heads=2, head_dim=head_dim,
+                  d_state=d_state, seed=80 + rank, phase=True, initial=True)
+    chunk = 32 // rank
+    segments(1)
+    y1, s1 = _scan(inp, chunk)
+    segments(segs)
+    y2, s2 = _scan(inp, chunk)
+    torch.testing.assert_close(y2, y1, **F32)
+    torch.testing.assert_close(s2, s1, **F32)
+
+
 @pytest.mark.parametrize("rank", [1, 4])
 def test_bf16_split_matches_unsplit(rank, segments):
     inp = _inputs(rank, torch.bfloat16, batch=1, length=2048, heads=3, seed=50 + rank)
@@ -133,6 +153,33 @@ def test_model_auto_split_matches_oracle(rank, bf16, segments):
         torch.testing.assert_close(got.cpu(), want, **F32)
         for g, w in zip(cache[0], want_cache[0]):
             torch.testing.assert_close(g.cpu().float(), w.float(), **F32)
+
+
+@pytest.mark.parametrize("d_model,d_state,rank,segs,length", [
+    (128, 128, 1, 32, 4096),  # 31 segments of 2 phase blocks: one short walker batch each
+    (18, 64, 2, 2, 8192),     # 64 blocks per segment (two walker batches); 4-row heads
+    (64, 128, 8, 4, 4096),    # rank 8
+])
+def test_model_split_walks_the_phase_carry(d_model, d_state, rank, segs, length, segments):
+    """The model's projection form (angle increments: the composition walks the phase carry
+    block by block) split into segments equals the unsplit prefill, FP32: output and every
+    cache tensor, the phase cache bit for bit."""
+    torch.manual_seed(90 + rank)
+    model = Mamba3(d_model, d_state=d_state, depth=1, mimo_rank=rank).eval().to(DEV)
+    x = torch.randn(1, length, d_model, device=DEV)
+    with torch.inference_mode():
+        segments(1)
+        want, want_cache = model.prefill(x)
+        segments(segs)
+        got, cache = model.prefill(x)
+    torch.testing.assert_close(got, want, **F32)
+    mixer = model.layers[0].mixer
+    phase_shape = (1, mixer.nheads, mixer.num_angles)
+    for g, w in zip(cache[0], want_cache[0]):
+        if tuple(w.shape) == phase_shape:
+            assert torch.equal(g, w), "the split's phase carry differs from the unsplit scan's"
+        else:
+            torch.testing.assert_close(g, w, **F32)
 
 
 def test_split_scan_continues_from_a_cache(segments):
