@@ -175,11 +175,14 @@ def test_model_split_walks_the_phase_carry(d_model, d_state, rank, segs, length,
     torch.testing.assert_close(got, want, **F32)
     mixer = model.layers[0].mixer
     phase_shape = (1, mixer.nheads, mixer.num_angles)
+    phases = 0
     for g, w in zip(cache[0], want_cache[0]):
         if tuple(w.shape) == phase_shape:
             assert torch.equal(g, w), "the split's phase carry differs from the unsplit scan's"
+            phases += 1
         else:
             torch.testing.assert_close(g, w, **F32)
+    assert phases == 1
 
 
 def test_split_scan_continues_from_a_cache(segments):
