@@ -3112,12 +3112,28 @@ __global__ __launch_bounds__(kCompThreads) void gather_kernel(const m3_scan_args
   const int H = a.heads, N = a.d_state, P = a.head_dim, S = a.num_angles;
   const int b = blockIdx.x / H, h = blockIdx.x - b * H;
   const int64_t sh = (static_cast<int64_t>(b) * sg.G + sg.G - 1) * H + h;
-  for (int e = threadIdx.x; e < P * N; e += kCompThreads) {
-    const int p = e / N, n = e - p * N;
-    static_cast<float*>(a.final_state.ptr)[b * a.final_state.stride[0] +
-                                           h * a.final_state.stride[1] +
-                                           p * a.final_state.stride[2] + n] =
-        sg.seg_state[sh * P * N + e];
+  // the state: every element loaded before any is stored (the compiler cannot tell the two
+  // buffers apart, so a load-store loop would take one round trip per element per thread)
+  {
+    constexpr int kPer = kPPad * kNPad / kCompThreads;
+    const int lgN = 31 - __builtin_clz(N), PN = P * N;
+    const float* src = sg.seg_state + sh * PN;
+    float v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int e = threadIdx.x + kCompThreads * u;
+      v[u] = e < PN ? src[e] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int e = threadIdx.x + kCompThreads * u;
+      if (e < PN) {
+        static_cast<float*>(a.final_state.ptr)[b * a.final_state.stride[0] +
+                                               h * a.final_state.stride[1] +
+                                               (e >> lgN) * a.final_state.stride[2] +
+                                               (e & (N - 1))] = v[u];
+      }
+    }
   }
   if (a.final_phase.ptr != nullptr) {
     for (int i = threadIdx.x; i < S; i += kCompThreads) {
@@ -3138,14 +3154,31 @@ __global__ __launch_bounds__(kCompThreads) void gather_kernel(const m3_scan_args
   // of the sequence, and its increment sum does not depend on the carry: pass 1's sums are the
   // call's.
   if (a.block_phase.ptr != nullptr) {
+    // 16 elements per thread loaded, then stored (as the state above)
+    constexpr int kPer = 16;
     const int nb = sg.G * sg.nbs;
-    for (int e = threadIdx.x; e < nb * S; e += kCompThreads) {
-      const int blk = e / S, i = e - blk * S, g = blk / sg.nbs, j = blk - g * sg.nbs;
-      const int64_t src = ((static_cast<int64_t>(b) * sg.G + g) * H + h) * sg.nbs + j;
-      static_cast<float*>(a.block_phase.ptr)[b * a.block_phase.stride[0] +
-                                             h * a.block_phase.stride[1] +
-                                             blk * a.block_phase.stride[2] +
-                                             i * a.block_phase.stride[3]] = sg.seg_blk[src * S + i];
+    for (int e0 = threadIdx.x; e0 < nb * S; e0 += kPer * kCompThreads) {
+      float v[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int e = e0 + kCompThreads * u;
+        if (e < nb * S) {
+          const int blk = e / S, i = e - blk * S, g = blk / sg.nbs, j = blk - g * sg.nbs;
+          const int64_t src = ((static_cast<int64_t>(b) * sg.G + g) * H + h) * sg.nbs + j;
+          v[u] = sg.seg_blk[src * S + i];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int e = e0 + kCompThreads * u;
+        if (e < nb * S) {
+          const int blk = e / S, i = e - blk * S;
+          static_cast<float*>(a.block_phase.ptr)[b * a.block_phase.stride[0] +
+                                                 h * a.block_phase.stride[1] +
+                                                 blk * a.block_phase.stride[2] +
+                                                 i * a.block_phase.stride[3]] = v[u];
+        }
+      }
     }
   }
 }
