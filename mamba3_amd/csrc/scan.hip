@@ -3061,7 +3061,11 @@ __global__ __launch_bounds__(kCompBlock) void compose_kernel(const m3_scan_args 
           if (tb + kCompThreads * i < RN) in_v[sh * P + p0 + pl[i]] = from_f<T>(vp[i]);
         }
       }
-      // the carry at segment g's start, once the walker has published it
+      // the carry at segment g's start, once the walker has published it. The walker is a wave
+      // of this workgroup (resident with it) and publishes every segment without waiting on
+      // anything, so the wait always ends; the spin cap (seconds) only keeps a defect from
+      // becoming a hang. LDS operations of one wave complete in order and the walker drains its
+      // carry stores before the count, so a count above g means the carry is readable.
       float cs = 1.f, sn = 0.f;
       if (walk) {
         for (int spin = 0;
