@@ -159,6 +159,8 @@ def test_model_auto_split_matches_oracle(rank, bf16, segments):
     (128, 128, 1, 32, 4096),  # 31 segments of 2 phase blocks: one short walker batch each
     (18, 64, 2, 2, 8192),     # 64 blocks per segment (two walker batches); 4-row heads
     (64, 128, 8, 4, 4096),    # rank 8
+    (32, 128, 1, 256, 16384), # the most segments, one phase block each
+    (64, 64, 4, 3, 1536),     # a segment count that is no power of 2; rank 4, d_state 64
 ])
 def test_model_split_walks_the_phase_carry(d_model, d_state, rank, segs, length, segments):
     """The model's projection form (angle increments: the composition walks the phase carry
